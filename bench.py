@@ -1,0 +1,292 @@
+"""Benchmark: one PLM round of dense linears on one MI355X.
+
+A step is one full 1.3B-shape round at k=7 (M = 56 rows): 24 GPT-style blocks (QKV 2048->6144,
+attention-out 2048->2048, MLP up 2048->8192, MLP down 8192->2048) plus the LM head 2048->50257,
+i.e. 97 GEMM launches through ``fast_gemm``'s kernel, chained output-to-input as in the model, with
+random-init bf16 weights (~N(0, 0.02^2)) resident in HBM. The round is recorded once as a HIP
+graph and replayed (the reference replays its round as a CUDA graph, plm/decoder.py:414-447).
+
+Prints one JSON line: ``value`` is microseconds per round (lower is better), plus the round's HBM
+GB/s and fraction of the 8 TB/s peak, the dominant kernel's roofline from HIP-event timing, the
+partial-round M sweep, the fused LM-head verify step, and the torch-CPU baseline of the same
+linears timed on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "plm-anon_amd"))
+
+METRIC = "µs/round of linears + HBM GB/s (% of peak) at M=56, 1.3B-shape bf16"
+HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--hidden", type=int, default=2048)
+    ap.add_argument("--mlp", type=int, default=8192)
+    ap.add_argument("--layers", type=int, default=24)
+    ap.add_argument("--M", type=int, default=56)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget (0 disables it)")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the partial-round M sweep")
+    ap.add_argument("--no-verify", action="store_true", help="skip the fused LM-head verify timing")
+    ap.add_argument("--only-round", action="store_true", help="time the round only (for profiling runs)")
+    return ap.parse_args()
+
+
+class Round:
+    """The round's weights, activation chain and captured graph at one width M."""
+
+    def __init__(self, M, hidden, mlp, layers, weights, tables, device):
+        import torch
+
+        from plm_amd.workloads import GPT2_VOCAB, gpt_block
+
+        self.M = M
+        self.gemms = [g for _ in range(layers) for g in gpt_block(hidden, mlp)]
+        self.gemms.append(type(self.gemms[0])("lm_head", GPT2_VOCAB, hidden))
+        self.weights = weights
+        self.cfgs = [tables[(M, g.N, g.K)] for g in self.gemms]
+        g = torch.Generator(device=device).manual_seed(3000 + M)
+        self.x0 = torch.randn(M, hidden, generator=g, device=device).bfloat16()
+        self.outs = [torch.empty(M, gm.N, device=device, dtype=torch.bfloat16) for gm in self.gemms]
+        self.inputs = []
+        x = self.x0
+        for gm, out in zip(self.gemms, self.outs):
+            self.inputs.append(x if x.shape[1] == gm.K else x[:, :gm.K])
+            x = out
+        self.graph = None
+
+    def launch(self, indices=None):
+        from plm_amd.fast_gemm import hip_linear
+
+        for i in (range(len(self.gemms)) if indices is None else indices):
+            hip_linear(self.inputs[i], self.weights[i], self.cfgs[i], self.outs[i])
+
+    def capture(self, indices=None):
+        import torch
+
+        self.launch(indices)                          # eager pass: sizes the split-K workspace
+        torch.cuda.synchronize()
+        stream = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            self.launch(indices)
+        return graph
+
+    @property
+    def bytes(self):
+        return sum(g.bytes(self.M) for g in self.gemms)
+
+
+def time_graph(graph, steps, warmup):
+    """Milliseconds per replay: warm-up replays, then `steps` replays bracketed by HIP events."""
+    import torch
+
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def kernel_class(M, K, cfg):
+    """The compiled kernel a GEMM launches: (MT, wave_frags, unroll, pipelined, k_waves)."""
+    steps = math.ceil(K / 32)
+    spw = math.ceil(steps / (cfg["split_k"] * cfg["k_waves"]))
+    return (math.ceil(M / 16), cfg["wave_frags"], cfg["unroll"], spw > cfg["unroll"], cfg["k_waves"])
+
+
+def kernel_name(cls):
+    mt, nf, u, pipe, kw = cls
+    return f"skinny_gemm_kernel<bf16, MT={mt}, NF={nf}, U={u}, PIPE={int(pipe)}, KW={kw}>"
+
+
+def dominant_kernel_roofline(rnd, steps):
+    """Per kernel class: graph of that class's launches only (in round order), HIP-event timed."""
+    classes = {}
+    for i, (g, cfg) in enumerate(zip(rnd.gemms, rnd.cfgs)):
+        classes.setdefault(kernel_class(rnd.M, g.K, cfg), []).append(i)
+    rows = []
+    for cls, idx in classes.items():
+        graph = rnd.capture(idx)
+        ms = time_graph(graph, max(5, steps // 2), 2)
+        per_launch_us = ms * 1000.0 / len(idx)
+        nbytes = sum(rnd.gemms[i].bytes(rnd.M) for i in idx) / len(idx)
+        flops = sum(rnd.gemms[i].flops(rnd.M) for i in idx) / len(idx)
+        rows.append({"kernel": kernel_name(cls), "launches": len(idx), "us_per_launch": per_launch_us,
+                     "bytes_per_launch": nbytes, "flops_per_launch": flops, "total_us": per_launch_us * len(idx)})
+        del graph
+    rows.sort(key=lambda r: -r["total_us"])
+    return rows
+
+
+def traffic_for(kernel: str):
+    """HBM bytes per launch measured with rocprofv3 counters, if a committed summary holds them."""
+    path = REPO / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    try:
+        return json.loads(path.read_text()).get(kernel)
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(hidden, mlp, M, budget_s):
+    """torch-CPU F.linear (the reference's --mode default op) over one block and the LM head, timed
+    on this host; the full round is 24 blocks + LM head, scaled from the per-GEMM medians."""
+    import torch
+
+    import oracle
+    from plm_amd.workloads import GPT2_VOCAB, gpt_block, normal
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    gemms = gpt_block(hidden, mlp) + [type(gpt_block(hidden, mlp)[0])("lm_head", GPT2_VOCAB, hidden)]
+    xs = {g.K: normal((M, g.K), 7000 + g.K) for g in gemms}
+    ws = [normal((g.N, g.K), 7100 + i, 0.02) for i, g in enumerate(gemms)]
+    medians = []
+    deadline = time.perf_counter() + budget_s
+    for g, w in zip(gemms, ws):
+        oracle.linear(xs[g.K], w)                     # warm-up
+        times = []
+        while len(times) < 5 or (time.perf_counter() < deadline and len(times) < 50):
+            t0 = time.perf_counter()
+            oracle.linear(xs[g.K], w)
+            times.append(time.perf_counter() - t0)
+            if len(times) >= 5 and time.perf_counter() > deadline:
+                break
+        medians.append(sorted(times)[len(times) // 2])
+    block_s = sum(medians[:4])
+    round_s = 24 * block_s + medians[4]
+    cpu_model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round_s * 1e6, "unit": "us/round", "cores": threads, "kind": "port",
+            "sample": f"torch CPU F.linear bf16, median of >=5 reps per GEMM of one {hidden}/{mlp} block and the "
+                      f"LM head at M={M}; round = 24 x block + LM head; CPU {cpu_model}"}
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build runs the round's linears on a single MI355X); "
+              f"got --gpus {args.gpus}", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from plm_amd import gemm_tables
+    from plm_amd.fast_gemm import hip_linear  # noqa: F401  (fails loudly if the library is missing)
+    from plm_amd.workloads import GPT2_VOCAB, gpt_block
+
+    torch.cuda.set_device(0)
+    device = torch.device("cuda", 0)
+    tables = gemm_tables.read_table(args.hidden)
+    gemms = [g for _ in range(args.layers) for g in gpt_block(args.hidden, args.mlp)]
+    gemms.append(type(gemms[0])("lm_head", GPT2_VOCAB, args.hidden))
+    gen = torch.Generator(device=device)
+    weights = []
+    for i, g in enumerate(gemms):
+        gen.manual_seed(1 + 1000 * 3 + i)
+        weights.append((0.02 * torch.randn(g.N, g.K, generator=gen, device=device)).bfloat16())
+    print(f"[bench] weights resident: {sum(w.numel() * 2 for w in weights) / 1e9:.2f} GB", file=sys.stderr,
+          flush=True)
+
+    rnd = Round(args.M, args.hidden, args.mlp, args.layers, weights, tables, device)
+    graph = rnd.capture()
+    ms = time_graph(graph, args.steps, args.warmup)
+    us_round = ms * 1000.0
+    gbps = rnd.bytes / (us_round * 1e-6) / 1e9
+    print(f"[bench] round: {us_round:.1f} us, {gbps:.0f} GB/s", file=sys.stderr, flush=True)
+    result = {
+        "metric": METRIC, "value": round(us_round, 2), "unit": "us/round", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (random-init weights ~N(0,0.02^2), seeded)",
+        "config": {"workload": f"{'1.3B' if args.hidden == 2048 else str(args.hidden)}-shape round of linears: "
+                               f"{args.layers} GPT-style blocks + LM head, M={args.M} (k=7)",
+                   "M": args.M, "hidden": args.hidden, "mlp": args.mlp, "layers": args.layers,
+                   "vocab": GPT2_VOCAB, "gemm_launches": len(gemms), "bytes_per_round": rnd.bytes,
+                   "timing": "HIP graph replay of the whole round, HIP events"},
+        "gbps": round(gbps, 1), "pct_of_hbm_peak": round(100.0 * gbps / HBM_PEAK_GBPS, 2),
+    }
+    del graph
+    if not args.only_round:
+        rows = dominant_kernel_roofline(rnd, args.steps)
+        top = rows[0]
+        achieved = top["bytes_per_launch"] / (top["us_per_launch"] * 1e-6) / 1e9
+        result["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                              "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic_for(top["kernel"]),
+                              "kernel": top["kernel"], "launches_per_round": top["launches"],
+                              "us_per_launch": round(top["us_per_launch"], 3),
+                              "bytes_per_launch": int(top["bytes_per_launch"])}
+        result["kernels"] = [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()} for r in rows]
+        if not args.no_sweep:
+            sweep = {}
+            for M in (7, 14, 28, 42, 56):
+                r = Round(M, args.hidden, args.mlp, args.layers, weights, tables, device)
+                g = r.capture()
+                us = time_graph(g, max(10, args.steps // 2), 3) * 1000.0
+                sweep[str(M)] = {"us": round(us, 1), "gbps": round(r.bytes / (us * 1e-6) / 1e9, 1)}
+                del g, r
+            result["m_sweep"] = sweep
+            print(f"[bench] M sweep: {sweep}", file=sys.stderr, flush=True)
+        if not args.no_verify:
+            result["verify"] = time_verify(weights[-1], args.hidden, device, args.steps)
+    if args.cpu_seconds > 0:
+        result["cpu_baseline"] = cpu_baseline(args.hidden, args.mlp, args.M, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+def time_verify(w_lm, hidden, device, steps):
+    """Fused LM-head verify (X[56,hidden] x W[50257,hidden]^T, softmax/argmax/top-p) as a graph,
+    rotating over enough LM-head copies that each replay streams its weight from HBM."""
+    import torch
+
+    from plm_amd.verify import lm_head_verify
+    from plm_amd.workloads import TOP_P, proposals
+
+    copies = [w_lm] + [w_lm.clone() for _ in range(4)]          # 5 x 206 MB > 256 MB MALL
+    gen = torch.Generator(device=device).manual_seed(5000)
+    x = torch.randn(56, hidden, generator=gen, device=device).bfloat16()
+    pending = proposals(56).to(device)
+    acc = torch.empty(56, dtype=torch.bool, device=device)
+    am = torch.empty(56, dtype=torch.int64, device=device)
+    for w in copies:
+        lm_head_verify(x, w, pending, TOP_P, accept=acc, argmax=am)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for w in copies:
+            lm_head_verify(x, w, pending, TOP_P, accept=acc, argmax=am)
+    ms = time_graph(graph, max(5, steps // 2), 2) / len(copies)
+    nbytes = 2 * (w_lm.shape[0] * hidden + 56 * hidden) + 56 * (8 + 8 + 1)
+    del graph, copies
+    return {"us": round(ms * 1000.0, 2), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "bytes": nbytes, "accepted": int(acc.sum().item())}
+
+
+if __name__ == "__main__":
+    main()

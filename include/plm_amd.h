@@ -1,0 +1,108 @@
+/*
+ * plm_amd.h — C ABI of the MI355X (gfx950) kernels for the PLM round's dense linears.
+ *
+ * Plain pointers, sizes and a stream handle; no torch types. Every entry point launches on the
+ * caller's HIP stream, performs no host synchronisation and allocates nothing, so it can be
+ * recorded into a HIP graph. Status codes are PLM_OK (0) or a negative PLM_ERR_* value;
+ * plm_status_string() names them.
+ *
+ * Layouts follow the reference's GEMM: Y[M,N] = X[M,K] · W[N,K]^T, all row-major with the
+ * last dimension contiguous (plm/fast_gemm.py:3, 17-48). Leading dimensions are in elements.
+ */
+#ifndef PLM_AMD_H
+#define PLM_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types of X, W and Y (the reference's HALF_DTYPES, plm/fast_gemm.py:66). */
+enum plm_dtype { PLM_BF16 = 0, PLM_F16 = 1 };
+
+/* Rounding applied to the fp32 logits before the verify epilogue reads them.
+ * PLM_ROUND_F32 keeps the fp32 accumulator; PLM_ROUND_BF16 / PLM_ROUND_F16 round to the model
+ * dtype first, which is what the reference's decoder sees (plm/fast_gemm.py:46 casts the
+ * accumulator, plm/decoder.py:73 upcasts it again). */
+enum plm_round_mode { PLM_ROUND_F32 = 0, PLM_ROUND_BF16 = 1, PLM_ROUND_F16 = 2 };
+
+enum plm_status {
+  PLM_OK = 0,
+  PLM_ERR_ARGUMENT = -1,      /* bad size, stride, dtype or null pointer */
+  PLM_ERR_ALIGNMENT = -2,     /* a pointer or leading dimension is not 16-byte aligned */
+  PLM_ERR_TILE = -3,          /* no compiled kernel for this tile / M combination */
+  PLM_ERR_WORKSPACE = -4,     /* workspace missing or smaller than the query function says */
+  PLM_ERR_LAUNCH = -5         /* the HIP launch itself failed */
+};
+
+/*
+ * Tile configuration of one GEMM shape: the MI355X counterpart of the reference's
+ * {BLOCK_M, BLOCK_N, BLOCK_K, SPLIT_K, num_warps, num_stages} dict (plm/fast_gemm.py:64).
+ *   wave_frags : 16-row weight fragments per wavefront; the workgroup's N tile is 16*wave_frags.
+ *   k_waves    : wavefronts per workgroup; each takes a contiguous K slice and the slices are
+ *                summed through LDS in wave order 0..k_waves-1.
+ *   split_k    : workgroups per N tile splitting K further; their fp32 partials are summed in
+ *                split order 0..split_k-1 by the last workgroup to finish (no float atomics).
+ *   unroll     : 32-wide K steps loaded per batch by each wavefront.
+ */
+typedef struct plm_tile {
+  int32_t wave_frags;
+  int32_t k_waves;
+  int32_t split_k;
+  int32_t unroll;
+} plm_tile;
+
+/*
+ * Y[M,N] = X[M,K] · W[N,K]^T with fp32 accumulation, Y in the input dtype.
+ * Replaces triton_linear (plm/fast_gemm.py:82-97) together with gemm_kernel (17-48) and
+ * splitk_reduce_kernel (51-61). Requirements: 1 <= M <= 128, K % 8 == 0, ldx/ldw % 8 == 0,
+ * x and w 16-byte aligned. `workspace` may be NULL when plm_gemm_workspace_bytes() is 0;
+ * otherwise it must be zero-filled before its first use and is left zeroed for the next call.
+ */
+int plm_gemm(int32_t dtype, const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
+             int64_t M, int64_t N, int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes,
+             void* stream);
+
+/*
+ * As plm_gemm, but Y is fp32: the accumulator before the cast to the input dtype (the value the
+ * reference's gemm_kernel holds at plm/fast_gemm.py:46 before `.to(c dtype)`). With split_k == 1
+ * and the tile plm_lm_head_verify uses, these are bit for bit the logits the verify step reads.
+ */
+int plm_gemm_f32out(int32_t dtype, const void* x, int64_t ldx, const void* w, int64_t ldw, float* y, int64_t ldy,
+                    int64_t M, int64_t N, int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/* Workspace bytes plm_gemm needs for this shape and tile (the reference's _partial_buffer,
+ * plm/fast_gemm.py:70-79). 0 when split_k == 1. */
+size_t plm_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, const plm_tile* tile);
+
+/* 1 when a kernel is compiled for this tile at this M and K, else 0. */
+int plm_gemm_tile_supported(int32_t dtype, int64_t M, int64_t K, const plm_tile* tile);
+
+/*
+ * Fused LM-head verify step: logits[R,V] = X[R,K] · W[V,K]^T are formed tile by tile and never
+ * written to memory. For every row r:
+ *   accept[r] = nucleus membership of pending[r] at top-p `p`, as nucleus_acceptance
+ *               (plm/decoder.py:71-75): mass strictly above the proposal's own probability < p,
+ *               or the proposal is the row maximum and p > 0; p <= 0 accepts nothing.
+ *   argmax[r] = index of the row maximum, lowest index on ties (plm/decoder.py:362).
+ * `round_mode` (enum plm_round_mode) fixes the logits the decision reads. Requirements as
+ * plm_gemm, plus 0 <= pending[r] < V. `tile` uses split_k == 1.
+ */
+int plm_lm_head_verify(int32_t dtype, const void* x, int64_t ldx, const void* w, int64_t ldw, int64_t R, int64_t V,
+                       int64_t K, const int64_t* pending, float p, int32_t round_mode, uint8_t* accept,
+                       int64_t* argmax, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes plm_lm_head_verify needs. Zero-filled before first use; left zeroed. */
+size_t plm_lm_head_verify_workspace_bytes(int64_t R, int64_t V, int64_t K, const plm_tile* tile);
+
+/* Human-readable name of a status code. */
+const char* plm_status_string(int32_t status);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PLM_AMD_H */

@@ -1,0 +1,34 @@
+"""CPU oracle for the PLM round's dense-linear hot path. TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg import this package,
+and only as the checker (or the timed CPU baseline) — never as a product path. The HIP library in
+``plm-anon_amd/`` never calls it.
+
+Every function cites the reference lines it restates. Pinning (each is checked in
+``tests/test_oracle.py`` against an independent fp64 brute force, closed forms or special cases):
+
+* ``linear``                — pinned (fp64 brute force within one bf16/fp16 ulp, exact small-integer
+                              products, one-hot selection, reduction-order independence).
+* ``linear_fp32``           — pinned (fp64 brute force, fp32 tolerance).
+* ``nucleus_acceptance``    — pinned (fp64 sort-based brute force, one-hot / uniform / p<=0 /
+                              proposal-is-max / tie cases).
+* ``floor_acceptance``      — pinned (fp64 brute force, closed-form uniform case).
+* ``argmax``                — pinned (ties resolve to the lowest index, brute force).
+* ``verify``                — composition of the two above; pinned through them.
+* ``epilogue``              — pinned (hand-worked rounds: all accepted, none, first rejection).
+
+The reference ships no tests or golden vectors for this path (it has none at all), so the fixtures
+under ``tests/golden/`` are generated from this oracle on seeded inputs.
+"""
+
+from .plm_oracle import (  # noqa: F401
+    argmax,
+    epilogue,
+    floor_acceptance,
+    linear,
+    linear_fp32,
+    linear_fp64,
+    nucleus_acceptance,
+    nucleus_margin,
+    verify,
+)

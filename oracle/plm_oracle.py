@@ -1,0 +1,138 @@
+"""CPU restatement of the reference's round linears and verify epilogue. TEST INFRASTRUCTURE ONLY
+(imported by tests/, __graft_entry__.smoke() and bench.py's CPU baseline; never by the product).
+
+The GEMM oracle is the reference's own ``--mode default`` path: torch ``F.linear`` on the same
+half-precision operands (plm/fast_gemm.py:111), here on the CPU. The epilogue functions restate
+plm/decoder.py:71-82 and 351-362 with torch CPU ops; the ``*_fp64`` helpers are independent
+brute-force versions used to pin them.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+
+# --------------------------------------------------------------------------- GEMM
+
+def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """``x[M,K] @ w[N,K]^T`` in x's dtype via CPU ``F.linear`` (plm/fast_gemm.py:111; layout 3)."""
+    return F.linear(x.cpu(), w.cpu())
+
+
+def linear_fp32(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """fp32 product of the half-precision operands, without rounding the result (the accumulator the
+    reference's GEMM holds before its cast, plm/fast_gemm.py:35-46)."""
+    return x.cpu().float() @ w.cpu().float().T
+
+
+def linear_fp64(x: torch.Tensor, w: torch.Tensor) -> np.ndarray:
+    """Exact-as-possible fp64 brute force (numpy), the pin for the two functions above."""
+    xa = x.cpu().float().numpy().astype(np.float64)
+    wa = w.cpu().float().numpy().astype(np.float64)
+    return xa @ wa.T
+
+
+# --------------------------------------------------------------------------- verify epilogue
+
+def nucleus_acceptance(logits: torch.Tensor, pending: torch.Tensor, nucleus: float) -> torch.Tensor:
+    """Proposal inside the top-``nucleus`` mass (plm/decoder.py:71-75): the probability mass strictly
+    above the proposal's own probability is below ``nucleus``, or the proposal is the row maximum
+    and ``nucleus > 0``. ``nucleus <= 0`` accepts nothing."""
+    probs = torch.softmax(logits.cpu().float(), dim=-1)
+    own = probs.gather(1, pending.cpu()[:, None]).squeeze(1)
+    above = (probs * (probs > own[:, None])).sum(-1)
+    return (above < nucleus) | ((own >= probs.amax(-1)) & (nucleus > 0))
+
+
+def floor_acceptance(logits: torch.Tensor, pending: torch.Tensor, epsilon: float) -> torch.Tensor:
+    """Proposal probability above ``epsilon``, in the log domain (plm/decoder.py:78-82)."""
+    scores = logits.cpu().float()
+    own_logit = scores.gather(1, pending.cpu()[:, None]).squeeze(1)
+    return own_logit - torch.logsumexp(scores, dim=-1) > torch.log(torch.tensor(float(epsilon)))
+
+
+def argmax(logits: torch.Tensor) -> torch.Tensor:
+    """Row argmax with the lowest index among equal maxima (``logits.argmax(-1)``, plm/decoder.py:362)."""
+    return logits.cpu().float().argmax(dim=-1)
+
+
+def verify(logits: torch.Tensor, pending: torch.Tensor, nucleus: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """The fused verify step's two outputs for every row: nucleus decision and argmax."""
+    return nucleus_acceptance(logits, pending, nucleus), argmax(logits)
+
+
+def nucleus_margin(logits: torch.Tensor, pending: torch.Tensor, nucleus: float) -> np.ndarray:
+    """fp64 distance between each row's mass-above-own and ``nucleus`` (how far a decision is from
+    flipping under rounding); +inf where the proposal is the row maximum."""
+    z = logits.cpu().double().numpy()
+    z = z - z.max(axis=1, keepdims=True)
+    p = np.exp(z)
+    p /= p.sum(axis=1, keepdims=True)
+    idx = pending.cpu().numpy()
+    own = p[np.arange(len(idx)), idx]
+    above = np.where(p > own[:, None], p, 0.0).sum(axis=1)
+    margin = np.abs(above - nucleus)
+    margin[own >= p.max(axis=1)] = np.inf
+    return margin
+
+
+def nucleus_acceptance_fp64(logits: torch.Tensor, pending: torch.Tensor, nucleus: float) -> np.ndarray:
+    """Sort-based fp64 brute force of the nucleus rule: walk each row's probabilities in descending
+    order and sum everything strictly more probable than the proposal."""
+    z = logits.cpu().double().numpy()
+    out = np.zeros(z.shape[0], dtype=bool)
+    for r in range(z.shape[0]):
+        row = np.exp(z[r] - z[r].max())
+        row /= row.sum()
+        own = row[int(pending[r])]
+        order = np.sort(row)[::-1]
+        mass = 0.0
+        for v in order:
+            if v <= own:
+                break
+            mass += v
+        out[r] = (mass < nucleus) or (own >= order[0] and nucleus > 0)
+    return out
+
+
+def floor_acceptance_fp64(logits: torch.Tensor, pending: torch.Tensor, epsilon: float) -> np.ndarray:
+    z = logits.cpu().double().numpy()
+    m = z.max(axis=1)
+    lse = m + np.log(np.exp(z - m[:, None]).sum(axis=1))
+    own = z[np.arange(z.shape[0]), pending.cpu().numpy()]
+    return own - lse > np.log(epsilon)
+
+
+def argmax_fp64(logits: torch.Tensor) -> np.ndarray:
+    z = logits.cpu().double().numpy()
+    out = np.empty(z.shape[0], dtype=np.int64)
+    for r in range(z.shape[0]):
+        best = 0
+        for j in range(1, z.shape[1]):
+            if z[r, j] > z[r, best]:
+                best = j
+        out[r] = best
+    return out
+
+
+# --------------------------------------------------------------------------- the round epilogue
+
+def epilogue(logits: torch.Tensor, verify_tokens: torch.Tensor, pending: torch.Tensor, k: int, rule: str,
+             threshold: float) -> dict:
+    """One round's bookkeeping after the LM head (plm/decoder.py:351-365), without the state writes.
+
+    ``logits`` is ``[k + k*k, V]`` (verify rows first, then ``k`` proposal blocks of ``k``),
+    ``verify_tokens[k]`` the verify rows' own decodes, ``pending[k-1]`` last round's proposals.
+    Returns ``accepted[k-1]``, ``num_correct``, the ``num_correct + 1`` committed tokens and the next
+    round's ``pending[k-1]``."""
+    widened = floor_acceptance if rule == "floor" else nucleus_acceptance
+    accepted = (verify_tokens[:-1].cpu() == pending.cpu()) | widened(logits[: k - 1], pending, threshold)
+    num_correct = int(accepted.to(torch.int64).cumprod(0).sum())
+    confirmed_head = torch.cat([pending.cpu(), verify_tokens[-1:].cpu()])
+    picked = verify_tokens.cpu()[min(num_correct, k - 1)]
+    committed = torch.cat([confirmed_head[:num_correct], picked.view(1)])
+    hypotheses = argmax(logits[k:]).view(k, k)
+    return {"accepted": accepted, "num_correct": num_correct, "committed": committed,
+            "next_pending": hypotheses[num_correct][1:k]}

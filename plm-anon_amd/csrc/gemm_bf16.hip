@@ -1,0 +1,10 @@
+// bf16 instantiations of the skinny GEMM (one translation unit per dtype so they build in parallel).
+#include "gemm_kernel.h"
+
+namespace plm {
+
+hipError_t gemm_dispatch_bf16(const GemmArgs& a, const plm_tile& t, hipStream_t s, bool dry) {
+  return gemm_dispatch<DT_BF16>(a, t, s, dry);
+}
+
+}  // namespace plm

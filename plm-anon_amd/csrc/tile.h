@@ -1,0 +1,202 @@
+// Device building blocks shared by the GEMM and the fused LM-head verify kernels.
+//
+// Orientation: a wavefront computes a slab of Y^T = W · X^T with v_mfma_f32_16x16x32_{bf16,f16}.
+// The MFMA's A operand is a 16-row weight fragment (16 rows of W[N,K], the long dimension), its
+// B operand a 16-row fragment of X[M,K] (the skinny round dimension). Lane l supplies row l%16
+// and the eight K elements [8*(l/16), 8*(l/16)+8) of a 32-wide K step to both operands, so every
+// operand is one 16-byte global load per lane, straight from HBM into VGPRs (weights are read
+// exactly once and need no LDS staging). Accumulator register r of lane l holds
+// D[row = 4*(l/16) + r][col = l%16], i.e. weight row n0 + 16f + 4*(l/16) + r and X row 16t + l%16.
+//
+// Bit-identity contract: wave_mma() visits K steps in ascending order and wg_sum() adds the
+// wavefronts' partials in wave order, so any kernel that calls them with the same tile geometry
+// and K partition produces the same fp32 value for an element, whatever the other rows hold.
+// The verify step relies on this to recompute a proposal's own logit outside the main pass.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace plm {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+enum { DT_BF16 = 0, DT_F16 = 1 };
+
+template <int DT>
+__device__ __forceinline__ f32x4 mfma_16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (DT == DT_BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+}
+
+// fp32 -> 16-bit storage, round to nearest even (what torch's .to(bfloat16/float16) does).
+template <int DT>
+__device__ __forceinline__ uint16_t to_bits16(float v) {
+  if constexpr (DT == DT_BF16) {
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
+  } else {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+  }
+}
+
+__device__ __forceinline__ float round_through(float v, int mode) {
+  if (mode == 1) return static_cast<float>(static_cast<__bf16>(v));
+  if (mode == 2) return static_cast<float>(static_cast<_Float16>(v));
+  return v;
+}
+
+// Buffer resource over `bytes` bytes at `base`. A raw buffer load whose byte offset is at or past
+// `bytes` returns zeros, which masks rows past the end of a tile, padded X rows and the K tail
+// without branches around the loads.
+constexpr uint32_t kOutOfRange = 0x80000000u;
+constexpr int kBufferWord3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                           kBufferWord3);
+}
+
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0));
+}
+
+inline bool aligned16_ptr(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Half-open K-step range [st0, st1) of slice `piece` out of `pieces`, over ceil(K/32) steps.
+__device__ __forceinline__ void k_slice(int K, int piece, int pieces, int& st0, int& st1) {
+  const int steps = (K + 31) >> 5;
+  st0 = static_cast<int>((static_cast<int64_t>(piece) * steps) / pieces);
+  st1 = static_cast<int>((static_cast<int64_t>(piece + 1) * steps) / pieces);
+}
+
+// Per-lane byte offsets of the operand rows this lane feeds. Rows outside [lo, hi) get an
+// out-of-range offset and load as zeros.
+template <int NROW16>
+__device__ __forceinline__ void row_offsets(int64_t ld, int lo, int hi, int lane, uint32_t (&off)[NROW16]) {
+  const int row = lane & 15;
+  const int kq = (lane >> 4) << 3;
+#pragma unroll
+  for (int i = 0; i < NROW16; ++i) {
+    const int r = 16 * i + row;
+    off[i] = (r >= lo && r < hi) ? static_cast<uint32_t>((r * ld + kq) * 2) : kOutOfRange;
+  }
+}
+
+template <int MT, int NF, int U>
+struct Chunk {
+  u32x4 w[NF][U];
+  u32x4 x[MT][U];
+};
+
+// Loads K steps [st, st+n) (n <= U; steps past n are not loaded). Lanes whose K index is past K
+// read zeros.
+template <int MT, int NF, int U>
+__device__ __forceinline__ void load_chunk(Chunk<MT, NF, U>& c, __amdgpu_buffer_rsrc_t xr, const uint32_t (&xoff)[MT],
+                                           __amdgpu_buffer_rsrc_t wr, const uint32_t (&woff)[NF], int K, int st,
+                                           int n, int lane) {
+  const int kq = (lane >> 4) << 3;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (u < n) {
+      const int k = (st + u) * 32;
+      const uint32_t kb = static_cast<uint32_t>(k) * 2u;
+      const bool kin = k + kq < K;
+#pragma unroll
+      for (int f = 0; f < NF; ++f) c.w[f][u] = buffer_load16(wr, kin ? woff[f] + kb : kOutOfRange);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) c.x[t][u] = buffer_load16(xr, kin ? xoff[t] + kb : kOutOfRange);
+    }
+  }
+}
+
+template <int DT, int MT, int NF, int U>
+__device__ __forceinline__ void mma_chunk(const Chunk<MT, NF, U>& c, int n, f32x4 (&acc)[NF][MT]) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (u < n) {
+#pragma unroll
+      for (int f = 0; f < NF; ++f)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) acc[f][t] = mfma_16x16x32<DT>(c.w[f][u], c.x[t][u], acc[f][t]);
+    }
+  }
+}
+
+// acc[f][t] += Wtile[16f .. 16f+16, steps] · X[16t .. 16t+16, steps]^T over K steps [st0, st1),
+// in ascending step order. `wr` covers the weight tile (rows past its end read as zeros), `xr`
+// covers X. st0/st1 must be wave-uniform.
+//   PIPE = false: batches of U steps, each loaded in full before its MFMAs (one register buffer;
+//                 the right choice when a wavefront's slice is at most U steps).
+//   PIPE = true : two register buffers; the next batch's loads are in flight while the current
+//                 batch's MFMAs run, so long slices stream without a latency bubble per batch.
+template <int DT, int MT, int NF, int U, bool PIPE>
+__device__ __forceinline__ void wave_mma(__amdgpu_buffer_rsrc_t xr, const uint32_t (&xoff)[MT],
+                                         __amdgpu_buffer_rsrc_t wr, const uint32_t (&woff)[NF], int K, int st0,
+                                         int st1, int lane, f32x4 (&acc)[NF][MT]) {
+  int st = st0;
+  int left = st1 - st0;
+  if constexpr (!PIPE) {
+    Chunk<MT, NF, U> c;
+    while (left > 0) {
+      const int n = left < U ? left : U;
+      load_chunk<MT, NF, U>(c, xr, xoff, wr, woff, K, st, n, lane);
+      mma_chunk<DT, MT, NF, U>(c, n, acc);
+      st += n;
+      left -= n;
+    }
+  } else {
+    if (left <= 0) return;
+    Chunk<MT, NF, U> ca, cb;
+    int na = left < U ? left : U;
+    load_chunk<MT, NF, U>(ca, xr, xoff, wr, woff, K, st, na, lane);
+    while (true) {
+      st += na;
+      left -= na;
+      const int nb = left < U ? left : U;
+      if (nb > 0) load_chunk<MT, NF, U>(cb, xr, xoff, wr, woff, K, st, nb, lane);
+      mma_chunk<DT, MT, NF, U>(ca, na, acc);
+      if (nb <= 0) break;
+      st += nb;
+      left -= nb;
+      na = left < U ? left : U;
+      if (na > 0) load_chunk<MT, NF, U>(ca, xr, xoff, wr, woff, K, st, na, lane);
+      mma_chunk<DT, MT, NF, U>(cb, nb, acc);
+      if (na <= 0) break;
+    }
+  }
+}
+
+// LDS layout of the wavefront partials: red[((w*NF*MT + f*MT + t)*4 + r)*64 + lane].
+template <int MT, int NF>
+__device__ __forceinline__ void wave_spill(float* red, int wave, int lane, const f32x4 (&acc)[NF][MT]) {
+#pragma unroll
+  for (int f = 0; f < NF; ++f)
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[((wave * NF * MT + f * MT + t) * 4 + r) * 64 + lane] = acc[f][t][r];
+}
+
+// LDS offset (within one wavefront's block) of tile element (n_local, m_local).
+template <int MT, int NF>
+__device__ __forceinline__ int red_offset(int n_local, int m_local) {
+  const int f = n_local >> 4, i = n_local & 15, t = m_local >> 4, mm = m_local & 15;
+  return ((f * MT + t) * 4 + (i & 3)) * 64 + (i >> 2) * 16 + mm;
+}
+
+// Sum of the k_waves partials of one element, in wave order.
+template <int MT, int NF>
+__device__ __forceinline__ float wg_sum(const float* red, int k_waves, int off) {
+  constexpr int per_wave = NF * MT * 256;
+  float s = red[off];
+  for (int w = 1; w < k_waves; ++w) s += red[w * per_wave + off];
+  return s;
+}
+
+}  // namespace plm

@@ -1,0 +1,94 @@
+"""ctypes binding of ``libplm_amd.so`` (the C ABI in ``include/plm_amd.h``).
+
+The library is the only compute path: if it is missing or fails to load, every entry point raises
+``RuntimeError`` naming the problem. There is no CPU or library fallback behind it.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch  # loads the HIP runtime the kernels register with, before the library is opened
+
+LIBRARY = Path(__file__).resolve().parent / "libplm_amd.so"
+
+PLM_BF16, PLM_F16 = 0, 1
+PLM_ROUND_F32, PLM_ROUND_BF16, PLM_ROUND_F16 = 0, 1, 2
+DTYPE_CODES = {torch.bfloat16: PLM_BF16, torch.float16: PLM_F16}
+
+# Every symbol include/plm_amd.h declares.
+EXPORTS = (
+    "plm_gemm",
+    "plm_gemm_f32out",
+    "plm_gemm_workspace_bytes",
+    "plm_gemm_tile_supported",
+    "plm_lm_head_verify",
+    "plm_lm_head_verify_workspace_bytes",
+    "plm_status_string",
+)
+
+
+class Tile(ctypes.Structure):
+    """``struct plm_tile``: wave_frags, k_waves, split_k, unroll."""
+
+    _fields_ = [("wave_frags", ctypes.c_int32), ("k_waves", ctypes.c_int32), ("split_k", ctypes.c_int32),
+                ("unroll", ctypes.c_int32)]
+
+    @classmethod
+    def from_config(cls, cfg: dict) -> "Tile":
+        return cls(int(cfg["wave_frags"]), int(cfg["k_waves"]), int(cfg.get("split_k", 1)), int(cfg["unroll"]))
+
+
+_lib: ctypes.CDLL | None = None
+_lock = threading.Lock()
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    c_i32, c_i64, c_p, c_sz = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t
+    tile_p = ctypes.POINTER(Tile)
+    lib.plm_gemm.argtypes = [c_i32, c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, tile_p, c_p, c_sz, c_p]
+    lib.plm_gemm.restype = ctypes.c_int
+    lib.plm_gemm_f32out.argtypes = lib.plm_gemm.argtypes
+    lib.plm_gemm_f32out.restype = ctypes.c_int
+    lib.plm_gemm_workspace_bytes.argtypes = [c_i64, c_i64, c_i64, tile_p]
+    lib.plm_gemm_workspace_bytes.restype = c_sz
+    lib.plm_gemm_tile_supported.argtypes = [c_i32, c_i64, c_i64, tile_p]
+    lib.plm_gemm_tile_supported.restype = ctypes.c_int
+    lib.plm_lm_head_verify.argtypes = [c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, c_p, ctypes.c_float, c_i32,
+                                       c_p, c_p, tile_p, c_p, c_sz, c_p]
+    lib.plm_lm_head_verify.restype = ctypes.c_int
+    lib.plm_lm_head_verify_workspace_bytes.argtypes = [c_i64, c_i64, c_i64, tile_p]
+    lib.plm_lm_head_verify_workspace_bytes.restype = c_sz
+    lib.plm_status_string.argtypes = [c_i32]
+    lib.plm_status_string.restype = ctypes.c_char_p
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded kernel library; raises RuntimeError if it has not been built."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not LIBRARY.exists():
+                    raise RuntimeError(f"{LIBRARY} is missing: build it with __graft_entry__.build() "
+                                       "(or `python -m plm_amd._build` in plm-anon_amd/)")
+                handle = ctypes.CDLL(str(LIBRARY))
+                missing = [name for name in EXPORTS if not hasattr(handle, name)]
+                if missing:
+                    raise RuntimeError(f"{LIBRARY} does not export {missing}")
+                _declare(handle)
+                _lib = handle
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = lib().plm_status_string(status).decode()
+        raise RuntimeError(f"{what} failed: {msg} (status {status})")
+
+
+def stream_handle(device: torch.device) -> int:
+    """The raw hipStream_t of torch's current stream on ``device``."""
+    return torch.cuda.current_stream(device).cuda_stream

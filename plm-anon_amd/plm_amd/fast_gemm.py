@@ -1,0 +1,181 @@
+"""HIP skinny GEMM for the decode-width shapes of a PLM round, as a drop-in for the reference's
+``plm.fast_gemm`` (plm/fast_gemm.py).
+
+``C[M,N] = A[M,K] @ W[N,K]^T`` with fp32 accumulation on gfx950 MFMA, output in the input dtype.
+Split-K partials are combined inside the same launch in a fixed order, so results are bitwise
+reproducible run to run (plm/fast_gemm.py:3-4). ``install`` routes eligible calls through the
+kernel: the build's own dispatch slot always, and vLLM's ``default_unquantized_gemm`` when vLLM is
+importable (plm/fast_gemm.py:100-113). Tile configs are keyed on ``(M, N, K)``; shapes without a
+config go to ``F.linear``, exactly as in the reference.
+"""
+
+from __future__ import annotations
+
+import threading
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+
+# {"wave_frags", "k_waves", "split_k", "unroll"}: the MI355X counterpart of the reference's
+# {BLOCK_M, BLOCK_N, BLOCK_K, SPLIT_K, num_warps, num_stages} (plm/fast_gemm.py:64).
+Config = dict[str, int]
+
+HALF_DTYPES = (torch.bfloat16, torch.float16)
+
+CONFIGS: dict[tuple[int, int, int], Config] = {}
+
+_tiles: dict[tuple[int, int, int, int], _lib.Tile] = {}
+_workspaces: dict[int, torch.Tensor] = {}
+_ws_lock = threading.Lock()
+
+
+def _tile(cfg: Config) -> _lib.Tile:
+    key = (int(cfg["wave_frags"]), int(cfg["k_waves"]), int(cfg.get("split_k", 1)), int(cfg["unroll"]))
+    t = _tiles.get(key)
+    if t is None:
+        t = _tiles[key] = _lib.Tile(*key)
+    return t
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Per-device zero-filled byte workspace of at least ``nbytes`` (the reference's ``_partials``,
+    plm/fast_gemm.py:70-79). Kernels leave it zeroed. It grows only outside HIP-graph capture:
+    size it with an eager call (or ``reserve_workspace``) before capturing."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    buf = _workspaces.get(index)
+    if buf is None or buf.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(f"plm_amd workspace needs {nbytes} bytes on cuda:{index} during graph capture; "
+                               "run the shape eagerly (or call reserve_workspace) before capturing")
+        with _ws_lock:
+            buf = _workspaces.get(index)
+            if buf is None or buf.numel() < nbytes:
+                size = max(nbytes, 2 * buf.numel() if buf is not None else 0, 1 << 20)
+                buf = torch.zeros(size, dtype=torch.uint8, device=torch.device("cuda", index))
+                _workspaces[index] = buf
+    return buf
+
+
+def gemm_workspace_bytes(M: int, N: int, K: int, cfg: Config) -> int:
+    return int(_lib.lib().plm_gemm_workspace_bytes(M, N, K, _tile(cfg)))
+
+
+def tile_supported(M: int, K: int, cfg: Config, dtype: torch.dtype = torch.bfloat16) -> bool:
+    return bool(_lib.lib().plm_gemm_tile_supported(_lib.DTYPE_CODES[dtype], M, K, _tile(cfg)))
+
+
+def reserve_workspace(device: torch.device, shapes: dict[tuple[int, int, int], Config] | None = None) -> None:
+    """Size the device workspace for every configured shape, so later calls can be graph-captured."""
+    shapes = CONFIGS if shapes is None else shapes
+    need = max((gemm_workspace_bytes(M, N, K, cfg) for (M, N, K), cfg in shapes.items()), default=0)
+    if need:
+        workspace(device, need)
+
+
+def _row_major(t: torch.Tensor) -> torch.Tensor:
+    """``t`` itself if the kernel can read it in place (unit inner stride, 16-byte aligned rows)."""
+    if t.stride(1) == 1 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0 and t.stride(0) >= t.shape[1]:
+        return t
+    return t.contiguous()
+
+
+def _launch(a: torch.Tensor, w: torch.Tensor, cfg: Config, out: torch.Tensor, f32_out: bool) -> torch.Tensor:
+    M, K = a.shape
+    N = w.shape[0]
+    a = _row_major(a)
+    w = _row_major(w)
+    tile = _tile(cfg)
+    lib = _lib.lib()
+    need = int(lib.plm_gemm_workspace_bytes(M, N, K, tile))
+    ws_ptr, ws_bytes = None, 0
+    if need:
+        ws = workspace(a.device, need)
+        ws_ptr, ws_bytes = ws.data_ptr(), ws.numel()
+    entry = lib.plm_gemm_f32out if f32_out else lib.plm_gemm
+    status = entry(_lib.DTYPE_CODES[a.dtype], a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0), out.data_ptr(),
+                   out.stride(0), M, N, K, tile, ws_ptr, ws_bytes, _lib.stream_handle(a.device))
+    _lib.check(status, f"plm_gemm(M={M}, N={N}, K={K}, cfg={cfg})")
+    return out
+
+
+def _check_operands(a: torch.Tensor, w: torch.Tensor) -> None:
+    if a.dim() != 2 or w.dim() != 2 or a.shape[1] != w.shape[1]:
+        raise ValueError(f"hip_linear expects a[M,K] and w[N,K], got {tuple(a.shape)} and {tuple(w.shape)}")
+    if a.dtype not in HALF_DTYPES or w.dtype != a.dtype:
+        raise TypeError(f"hip_linear needs matching bf16/fp16 operands, got {a.dtype} and {w.dtype}")
+    if not (a.is_cuda and w.is_cuda):
+        raise RuntimeError("hip_linear runs on the GPU only; got a CPU tensor")
+
+
+def hip_linear(a: torch.Tensor, w: torch.Tensor, cfg: Config, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``out[M,N] = a[M,K] @ w[N,K]^T`` on the HIP kernel (the reference's ``triton_linear``,
+    plm/fast_gemm.py:82-97). ``out`` is allocated as ``empty(M, N)`` in ``a``'s dtype if None."""
+    _check_operands(a, w)
+    M, N = a.shape[0], w.shape[0]
+    if out is None:
+        out = torch.empty(M, N, device=a.device, dtype=a.dtype)
+    elif out.shape != (M, N) or out.dtype != a.dtype or out.stride(1) != 1:
+        raise ValueError(f"out must be a row-major [{M},{N}] {a.dtype} tensor")
+    return _launch(a, w, cfg, out, False)
+
+
+def hip_linear_f32(a: torch.Tensor, w: torch.Tensor, cfg: Config, out: torch.Tensor | None = None) -> torch.Tensor:
+    """As ``hip_linear`` but returns the fp32 accumulator (no cast to the input dtype)."""
+    _check_operands(a, w)
+    M, N = a.shape[0], w.shape[0]
+    if out is None:
+        out = torch.empty(M, N, device=a.device, dtype=torch.float32)
+    elif out.shape != (M, N) or out.dtype != torch.float32 or out.stride(1) != 1:
+        raise ValueError(f"out must be a row-major [{M},{N}] float32 tensor")
+    return _launch(a, w, cfg, out, True)
+
+
+def fast_gemm(layer, x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """vLLM ``default_unquantized_gemm`` signature; tuned 2-D half-precision calls without bias go to
+    the HIP kernel, everything else to ``F.linear`` (plm/fast_gemm.py:106-111)."""
+    if bias is None and x.dim() == 2 and x.dtype in HALF_DTYPES:
+        cfg = CONFIGS.get((x.shape[0], weight.shape[0], weight.shape[1]))
+        if cfg is not None:
+            return hip_linear(x, weight, cfg)
+    return F.linear(x, weight, bias)
+
+
+def _default_gemm(layer, x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    return F.linear(x, weight, bias)
+
+
+# The build's own dispatch slot, standing in for vLLM's where vLLM is absent.
+default_unquantized_gemm = _default_gemm
+
+
+def dispatch_unquantized_gemm():
+    """The GEMM currently installed in the build's slot (vLLM's ``dispatch_unquantized_gemm()``)."""
+    return default_unquantized_gemm
+
+
+def install(configs: dict[tuple[int, int, int], Config]) -> None:
+    """Route unquantized GEMMs with a configured ``(M, N, K)`` through the HIP kernel.
+
+    Loads the kernel library first (raising if it is not built) and rejects tiles the library has
+    no kernel for, so a bad table fails here rather than at the first call."""
+    global default_unquantized_gemm
+    lib = _lib.lib()
+    for (M, N, K), cfg in configs.items():
+        if not lib.plm_gemm_tile_supported(_lib.PLM_BF16, M, K, _tile(cfg)):
+            raise ValueError(f"no compiled MI355X kernel for tile {cfg} at (M={M}, N={N}, K={K})")
+    CONFIGS.update(configs)
+    default_unquantized_gemm = fast_gemm
+    try:
+        import vllm.model_executor.layers.utils as vllm_utils
+    except ImportError:
+        return
+    vllm_utils.default_unquantized_gemm = fast_gemm
+
+
+def uninstall() -> None:
+    """Restore ``F.linear`` in the build's slot and forget every configured shape."""
+    global default_unquantized_gemm
+    CONFIGS.clear()
+    default_unquantized_gemm = _default_gemm

@@ -1,0 +1,162 @@
+"""Per-shape tile tuner for MI355X and the tile-table key sets.
+
+``python -m plm_amd.tune --heuristic`` writes every table from ``tiles.heuristic_tile`` (no GPU).
+``python -m plm_amd.tune [--hidden 2048 ...]`` times every candidate tile of every key on the GPU
+and writes the fastest into ``gpu_tuning/tiles_hidden<H>.json``.
+
+Timing: each candidate runs as a HIP graph of back-to-back launches that rotate over enough
+distinct weight copies (>= 1 GiB in total) that no launch finds its weight in the 256 MB
+Infinity Cache; the figure is graph time / launches, so it includes the inter-kernel gap a round
+sees. Only correct candidates count: each is checked against the fp32 product first.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import sys
+
+from . import tiles
+from .gemm_tables import TABLES
+from .workloads import GPT2_VOCAB, M_SWEEP
+
+# The reference's tuned keys (plm/gpu_tuning/tiles_hidden<H>.json): Llama shapes from
+# model_shapes() at the widths the reference tunes.
+REFERENCE_KEYS: dict[int, list[tuple[int, int, int]]] = {
+    512: [(42, 768, 512), (42, 512, 512), (42, 2816, 512), (42, 512, 1408), (42, 50304, 512)],
+    768: [(42, 1152, 768), (42, 768, 768), (42, 4096, 768), (42, 768, 2048), (42, 50304, 768)],
+    1024: [(42, 1536, 1024), (42, 1024, 1024), (42, 5120, 1024), (42, 1024, 2560), (42, 50304, 1024)],
+    2048: [(w, n, k) for w in (42, 56, 110)
+           for n, k in ((3072, 2048), (2048, 2048), (11264, 2048), (2048, 5632), (50304, 2048))],
+    3072: [(w, n, k) for w in (42, 56, 110)
+           for n, k in ((4608, 3072), (3072, 3072), (16384, 3072), (3072, 8192), (50304, 3072))],
+}
+
+
+def _gpt_keys(M: int, hidden: int, mlp: int) -> list[tuple[int, int, int]]:
+    return [(M, 3 * hidden, hidden), (M, hidden, hidden), (M, mlp, hidden), (M, hidden, mlp), (M, GPT2_VOCAB, hidden)]
+
+
+# The GPT-style shapes the benchmark measures: the 350M MLP up at k=6, the 1.3B round at every
+# partial-round width, and the 3B round at k=7.
+BENCH_KEYS: dict[int, list[tuple[int, int, int]]] = {
+    1024: [(42, 4096, 1024)],
+    2048: [key for M in M_SWEEP for key in _gpt_keys(M, 2048, 8192)],
+    2560: _gpt_keys(56, 2560, 10240),
+}
+
+
+def table_keys(hidden: int) -> list[tuple[int, int, int]]:
+    keys = REFERENCE_KEYS.get(hidden, []) + BENCH_KEYS.get(hidden, [])
+    return sorted(set(keys), key=lambda k: (k[0], k[1], k[2]))
+
+
+def all_hidden() -> list[int]:
+    return sorted(set(REFERENCE_KEYS) | set(BENCH_KEYS))
+
+
+def write_table(hidden: int, table: dict[tuple[int, int, int], dict]) -> None:
+    TABLES.mkdir(exist_ok=True)
+    text = json.dumps({f"{M},{N},{K}": cfg for (M, N, K), cfg in sorted(table.items())}, indent=1)
+    (TABLES / f"tiles_hidden{hidden}.json").write_text(text + "\n")
+
+
+def heuristic_tables() -> None:
+    from .fast_gemm import tile_supported
+
+    for hidden in all_hidden():
+        write_table(hidden, {key: tiles.heuristic_tile(*key, supported=lambda c, k=key: tile_supported(k[0], k[2], c))
+                             for key in table_keys(hidden)})
+
+
+# --------------------------------------------------------------------------- GPU tuning
+
+
+def time_tile(M: int, N: int, K: int, cfg: dict, weights, x, out, reps: int = 3) -> float:
+    """Microseconds per launch of ``cfg`` over the rotating weight copies, from graph replays."""
+    import torch
+
+    from .fast_gemm import hip_linear
+
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for w in weights:                       # eager warm-up (also sizes the workspace)
+            hip_linear(x, w, cfg, out)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for w in weights:
+                hip_linear(x, w, cfg, out)
+        graph.replay()
+        torch.cuda.synchronize()
+        best = math.inf
+        for _ in range(reps):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            graph.replay()
+            end.record(stream)
+            end.synchronize()
+            best = min(best, start.elapsed_time(end) * 1000.0 / len(weights))
+    return best
+
+
+def tune_key(M: int, N: int, K: int, verbose: bool = True) -> tuple[dict, float, list]:
+    import torch
+
+    from .fast_gemm import hip_linear, tile_supported
+
+    dev = torch.device("cuda")
+    w_bytes = 2 * N * K
+    copies = max(2, min(64, math.ceil((1 << 30) / w_bytes)))
+    gen = torch.Generator(device=dev).manual_seed(N * 7 + K)
+    weights = [(0.02 * torch.randn(N, K, generator=gen, device=dev)).bfloat16() for _ in range(copies)]
+    x = torch.randn(M, K, generator=gen, device=dev).bfloat16()
+    out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+    ref = (x.float() @ weights[0].float().T)
+    results = []
+    for cfg in tiles.candidates(M, N, K, lambda c: tile_supported(M, K, c)):
+        y = hip_linear(x, weights[0], cfg).float()
+        if not torch.allclose(y, ref, rtol=1e-2, atol=2e-2):
+            raise RuntimeError(f"tile {cfg} is wrong at {(M, N, K)}: max err {(y - ref).abs().max().item()}")
+        results.append((time_tile(M, N, K, cfg, weights, x, out), cfg))
+    results.sort(key=lambda r: r[0])
+    best_us, best = results[0]
+    if verbose:
+        gbps = (2 * (N * K + M * K + M * N)) / (best_us * 1e-6) / 1e9
+        print(f"{M},{N},{K}: {best} {best_us:.2f} us {gbps:.0f} GB/s ({len(results)} candidates)", flush=True)
+    del weights
+    torch.cuda.empty_cache()
+    return best, best_us, results
+
+
+def main(argv: list[str] | None = None) -> None:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--heuristic", action="store_true", help="write heuristic tables without a GPU")
+    ap.add_argument("--hidden", type=int, nargs="*", help="hidden sizes to tune (default: all)")
+    ap.add_argument("--keys", nargs="*", help="only these M,N,K keys")
+    ap.add_argument("--log", help="write every candidate's timing to this JSON file")
+    args = ap.parse_args(argv)
+    if args.heuristic:
+        heuristic_tables()
+        return
+    log = {}
+    for hidden in args.hidden or all_hidden():
+        path = TABLES / f"tiles_hidden{hidden}.json"
+        table = {tuple(int(v) for v in k.split(",")): c for k, c in json.loads(path.read_text()).items()} \
+            if path.exists() else {}
+        for key in table_keys(hidden):
+            if args.keys and f"{key[0]},{key[1]},{key[2]}" not in args.keys:
+                continue
+            best, best_us, results = tune_key(*key)
+            table[key] = best
+            log[f"{key[0]},{key[1]},{key[2]}"] = [(us, cfg) for us, cfg in results]
+            write_table(hidden, table)
+    if args.log:
+        with open(args.log, "w") as fh:
+            json.dump(log, fh)
+    print("tuning done", file=sys.stderr)
+
+
+if __name__ == "__main__":
+    main()

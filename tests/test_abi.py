@@ -1,0 +1,181 @@
+"""CPU checks of the C ABI and the host logic: the library loads, exports every symbol the header
+declares, validates arguments before touching the GPU, and the tile tables follow the reference's
+contract (plm/gemm_tables.py). No kernel is launched here."""
+
+from __future__ import annotations
+
+import ctypes
+import json
+import re
+from pathlib import Path
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from plm_amd import _lib, fast_gemm, gemm_tables, tiles, workloads
+
+REPO = Path(__file__).resolve().parents[1]
+HEADER = REPO / "include" / "plm_amd.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(plm_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    names = declared_functions()
+    assert "plm_gemm" in names and "plm_lm_head_verify" in names
+    lib = ctypes.CDLL(str(_lib.LIBRARY))
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_lib.EXPORTS)
+
+
+def test_status_strings():
+    lib = _lib.lib()
+    assert lib.plm_status_string(0).decode() == "ok"
+    for code in (-1, -2, -3, -4, -5):
+        assert lib.plm_status_string(code).decode() != "unknown status"
+
+
+def test_argument_validation_happens_before_launch():
+    lib = _lib.lib()
+    tile = _lib.Tile(2, 8, 1, 8)
+    fake = 1 << 20  # never dereferenced: every call below fails validation first
+    # K not a multiple of 8.
+    assert lib.plm_gemm(0, fake, 1024, fake, 1024, fake, 4096, 42, 4096, 1020, tile, None, 0, None) == -1
+    # M out of range.
+    assert lib.plm_gemm(0, fake, 1024, fake, 1024, fake, 4096, 0, 4096, 1024, tile, None, 0, None) == -1
+    assert lib.plm_gemm(0, fake, 1024, fake, 1024, fake, 4096, 129, 4096, 1024, tile, None, 0, None) == -1
+    # Misaligned pointer.
+    assert lib.plm_gemm(0, fake + 2, 1024, fake, 1024, fake, 4096, 42, 4096, 1024, tile, None, 0, None) == -2
+    # Unknown dtype.
+    assert lib.plm_gemm(7, fake, 1024, fake, 1024, fake, 4096, 42, 4096, 1024, tile, None, 0, None) == -1
+    # Split-K without a workspace.
+    split = _lib.Tile(2, 8, 4, 2)
+    assert lib.plm_gemm(0, fake, 1024, fake, 1024, fake, 4096, 42, 4096, 1024, split, None, 0, None) == -4
+    # A tile with no compiled kernel.
+    odd = _lib.Tile(3, 8, 1, 8)
+    assert lib.plm_gemm(0, fake, 1024, fake, 1024, fake, 4096, 42, 4096, 1024, odd, None, 0, None) == -3
+    # Verify: bad round mode, R too large.
+    vt = _lib.Tile(2, 4, 1, 4)
+    assert lib.plm_lm_head_verify(0, fake, 2048, fake, 2048, 56, 50257, 2048, fake, 0.94, 9, fake, fake, vt, fake,
+                                  1 << 30, None) == -1
+    assert lib.plm_lm_head_verify(0, fake, 2048, fake, 2048, 65, 50257, 2048, fake, 0.94, 0, fake, fake, vt, fake,
+                                  1 << 30, None) == -1
+
+
+def test_workspace_sizes():
+    lib = _lib.lib()
+    assert lib.plm_gemm_workspace_bytes(56, 2048, 8192, _lib.Tile(2, 8, 1, 4)) == 0
+    n = lib.plm_gemm_workspace_bytes(56, 2048, 8192, _lib.Tile(2, 8, 4, 4))
+    assert n >= 4 * 56 * 2048 * 4 + 64 * 4
+    assert lib.plm_lm_head_verify_workspace_bytes(56, 50257, 2048, _lib.Tile(2, 4, 1, 4)) > 56 * 4
+
+
+def test_tile_support_matches_register_budget():
+    # Every heuristic tile for the measured shapes has a compiled kernel.
+    for w in workloads.WORKLOADS.values():
+        for g in w.gemms:
+            cfg = tiles.heuristic_tile(w.M, g.N, g.K)
+            assert fast_gemm.tile_supported(w.M, g.K, cfg), (g, cfg)
+    assert not fast_gemm.tile_supported(56, 2048, {"wave_frags": 4, "k_waves": 8, "split_k": 1, "unroll": 8})
+
+
+# --------------------------------------------------------------------------- tile tables
+
+
+def llama(hidden, intermediate, heads, kv_heads, vocab=50257):
+    return SimpleNamespace(hidden_size=hidden, intermediate_size=intermediate, head_dim=hidden // heads,
+                           num_attention_heads=heads, num_key_value_heads=kv_heads, vocab_size=vocab)
+
+
+def test_model_shapes_follow_reference_formula():
+    cfg = llama(2048, 5632, 16, 4)
+    shapes = gemm_tables.model_shapes(cfg)
+    assert shapes == {"qkv": (3072, 2048), "o": (2048, 2048), "gate_up": (11264, 2048), "down": (2048, 5632),
+                      "lm_head": (50304, 2048)}
+
+
+def test_every_table_covers_the_reference_keys():
+    # The reference's tile tables' keys (plm/gpu_tuning/*.json), at the widths it tunes.
+    expect = {
+        512: {(42, 768, 512), (42, 512, 512), (42, 2816, 512), (42, 512, 1408), (42, 50304, 512)},
+        768: {(42, 1152, 768), (42, 768, 768), (42, 4096, 768), (42, 768, 2048), (42, 50304, 768)},
+        1024: {(42, 1536, 1024), (42, 1024, 1024), (42, 5120, 1024), (42, 1024, 2560), (42, 50304, 1024)},
+        2048: {(w, n, k) for w in (42, 56, 110)
+               for n, k in ((3072, 2048), (2048, 2048), (11264, 2048), (2048, 5632), (50304, 2048))},
+        3072: {(w, n, k) for w in (42, 56, 110)
+               for n, k in ((4608, 3072), (3072, 3072), (16384, 3072), (3072, 8192), (50304, 3072))},
+    }
+    for hidden, keys in expect.items():
+        table = gemm_tables.read_table(hidden)
+        assert keys <= set(table), (hidden, sorted(keys - set(table)))
+
+
+def test_tables_hold_only_compiled_tiles():
+    for path in sorted(gemm_tables.TABLES.glob("tiles_hidden*.json")):
+        for key, cfg in json.loads(path.read_text()).items():
+            M, N, K = map(int, key.split(","))
+            assert set(cfg) == {"wave_frags", "k_waves", "split_k", "unroll"}, (path.name, key)
+            assert fast_gemm.tile_supported(M, K, cfg), (path.name, key, cfg)
+
+
+def test_load_table_missing_hidden_size_exits():
+    with pytest.raises(SystemExit, match="no tile table for hidden size 1536"):
+        gemm_tables.load_table(llama(1536, 4096, 12, 12), 42)
+
+
+def test_load_table_missing_shape_exits():
+    # hidden 1024 is tuned only at width 42.
+    with pytest.raises(SystemExit, match="no tuned tile"):
+        gemm_tables.load_table(llama(1024, 2560, 16, 4), 56)
+
+
+def test_load_table_wide_round_overrides_down():
+    cfg = llama(2048, 5632, 16, 4)
+    table = gemm_tables.load_table(cfg, 110)
+    assert table[(110, 2048, 5632)] == gemm_tables.DOWN_SPLIT_K1
+    narrow = gemm_tables.load_table(cfg, 56)
+    assert narrow[(56, 2048, 5632)] == gemm_tables.read_table(2048)[(56, 2048, 5632)]
+    assert len(table) == 5
+
+
+def test_fast_gemm_routes_only_eligible_calls(monkeypatch):
+    calls = []
+    monkeypatch.setattr(fast_gemm, "hip_linear", lambda a, w, cfg, out=None: calls.append(cfg) or "hip")
+    monkeypatch.setitem(fast_gemm.CONFIGS, (4, 16, 8), {"wave_frags": 1, "k_waves": 4, "split_k": 1, "unroll": 2})
+    x = torch.randn(4, 8).bfloat16()
+    w = torch.randn(16, 8).bfloat16()
+    assert fast_gemm.fast_gemm(None, x, w) == "hip"                      # tuned, eligible
+    assert torch.is_tensor(fast_gemm.fast_gemm(None, x, w, torch.zeros(16).bfloat16()))   # bias -> F.linear
+    assert torch.is_tensor(fast_gemm.fast_gemm(None, x.float(), w.float()))              # fp32 -> F.linear
+    assert torch.is_tensor(fast_gemm.fast_gemm(None, x[None], w))                          # 3-D -> F.linear
+    assert torch.is_tensor(fast_gemm.fast_gemm(None, torch.randn(5, 8).bfloat16(), w))    # untuned M
+    assert len(calls) == 1
+
+
+def test_install_rejects_uncompiled_tiles():
+    with pytest.raises(ValueError, match="no compiled MI355X kernel"):
+        fast_gemm.install({(56, 2048, 2048): {"wave_frags": 3, "k_waves": 8, "split_k": 1, "unroll": 8}})
+    assert (56, 2048, 2048) not in fast_gemm.CONFIGS
+
+
+def test_install_sets_the_dispatch_slot():
+    try:
+        fast_gemm.install({(42, 4096, 1024): tiles.heuristic_tile(42, 4096, 1024)})
+        assert fast_gemm.dispatch_unquantized_gemm() is fast_gemm.fast_gemm
+    finally:
+        fast_gemm.uninstall()
+    assert fast_gemm.dispatch_unquantized_gemm() is not fast_gemm.fast_gemm
+
+
+def test_workload_bytes_match_the_published_roofline_table():
+    assert workloads.SINGLE_GEMM.bytes == 8_818_688
+    assert workloads.BLOCK_1P3B.bytes == 104_333_312
+    assert workloads.ROUND_1P3B.bytes == 2_715_710_320
+    assert workloads.ROUND_3B.bytes == 5_443_196_784
+    for M, b in zip(workloads.M_SWEEP, (2_633_514_094, 2_645_256_412, 2_668_741_048, 2_692_225_684, 2_715_710_320)):
+        assert workloads.ROUND_1P3B.at(M).bytes == b

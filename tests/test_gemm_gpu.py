@@ -1,0 +1,236 @@
+"""GPU parity of the HIP skinny GEMM against the CPU oracle (the reference's own F.linear path).
+
+Tolerance: bf16/fp16 outputs within 1e-3 relative / 2e-2 absolute of the oracle, and within one
+output ulp of the fp32-accumulated product rounded once (a tighter, order-independent bound)."""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+import oracle
+from plm_amd import fast_gemm, gemm_tables, tiles, tune, workloads
+from plm_amd.fast_gemm import hip_linear, hip_linear_f32
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-3, 2e-2
+
+
+def _inputs(M, N, K, seed, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    w = (0.02 * torch.randn(N, K, generator=g)).to(dtype)
+    return x, w
+
+
+def _inputs_on_gpu(M, N, K, seed, device, dtype=torch.bfloat16):
+    """Large weights drawn directly on the GPU (seeded); the oracle reads a CPU copy of the rows it
+    checks, so both sides see the same bits."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    x = torch.randn(M, K, generator=g, device=device).to(dtype)
+    w = (0.02 * torch.randn(N, K, generator=g, device=device)).to(dtype)
+    return x, w
+
+
+def check_cols(y: torch.Tensor, x: torch.Tensor, w: torch.Tensor, cols: torch.Tensor):
+    """Columns ``cols`` of GPU ``y`` against the oracle on CPU copies of x and of those W rows."""
+    cols_d = cols.to(w.device)
+    got = y[:, cols_d].cpu().float()
+    xc, wc = x.cpu(), w[cols_d].cpu()
+    torch.testing.assert_close(got, oracle.linear(xc, wc).float(), rtol=RTOL, atol=ATOL)
+    exact = oracle.linear_fp32(xc, wc)
+    assert bool(((got - exact).abs() <= _ulp(exact, x.dtype) * 1.0001).all()), (got - exact).abs().max()
+
+
+def _ulp(v: torch.Tensor, dtype) -> torch.Tensor:
+    bits = 8 if dtype == torch.bfloat16 else 11
+    e = torch.floor(torch.log2(v.abs().clamp_min(2.0 ** -14)))
+    return 2.0 ** (e - (bits - 1))
+
+
+def check(y: torch.Tensor, x: torch.Tensor, w: torch.Tensor):
+    """GPU ``y`` against the oracle on the CPU operands x, w."""
+    wc = w
+    got = y.cpu().float()
+    ref = oracle.linear(x, wc).float()
+    torch.testing.assert_close(got, ref, rtol=RTOL, atol=ATOL)
+    exact = oracle.linear_fp32(x, wc)
+    assert bool(((got - exact).abs() <= _ulp(exact, x.dtype) * 1.0001).all()), (got - exact).abs().max()
+
+
+def _run(x, w, cfg, device):
+    return hip_linear(x.to(device), w.to(device), cfg)
+
+
+@pytest.mark.parametrize("which", ["table", "heuristic"])
+def test_single_gemm_350m_mlp_up(device, which):
+    M, N, K = 42, 4096, 1024
+    x, w = _inputs(M, N, K, 1)
+    cfg = gemm_tables.read_table(1024)[(M, N, K)] if which == "table" else tiles.heuristic_tile(M, N, K)
+    check(_run(x, w, cfg, device), x, w)
+
+
+@pytest.mark.parametrize("gemm", workloads.gpt_block(2048, 8192), ids=lambda g: g.name)
+def test_block_1p3b(device, gemm):
+    M = 56
+    x, w = _inputs(M, gemm.N, gemm.K, 2)
+    cfg = gemm_tables.read_table(2048)[(M, gemm.N, gemm.K)]
+    check(_run(x, w, cfg, device), x, w)
+
+
+@pytest.mark.parametrize("M", workloads.M_SWEEP)
+def test_lm_head_m_sweep(device, M):
+    N, K = workloads.GPT2_VOCAB, 2048
+    x, w = _inputs_on_gpu(M, N, K, 3, device)
+    cols = torch.cat([torch.arange(0, 96), torch.randperm(N, generator=torch.Generator().manual_seed(M))[:400],
+                      torch.arange(N - 81, N)])
+    check_cols(hip_linear(x, w, gemm_tables.read_table(2048)[(M, N, K)]), x, w, cols)
+
+
+@pytest.mark.parametrize("shape", [(56, 2048, 2048), (42, 4096, 1024), (56, 2048, 8192), (110, 2048, 2048)])
+def test_every_candidate_tile(device, shape):
+    M, N, K = shape
+    x, w = _inputs(M, N, K, 4)
+    xd, wd = x.to(device), w.to(device)
+    cands = tiles.candidates(M, N, K, lambda c: fast_gemm.tile_supported(M, K, c))
+    assert cands
+    for cfg in cands:
+        y = hip_linear(xd, wd, cfg)
+        check(y, x, w)
+
+
+@pytest.mark.parametrize("M", [1, 15, 16, 17, 33, 64, 65, 110, 128])
+def test_round_widths_edge_cases(device, M):
+    N, K = 1000, 1416   # N not a multiple of any tile; K a multiple of 8 but not of 32
+    x, w = _inputs(M, N, K, 5)
+    supported = lambda c: fast_gemm.tile_supported(M, K, c)  # noqa: E731
+    for cfg in (tiles.heuristic_tile(M, N, K, supported=supported),
+                {"wave_frags": 1, "k_waves": 4, "split_k": 3, "unroll": 2}):
+        if supported(cfg):
+            check(_run(x, w, cfg, device), x, w)
+
+
+def test_split_k_is_deterministic_and_consistent(device):
+    M, N, K = 56, 2048, 8192
+    x, w = _inputs(M, N, K, 6)
+    xd, wd = x.to(device), w.to(device)
+    split = {"wave_frags": 2, "k_waves": 8, "split_k": 8, "unroll": 4}
+    a = hip_linear_f32(xd, wd, split)
+    b = hip_linear_f32(xd, wd, split)
+    assert torch.equal(a, b)
+    single = hip_linear_f32(xd, wd, {"wave_frags": 2, "k_waves": 8, "split_k": 1, "unroll": 4})
+    torch.testing.assert_close(a, single, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(a.cpu(), oracle.linear_fp32(x, w), rtol=1e-4, atol=1e-4)
+
+
+def test_fp16(device):
+    M, N, K = 56, 3072, 2048
+    x, w = _inputs(M, N, K, 7, torch.float16)
+    for cfg in ({"wave_frags": 2, "k_waves": 8, "split_k": 2, "unroll": 4},
+                {"wave_frags": 4, "k_waves": 4, "split_k": 1, "unroll": 4}):
+        check(_run(x, w, cfg, device), x, w)
+
+
+def test_small_integers_are_exact(device):
+    M, N, K = 56, 512, 2048
+    g = torch.Generator().manual_seed(8)
+    x = torch.randint(-2, 3, (M, K), generator=g).bfloat16()
+    w = torch.randint(-1, 2, (N, K), generator=g).bfloat16()
+    exact = oracle.linear_fp64(x, w)
+    assert abs(exact).max() < 256
+    for cfg in ({"wave_frags": 2, "k_waves": 8, "split_k": 1, "unroll": 8},
+                {"wave_frags": 1, "k_waves": 4, "split_k": 4, "unroll": 4}):
+        y = _run(x, w, cfg, device).cpu().double().numpy()
+        assert (y == exact).all()
+
+
+def test_one_hot_weight_selects_columns(device):
+    M, K = 42, 1024
+    x, _ = _inputs(M, 1, K, 9)
+    cols = torch.tensor([0, 5, 1023, 512, 77, 31, 32, 999])
+    w = torch.zeros(len(cols), K).bfloat16()
+    w[torch.arange(len(cols)), cols] = 1.0
+    y = _run(x, w, {"wave_frags": 1, "k_waves": 4, "split_k": 1, "unroll": 8}, device)
+    assert torch.equal(y.cpu(), x[:, cols])
+
+
+def test_strided_activation_view(device):
+    # X as the first K columns of a wider buffer (ldx > K), as when a QKV output feeds the next GEMM.
+    M, N, K = 56, 2048, 2048
+    g = torch.Generator().manual_seed(10)
+    wide = torch.randn(M, 3 * K, generator=g).bfloat16()
+    w = (0.02 * torch.randn(N, K, generator=g)).bfloat16()
+    xd = wide.to(device)[:, :K]
+    assert xd.stride(0) == 3 * K
+    y = hip_linear(xd, w.to(device), gemm_tables.read_table(2048)[(M, N, K)])
+    check(y, wide[:, :K].contiguous(), w)
+
+
+def test_fast_gemm_install_routes_table_shapes(device):
+    from types import SimpleNamespace
+
+    cfg = SimpleNamespace(hidden_size=2048, intermediate_size=5632, head_dim=128, num_attention_heads=16,
+                          num_key_value_heads=4, vocab_size=50257)
+    try:
+        gemm_tables.install(cfg, 56)
+        gemm = fast_gemm.dispatch_unquantized_gemm()
+        for (M, N, K) in gemm_tables.load_table(cfg, 56):
+            x, w = _inputs_on_gpu(M, N, K, 11, device)
+            cols = torch.cat([torch.arange(0, min(N, 320)), torch.arange(N - 64, N)])
+            check_cols(gemm(None, x, w), x, w, cols)
+        x, w = _inputs(57, 64, 2048, 12)     # untuned width: F.linear on the GPU
+        torch.testing.assert_close(gemm(None, x.to(device), w.to(device)).cpu().float(),
+                                   oracle.linear(x, w).float(), rtol=RTOL, atol=ATOL)
+    finally:
+        fast_gemm.uninstall()
+
+
+@pytest.mark.parametrize("hidden", tune.all_hidden())
+def test_every_table_entry(device, hidden):
+    table = gemm_tables.read_table(hidden)
+    for (M, N, K), cfg in table.items():
+        x, w = _inputs_on_gpu(M, N, K, 13, device)
+        cols = torch.cat([torch.arange(0, min(N, 160)), torch.arange(max(0, N - 70), N)]).unique()
+        check_cols(hip_linear(x, w, cfg), x, w, cols)
+
+
+def test_graph_capture_and_replay(device):
+    shapes = [(56, 2048, 8192), (56, 6144, 2048), (56, 2048, 2048)]
+    table = gemm_tables.read_table(2048)
+    data = [_inputs(*s, 14 + i) for i, s in enumerate(shapes)]
+    dev = [(x.to(device), w.to(device)) for x, w in data]
+    outs = [torch.empty(s[0], s[1], device=device, dtype=torch.bfloat16) for s in shapes]
+    cfgs = [table[s] for s in shapes]
+    for (x, w), o, c in zip(dev, outs, cfgs):
+        hip_linear(x, w, c, o)                        # eager: sizes the workspace
+    eager = [o.clone() for o in outs]
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for (x, w), o, c in zip(dev, outs, cfgs):
+            hip_linear(x, w, c, o)
+    for rep in range(4):
+        for o in outs:
+            o.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e), rep
+        hip_linear(dev[0][0], dev[0][1], cfgs[0], outs[0])   # eager work between replays
+        torch.cuda.synchronize()
+    check(outs[1], *data[1])
+
+
+def test_wide_workgroup_count_stays_in_bounds(device):
+    # Many tiles (N = 50304 at 16-row tiles) and the largest split: every workgroup index maps to a
+    # real tile and split slot.
+    M, N, K = 42, 50304, 1024
+    x, w = _inputs_on_gpu(M, N, K, 15, device)
+    cfg = {"wave_frags": 1, "k_waves": 4, "split_k": 2, "unroll": 4}
+    assert math.ceil(N / 16) * 2 > 4096
+    cols = torch.cat([torch.arange(0, 64), torch.arange(N - 64, N)])
+    check_cols(hip_linear(x, w, cfg), x, w, cols)

@@ -1,0 +1,168 @@
+"""GPU parity of the fused LM-head verify step (nucleus membership + argmax, no logits written).
+
+Two checks per case:
+* bit-exact decisions: the kernel's accept bits and argmax ids equal the oracle's
+  (nucleus_acceptance / argmax, plm/decoder.py:71-75, 362) evaluated on the kernel's own logits
+  (the same tile's fp32 accumulator from ``hip_linear_f32``, rounded per mode);
+* end to end: those logits match the CPU fp32 product within 1e-3 relative, and the decisions
+  match the oracle on CPU logits wherever the row is not within rounding of a decision boundary."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle
+from oracle import plm_oracle as po
+from plm_amd import fast_gemm, workloads
+from plm_amd.fast_gemm import hip_linear_f32
+from plm_amd.verify import VERIFY_CONFIG, lm_head_verify
+
+pytestmark = pytest.mark.gpu
+
+P = workloads.TOP_P
+
+
+def _rounded(logits: torch.Tensor, mode: str) -> torch.Tensor:
+    if mode == "bf16":
+        return logits.bfloat16().float()
+    if mode == "fp16":
+        return logits.half().float()
+    return logits
+
+
+def _own_logits_from_workspace(R: int, device) -> torch.Tensor:
+    """The own-logit pass's fp32 outputs, read back from the workspace (bytes 256 .. 256 + 4R)."""
+    ws = fast_gemm._workspaces[device.index if device.index is not None else 0]
+    return ws[256:256 + 4 * R].view(torch.float32).cpu()
+
+
+def run_case(x, w, pending, p, mode, device, cfg=None, check_cpu=True):
+    acc, am = lm_head_verify(x, w, pending, p, mode, cfg)
+    acc, am = acc.cpu(), am.cpu()
+    logits = _rounded(hip_linear_f32(x, w, cfg or VERIFY_CONFIG).cpu(), mode)
+    # The own-logit pass reproduces the main pass's value for each proposal bit for bit.
+    own = _own_logits_from_workspace(x.shape[0], device)
+    valid = (pending.cpu() >= 0) & (pending.cpu() < w.shape[0])
+    rows = torch.arange(x.shape[0])[valid]
+    assert torch.equal(own[rows], logits[rows, pending.cpu()[rows]])
+    # Bit-exact decisions on the kernel's own logits.
+    ref_acc = torch.zeros_like(acc)
+    if rows.numel():
+        ref_acc[rows] = oracle.nucleus_acceptance(logits[rows], pending.cpu()[rows], p)
+    assert torch.equal(am, oracle.argmax(logits)), (am != oracle.argmax(logits)).nonzero()
+    assert torch.equal(acc, ref_acc), (acc != ref_acc).nonzero()
+    if check_cpu:
+        cpu = oracle.linear_fp32(x.cpu(), w.cpu())
+        torch.testing.assert_close(hip_linear_f32(x, w, cfg or VERIFY_CONFIG).cpu(), cpu, rtol=1e-3, atol=1e-4)
+    return acc, am, logits
+
+
+def _config5(device, dtype=torch.bfloat16, R=56, V=workloads.GPT2_VOCAB, K=2048):
+    g = torch.Generator(device=device).manual_seed(5000)
+    x = torch.randn(R, K, generator=g, device=device).to(dtype)
+    w = (0.02 * torch.randn(V, K, generator=g, device=device)).to(dtype)
+    pending = workloads.proposals(R, V).to(device)
+    return x, w, pending
+
+
+@pytest.mark.parametrize("mode", ["fp32", "bf16"])
+def test_config5_fused_verify(device, mode):
+    x, w, pending = _config5(device)
+    acc, am, logits = run_case(x, w, pending, P, mode, device)
+    # Against the oracle on CPU-computed logits, away from rounding-sensitive rows.
+    cpu_logits = _rounded(oracle.linear_fp32(x.cpu(), w.cpu()), mode)
+    ref_acc, ref_am = oracle.verify(cpu_logits, pending.cpu(), P)
+    margin = po.nucleus_margin(cpu_logits, pending.cpu(), P)
+    top2 = cpu_logits.topk(2, dim=-1).values
+    gap = (top2[:, 0] - top2[:, 1]).numpy()
+    safe_acc = torch.from_numpy(margin > 1e-4)
+    safe_am = torch.from_numpy(gap > 1e-3)
+    assert safe_acc.sum() >= 50 and safe_am.sum() >= 50
+    assert torch.equal(acc[safe_acc], ref_acc[safe_acc])
+    assert torch.equal(am[safe_am], ref_am[safe_am])
+    assert 0 < int(acc.sum()) < 56
+
+
+def test_fp16_model_dtype(device):
+    x, w, pending = _config5(device, torch.float16, R=42, V=8000)
+    run_case(x, w, pending, P, "fp16", device)
+
+
+@pytest.mark.parametrize("R", [1, 7, 14, 28, 42, 64])
+def test_round_widths(device, R):
+    x, w, pending = _config5(device, R=R, V=5003)
+    run_case(x, w, pending, P, "fp32", device)
+
+
+@pytest.mark.parametrize("cfg", [{"wave_frags": 2, "k_waves": 8, "split_k": 1, "unroll": 2},
+                                 {"wave_frags": 4, "k_waves": 4, "split_k": 1, "unroll": 4},
+                                 {"wave_frags": 2, "k_waves": 4, "split_k": 1, "unroll": 8}])
+def test_other_tiles(device, cfg):
+    x, w, pending = _config5(device, R=56, V=12345, K=1024)
+    run_case(x, w, pending, 0.5, "fp32", device, cfg)
+
+
+def test_proposals_at_the_argmax_and_exact_mode(device):
+    x, w, _ = _config5(device, R=56, V=9000)
+    am0 = oracle.argmax(hip_linear_f32(x, w, VERIFY_CONFIG).cpu()).to(device)
+    acc, am, _ = run_case(x, w, am0, P, "fp32", device)
+    assert bool(acc.all())                       # the maximum is always inside the nucleus
+    acc0, _, _ = run_case(x, w, am0, 0.0, "fp32", device)
+    assert not bool(acc0.any())                  # p <= 0 accepts nothing (exact matching)
+    accn, _, _ = run_case(x, w, am0, -1.0, "fp32", device)
+    assert not bool(accn.any())
+
+
+def test_uniform_rows_and_ties(device):
+    R, V, K = 16, 3000, 256
+    x = torch.randn(R, K, device=device).bfloat16()
+    w = torch.zeros(V, K, device=device).bfloat16()
+    pending = torch.randint(0, V, (R,), device=device)
+    acc, am, _ = run_case(x, w, pending, 0.01, "fp32", device)
+    assert bool(acc.all()) and bool((am == 0).all())   # all logits 0: no mass above, argmax index 0
+    # Duplicate the best row further down the vocabulary: the tie resolves to the lower index.
+    w = (0.05 * torch.randn(V, K, device=device)).bfloat16()
+    logits = hip_linear_f32(x, w, VERIFY_CONFIG).cpu()
+    best = logits.argmax(-1)
+    for r in range(R):
+        w[V - 1 - r] = w[int(best[r])]
+    _, am2, logits2 = run_case(x, w, pending, 0.5, "fp32", device)
+    assert torch.equal(am2, oracle.argmax(logits2))
+
+
+def test_pending_outside_vocabulary_is_rejected(device):
+    x, w, pending = _config5(device, R=8, V=4000)
+    am_ids = oracle.argmax(hip_linear_f32(x, w, VERIFY_CONFIG).cpu())
+    pending = am_ids.clone().to(device)
+    pending[1] = -1
+    pending[5] = 4000
+    acc, _, _ = run_case(x, w, pending, P, "fp32", device)
+    assert acc.tolist() == [True, False, True, True, True, False, True, True]
+
+
+def test_deterministic(device):
+    x, w, pending = _config5(device)
+    a1, m1 = lm_head_verify(x, w, pending, P)
+    a2, m2 = lm_head_verify(x, w, pending, P)
+    assert torch.equal(a1, a2) and torch.equal(m1, m2)
+
+
+def test_graph_capture(device):
+    x, w, pending = _config5(device)
+    eager_acc, eager_am = lm_head_verify(x, w, pending, P)
+    acc = torch.zeros(56, dtype=torch.bool, device=device)
+    am = torch.zeros(56, dtype=torch.int64, device=device)
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        lm_head_verify(x, w, pending, P, accept=acc, argmax=am)
+    for _ in range(3):
+        acc.zero_()
+        am.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(acc, eager_acc) and torch.equal(am, eager_am)
+        lm_head_verify(x, w, pending, P)
+        torch.cuda.synchronize()
