@@ -28,6 +28,12 @@ enum plm_dtype { PLM_BF16 = 0, PLM_F16 = 1 };
  * accumulator, plm/decoder.py:73 upcasts it again). */
 enum plm_round_mode { PLM_ROUND_F32 = 0, PLM_ROUND_BF16 = 1, PLM_ROUND_F16 = 2 };
 
+/* Every workspace starts with this many bytes of integer arrival counters, which must be zero
+ * before the first call and which every kernel leaves zero; the rest of a workspace is scratch
+ * that needs no initialisation. One workspace may therefore serve every entry point in turn on
+ * one stream (calls that overlap on different streams need separate workspaces). */
+#define PLM_WORKSPACE_COUNTER_BYTES (1u << 18)
+
 enum plm_status {
   PLM_OK = 0,
   PLM_ERR_ARGUMENT = -1,      /* bad size, stride, dtype or null pointer */
@@ -59,7 +65,7 @@ typedef struct plm_tile {
  * Replaces triton_linear (plm/fast_gemm.py:82-97) together with gemm_kernel (17-48) and
  * splitk_reduce_kernel (51-61). Requirements: 1 <= M <= 128, K % 8 == 0, ldx/ldw % 8 == 0,
  * x and w 16-byte aligned. `workspace` may be NULL when plm_gemm_workspace_bytes() is 0;
- * otherwise it must be zero-filled before its first use and is left zeroed for the next call.
+ * otherwise its counter area must be zero before its first use (it is left zero).
  */
 int plm_gemm(int32_t dtype, const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
              int64_t M, int64_t N, int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes,
@@ -75,7 +81,8 @@ int plm_gemm_f32out(int32_t dtype, const void* x, int64_t ldx, const void* w, in
                     void* stream);
 
 /* Workspace bytes plm_gemm needs for this shape and tile (the reference's _partial_buffer,
- * plm/fast_gemm.py:70-79). 0 when split_k == 1. */
+ * plm/fast_gemm.py:70-79): PLM_WORKSPACE_COUNTER_BYTES plus the fp32 split partials. 0 when
+ * split_k == 1. */
 size_t plm_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, const plm_tile* tile);
 
 /* 1 when a kernel is compiled for this tile at this M and K, else 0. */
@@ -95,7 +102,7 @@ int plm_lm_head_verify(int32_t dtype, const void* x, int64_t ldx, const void* w,
                        int64_t K, const int64_t* pending, float p, int32_t round_mode, uint8_t* accept,
                        int64_t* argmax, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream);
 
-/* Workspace bytes plm_lm_head_verify needs. Zero-filled before first use; left zeroed. */
+/* Workspace bytes plm_lm_head_verify needs (counter area first, as for plm_gemm). */
 size_t plm_lm_head_verify_workspace_bytes(int64_t R, int64_t V, int64_t K, const plm_tile* tile);
 
 /* Human-readable name of a status code. */

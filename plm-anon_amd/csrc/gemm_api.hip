@@ -20,10 +20,7 @@ extern "C" {
 size_t plm_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, const plm_tile* tile) {
   (void)K;
   if (tile == nullptr || tile->split_k <= 1 || tile->wave_frags <= 0 || M <= 0 || N <= 0) return 0;
-  const int64_t tn = 16 * static_cast<int64_t>(tile->wave_frags);
-  const int64_t n_tiles = (N + tn - 1) / tn;
-  const size_t counters = static_cast<size_t>((n_tiles * 4 + 255) / 256 * 256);
-  return counters + static_cast<size_t>(tile->split_k) * M * N * sizeof(float);
+  return plm::kCounterBytes + static_cast<size_t>(tile->split_k) * M * N * sizeof(float);
 }
 
 int plm_gemm_tile_supported(int32_t dtype, int64_t M, int64_t K, const plm_tile* tile) {
@@ -52,6 +49,8 @@ int gemm_entry(int32_t dtype, const void* x, int64_t ldx, const void* w, int64_t
   if (!plm_gemm_tile_supported(dtype, M, K, tile)) return PLM_ERR_TILE;
   const size_t need = plm_gemm_workspace_bytes(M, N, K, tile);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need || !plm::aligned16_ptr(workspace))) return PLM_ERR_WORKSPACE;
+  // One arrival counter per weight tile when K is split across workgroups.
+  if (need > 0 && (N + 16 * tile->wave_frags - 1) / (16 * tile->wave_frags) > plm::kMaxCounters) return PLM_ERR_ARGUMENT;
 
   plm::GemmArgs a{};
   a.x = static_cast<const uint16_t*>(x);
@@ -66,10 +65,8 @@ int gemm_entry(int32_t dtype, const void* x, int64_t ldx, const void* w, int64_t
   a.split = tile->split_k;
   a.out_f32 = out_f32;
   if (need > 0) {
-    const int64_t tn = 16 * static_cast<int64_t>(tile->wave_frags);
-    const size_t counters = static_cast<size_t>((((N + tn - 1) / tn) * 4 + 255) / 256 * 256);
     a.counter = static_cast<int*>(workspace);
-    a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + counters);
+    a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + plm::kCounterBytes);
   }
   const hipError_t err = plm::dispatch(dtype, a, *tile, static_cast<hipStream_t>(stream), false);
   return err == hipSuccess ? PLM_OK : PLM_ERR_LAUNCH;

@@ -9,7 +9,7 @@
 //   * wavefront  = one of KW contiguous K slices of that range; it streams its slice of the
 //                  weight tile from HBM with 16-byte loads straight into MFMA operands;
 //   * LDS        = the KW wavefront partials, summed in wave order;
-//   * split > 1  = each workgroup writes an fp32 partial, the last one of the tile to arrive
+//   * split > 1  = each workgroup publishes an fp32 partial, the last one of the tile to arrive
 //                  (integer counter) sums the partials in split order and writes Y. The sum
 //                  order is fixed, so results are bitwise reproducible run to run, as in the
 //                  reference's two-kernel split-K (plm/fast_gemm.py:3-4, 48, 51-61).
@@ -44,7 +44,6 @@ __device__ __forceinline__ void store_y(const GemmArgs& a, int64_t idx, float v)
 template <int DT, int MT, int NF, int U, bool PIPE, int KW>
 __global__ __launch_bounds__(64 * KW) void skinny_gemm_kernel(GemmArgs a) {
   extern __shared__ float red[];
-  __shared__ int last_arrival;
   constexpr int TN = 16 * NF;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -83,24 +82,18 @@ __global__ __launch_bounds__(64 * KW) void skinny_gemm_kernel(GemmArgs a) {
   float* part = a.partial + s * plane;
   for (int e = threadIdx.x; e < elems; e += 64 * KW) {
     const int m = e / TN, nl = e - m * TN;
-    if (nl < tn) part[static_cast<int64_t>(m) * a.N + n0 + nl] = wg_sum<MT, NF>(red, KW, red_offset<MT, NF>(nl, m));
+    if (nl < tn) publish(part + static_cast<int64_t>(m) * a.N + n0 + nl, wg_sum<MT, NF>(red, KW, red_offset<MT, NF>(nl, m)));
   }
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) last_arrival = (atomicAdd(&a.counter[tile], 1) == a.split - 1);
-  __syncthreads();
-  if (!last_arrival) return;
-  __threadfence();
+  if (!arrive_last(a.counter + tile, a.split)) return;
   for (int e = threadIdx.x; e < elems; e += 64 * KW) {
     const int m = e / TN, nl = e - m * TN;
     if (nl < tn) {
       const int64_t idx = static_cast<int64_t>(m) * a.N + n0 + nl;
-      float v = a.partial[idx];
-      for (int q = 1; q < a.split; ++q) v += a.partial[q * plane + idx];
+      float v = collect(a.partial + idx);
+      for (int q = 1; q < a.split; ++q) v += collect(a.partial + q * plane + idx);
       store_y<DT>(a, m * a.ldy + n0 + nl, v);
     }
   }
-  if (threadIdx.x == 0) a.counter[tile] = 0;
 }
 
 // The compiled tile set. MT = ceil(M/16) is picked from M at run time; PIPE is picked from the

@@ -17,6 +17,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "plm_amd.h"
+
 namespace plm {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -66,7 +68,43 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0));
 }
 
+// Workspace layout common to every entry point: the counter area (zero between calls), then scratch.
+constexpr size_t kCounterBytes = PLM_WORKSPACE_COUNTER_BYTES;
+constexpr int64_t kMaxCounters = static_cast<int64_t>(kCounterBytes / sizeof(int));
+
 inline bool aligned16_ptr(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Cross-workgroup hand-off (split-K partials, per-workgroup row states) without cache-wide
+// maintenance. The MI355X has one L2 per XCD and they are not coherent with each other for
+// ordinary accesses, which is why __threadfence() costs a full L2 writeback + invalidate in every
+// wavefront. Instead the producer writes with device-coherent stores (written through its L2),
+// waits for them to complete, and only then counts itself in with a device-scope atomic; the
+// consumer reads with device-coherent loads, which never return a stale L2 line.
+template <typename T>
+__device__ __forceinline__ void publish(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename T>
+__device__ __forceinline__ T collect(const T* p) {
+  return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Called by every thread of the workgroup after its publish() calls. Returns true in the
+// workgroup that arrives last out of `expected`; that workgroup also resets the counter to zero
+// for the next launch.
+__device__ __forceinline__ bool arrive_last(int* counter, int expected) {
+  __shared__ int last;
+  __builtin_amdgcn_s_waitcnt(0);  // this wavefront's published stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = before == expected - 1;
+    if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  return last != 0;
+}
 
 // Half-open K-step range [st0, st1) of slice `piece` out of `pieces`, over ceil(K/32) steps.
 __device__ __forceinline__ void k_slice(int K, int piece, int pieces, int& st0, int& st1) {

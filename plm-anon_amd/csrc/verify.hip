@@ -116,7 +116,6 @@ __global__ __launch_bounds__(64 * KW) void own_logit_kernel(VerifyArgs a) {
 template <int DT, int MT, int NF, int U, bool PIPE, int KW>
 __global__ __launch_bounds__(64 * KW) void verify_main_kernel(VerifyArgs a) {
   extern __shared__ float red[];
-  __shared__ int last_arrival;
   constexpr int TN = 16 * NF;
   static_assert(TN <= 64, "one lane per tile column");
   constexpr int RPW = (16 * MT + KW - 1) / KW;  // rows of X per wavefront in the epilogue
@@ -194,19 +193,14 @@ __global__ __launch_bounds__(64 * KW) void verify_main_kernel(VerifyArgs a) {
       const int m = wave + KW * j;
       if (m < a.R) {
         const int64_t slot = static_cast<int64_t>(blockIdx.x) * a.R + m;
-        a.state[slot * 3 + 0] = rs[j].mx;
-        a.state[slot * 3 + 1] = rs[j].se;
-        a.state[slot * 3 + 2] = rs[j].ab;
-        a.state_idx[slot] = rs[j].ai;
+        publish(a.state + slot * 3 + 0, rs[j].mx);
+        publish(a.state + slot * 3 + 1, rs[j].se);
+        publish(a.state + slot * 3 + 2, rs[j].ab);
+        publish(a.state_idx + slot, rs[j].ai);
       }
     }
   }
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) last_arrival = (atomicAdd(a.counter, 1) == a.G - 1);
-  __syncthreads();
-  if (!last_arrival) return;
-  __threadfence();
+  if (!arrive_last(a.counter, a.G)) return;
 
   // Last workgroup: merge the G states of every row (lane-strided, then a butterfly).
   for (int j = 0; j < RPW; ++j) {
@@ -215,7 +209,8 @@ __global__ __launch_bounds__(64 * KW) void verify_main_kernel(VerifyArgs a) {
     RowState s = empty_state();
     for (int g = lane; g < a.G; g += 64) {
       const int64_t slot = static_cast<int64_t>(g) * a.R + m;
-      s = merge(s, RowState{a.state[slot * 3 + 0], a.state[slot * 3 + 1], a.state[slot * 3 + 2], a.state_idx[slot]});
+      s = merge(s, RowState{collect(a.state + slot * 3 + 0), collect(a.state + slot * 3 + 1),
+                            collect(a.state + slot * 3 + 2), collect(a.state_idx + slot)});
     }
     s = wave_merge(s);
     if (lane == 0) {
@@ -227,7 +222,6 @@ __global__ __launch_bounds__(64 * KW) void verify_main_kernel(VerifyArgs a) {
       a.argmax[m] = s.ai;
     }
   }
-  if (threadIdx.x == 0) *a.counter = 0;
 }
 
 template <int MT, int NF, int U, bool PIPE, int KW>
@@ -315,9 +309,10 @@ hipError_t verify_dispatch(const VerifyArgs& a, const plm_tile& t, int cu, hipSt
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
-// Workspace layout: counter | own[R] | state[kMaxVerifyGroups][R][3] | state_idx[kMaxVerifyGroups][R]
+// Workspace layout: counter area (counter 0 used) | own[R] | state[kMaxVerifyGroups][R][3] |
+// state_idx[kMaxVerifyGroups][R]
 void verify_layout(int64_t R, size_t& own_off, size_t& state_off, size_t& idx_off, size_t& total) {
-  own_off = 256;
+  own_off = kCounterBytes;
   state_off = own_off + align256(static_cast<size_t>(R) * sizeof(float));
   idx_off = state_off + align256(static_cast<size_t>(kMaxVerifyGroups) * R * 3 * sizeof(float));
   total = idx_off + align256(static_cast<size_t>(kMaxVerifyGroups) * R * sizeof(int));

@@ -69,9 +69,11 @@ def test_argument_validation_happens_before_launch():
 
 def test_workspace_sizes():
     lib = _lib.lib()
+    m = re.search(r"#define PLM_WORKSPACE_COUNTER_BYTES \(1u << (\d+)\)", HEADER.read_text())
+    assert m and _lib.COUNTER_BYTES == 1 << int(m.group(1))
     assert lib.plm_gemm_workspace_bytes(56, 2048, 8192, _lib.Tile(2, 8, 1, 4)) == 0
     n = lib.plm_gemm_workspace_bytes(56, 2048, 8192, _lib.Tile(2, 8, 4, 4))
-    assert n >= 4 * 56 * 2048 * 4 + 64 * 4
+    assert n == _lib.COUNTER_BYTES + 4 * 56 * 2048 * 4
     assert lib.plm_lm_head_verify_workspace_bytes(56, 50257, 2048, _lib.Tile(2, 4, 1, 4)) > 56 * 4
 
 

@@ -14,7 +14,7 @@ import torch
 
 import oracle
 from oracle import plm_oracle as po
-from plm_amd import fast_gemm, workloads
+from plm_amd import _lib, fast_gemm, workloads
 from plm_amd.fast_gemm import hip_linear_f32
 from plm_amd.verify import VERIFY_CONFIG, lm_head_verify
 
@@ -32,9 +32,10 @@ def _rounded(logits: torch.Tensor, mode: str) -> torch.Tensor:
 
 
 def _own_logits_from_workspace(R: int, device) -> torch.Tensor:
-    """The own-logit pass's fp32 outputs, read back from the workspace (bytes 256 .. 256 + 4R)."""
+    """The own-logit pass's fp32 outputs, read back from the workspace (right after the counter area)."""
     ws = fast_gemm._workspaces[device.index if device.index is not None else 0]
-    return ws[256:256 + 4 * R].view(torch.float32).cpu()
+    base = _lib.COUNTER_BYTES
+    return ws[base:base + 4 * R].view(torch.float32).cpu()
 
 
 def run_case(x, w, pending, p, mode, device, cfg=None, check_cpu=True):
