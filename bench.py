@@ -2,12 +2,14 @@
 
 A step is one full 1.3B-shape round at k=7 (M = 56 rows): 24 GPT-style blocks (QKV 2048->6144,
 attention-out 2048->2048, MLP up 2048->8192, MLP down 8192->2048) plus the LM head 2048->50257,
-i.e. 97 GEMM launches through ``fast_gemm``'s kernel, chained output-to-input as in the model, with
-random-init bf16 weights (~N(0, 0.02^2)) resident in HBM. The round is recorded once as a HIP
-graph and replayed (the reference replays its round as a CUDA graph, plm/decoder.py:414-447).
+97 linears chained output-to-input as in the model, with random-init bf16 weights
+(~N(0, 0.02^2)) resident in HBM. The round is recorded once as a HIP graph and replayed (the
+reference replays its round as a CUDA graph, plm/decoder.py:414-447), two ways:
+  * the headline: all 97 linears in one chained launch of the streaming kernel (plm_gemm_chain);
+  * the per-GEMM drop-in path: 97 fast_gemm launches (plm_gemm), reported beside it.
 
 Prints one JSON line: ``value`` is microseconds per round (lower is better), plus the round's HBM
-GB/s and fraction of the 8 TB/s peak, the dominant kernel's roofline from HIP-event timing, the
+GB/s and fraction of the 8 TB/s peak, the kernel roofline from HIP-event timing, the
 partial-round M sweep, the fused LM-head verify step, and the torch-CPU baseline of the same
 linears timed on this host.
 """
@@ -43,6 +45,10 @@ def parse_args():
     ap.add_argument("--no-sweep", action="store_true", help="skip the partial-round M sweep")
     ap.add_argument("--no-verify", action="store_true", help="skip the fused LM-head verify timing")
     ap.add_argument("--only-round", action="store_true", help="time the round only (for profiling runs)")
+    ap.add_argument("--profile", choices=("eager", "copy"),
+                    help="no JSON: 'eager' launches the round and the fused verify step --steps times without a "
+                         "graph (for rocprofv3 counter runs); 'copy' runs a 1 GiB device copy, the reference "
+                         "kernel that scales the HBM byte counters")
     return ap.parse_args()
 
 
@@ -108,15 +114,13 @@ def time_graph(graph, steps, warmup):
 
 
 def kernel_class(M, K, cfg):
-    """The compiled kernel a GEMM launches: (MT, wave_frags, unroll, pipelined, k_waves)."""
-    steps = math.ceil(K / 32)
-    spw = math.ceil(steps / (cfg["split_k"] * cfg["k_waves"]))
-    return (math.ceil(M / 16), cfg["wave_frags"], cfg["unroll"], spw > cfg["unroll"], cfg["k_waves"])
+    """The compiled kernel a GEMM launches: (MT, wave_frags, unroll)."""
+    return (math.ceil(M / 16), cfg["wave_frags"], cfg["unroll"])
 
 
 def kernel_name(cls):
-    mt, nf, u, pipe, kw = cls
-    return f"skinny_gemm_kernel<bf16, MT={mt}, NF={nf}, U={u}, PIPE={int(pipe)}, KW={kw}>"
+    mt, nf, u = cls
+    return f"stream_gemm_kernel<bf16, MT={mt}, NF={nf}, U={u}>"
 
 
 def dominant_kernel_roofline(rnd, steps):
@@ -189,6 +193,29 @@ def cpu_baseline(hidden, mlp, M, budget_s):
                       f"LM head at M={M}; round = 24 x block + LM head; CPU {cpu_model}"}
 
 
+def capture_graph(fn):
+    """A HIP graph of ``fn()`` recorded on a side stream after one eager call."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        fn()
+    return graph
+
+
+def round_chain(rnd):
+    """The round's 97 linears as one chained launch (plm_gemm_chain), output-to-input."""
+    from plm_amd.chain import Link, LinearChain
+    from plm_amd.tiles import CHAIN_TILE, chain_split
+
+    links = [Link(x, w, y, i - 1, chain_split(g.N, g.K))
+             for i, (g, x, w, y) in enumerate(zip(rnd.gemms, rnd.inputs, rnd.weights, rnd.outs))]
+    return LinearChain(links, CHAIN_TILE)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -199,10 +226,19 @@ def main():
 
     from plm_amd import gemm_tables
     from plm_amd.fast_gemm import hip_linear  # noqa: F401  (fails loudly if the library is missing)
+    from plm_amd.tiles import CHAIN_TILE
     from plm_amd.workloads import GPT2_VOCAB, gpt_block
 
     torch.cuda.set_device(0)
     device = torch.device("cuda", 0)
+    if args.profile == "copy":
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=device).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(max(1, args.steps)):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"[bench] copied 1 GiB x {max(1, args.steps)}", file=sys.stderr)
+        return
     tables = gemm_tables.read_table(args.hidden)
     gemms = [g for _ in range(args.layers) for g in gpt_block(args.hidden, args.mlp)]
     gemms.append(type(gemms[0])("lm_head", GPT2_VOCAB, args.hidden))
@@ -215,11 +251,49 @@ def main():
           flush=True)
 
     rnd = Round(args.M, args.hidden, args.mlp, args.layers, weights, tables, device)
-    graph = rnd.capture()
+    chain = round_chain(rnd)
+    if args.profile == "eager":
+        from plm_amd.verify import lm_head_verify
+        from plm_amd.workloads import TOP_P, proposals
+
+        pending = proposals(args.M).to(device)
+        for _ in range(max(1, args.steps)):
+            chain.run()
+            rnd.launch()
+            lm_head_verify(rnd.inputs[-1], weights[-1], pending, TOP_P)
+        torch.cuda.synchronize()
+        print(f"[bench] eager chained round + per-GEMM round + verify x {max(1, args.steps)}", file=sys.stderr)
+        return
+
+    # Headline: the round's linears as one chained launch, replayed as a HIP graph.
+    graph = capture_graph(chain.run)
     ms = time_graph(graph, args.steps, args.warmup)
+    if chain.error_flag():
+        print("[bench] chained launch reported a timed-out wait: results invalid", file=sys.stderr)
+        sys.exit(1)
+    chain_outs = [o.clone() for o in rnd.outs]
+    del graph
+    # The chained launch computes what the single-linear kernel does with the same tiles, bit for
+    # bit, through all 97 linears.
+    for i, ln in enumerate(chain.links):
+        hip_linear(ln.x, ln.w, dict(chain.cfg, split_k=ln.split_k), rnd.outs[i])
+    torch.cuda.synchronize()
+    mismatched = [i for i, (a, b) in enumerate(zip(chain_outs, rnd.outs)) if not torch.equal(a, b)]
+    if mismatched:
+        print(f"[bench] chained round differs from per-linear launches at linears {mismatched[:8]}", file=sys.stderr)
+        sys.exit(1)
     us_round = ms * 1000.0
     gbps = rnd.bytes / (us_round * 1e-6) / 1e9
-    print(f"[bench] round: {us_round:.1f} us, {gbps:.0f} GB/s", file=sys.stderr, flush=True)
+    print(f"[bench] chained round: {us_round:.1f} us, {gbps:.0f} GB/s", file=sys.stderr, flush=True)
+
+    # The per-GEMM drop-in path (fast_gemm's kernel, 97 launches) replayed as a HIP graph.
+    graph = rnd.capture()
+    ms_graph = time_graph(graph, args.steps, args.warmup)
+    del graph
+    us_graph = ms_graph * 1000.0
+    print(f"[bench] per-GEMM graph round: {us_graph:.1f} us, {rnd.bytes / (us_graph * 1e-6) / 1e9:.0f} GB/s",
+          file=sys.stderr, flush=True)
+
     result = {
         "metric": METRIC, "value": round(us_round, 2), "unit": "us/round", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
@@ -228,28 +302,32 @@ def main():
                                f"{args.layers} GPT-style blocks + LM head, M={args.M} (k=7)",
                    "M": args.M, "hidden": args.hidden, "mlp": args.mlp, "layers": args.layers,
                    "vocab": GPT2_VOCAB, "gemm_launches": len(gemms), "bytes_per_round": rnd.bytes,
-                   "timing": "HIP graph replay of the whole round, HIP events"},
+                   "timing": "HIP graph replay, HIP events; value = the round as one chained launch "
+                             "(plm_gemm_chain)", "chain_tile": CHAIN_TILE},
         "gbps": round(gbps, 1), "pct_of_hbm_peak": round(100.0 * gbps / HBM_PEAK_GBPS, 2),
+        "per_gemm_graph": {"us": round(us_graph, 2), "gbps": round(rnd.bytes / (us_graph * 1e-6) / 1e9, 1),
+                           "launches": len(gemms)},
     }
-    del graph
     if not args.only_round:
-        rows = dominant_kernel_roofline(rnd, args.steps)
-        top = rows[0]
-        achieved = top["bytes_per_launch"] / (top["us_per_launch"] * 1e-6) / 1e9
+        # The chained launch is the round's only kernel: its HIP-event time per replay is its duration.
+        kernel = "stream_gemm_kernel<bf16, MT=%d, NF=4, U=2> (chained round)" % math.ceil(args.M / 16)
+        achieved = rnd.bytes / (us_round * 1e-6) / 1e9
         result["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                              "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic_for(top["kernel"]),
-                              "kernel": top["kernel"], "launches_per_round": top["launches"],
-                              "us_per_launch": round(top["us_per_launch"], 3),
-                              "bytes_per_launch": int(top["bytes_per_launch"])}
-        result["kernels"] = [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()} for r in rows]
+                              "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic_for("chain_round"),
+                              "kernel": kernel, "launches_per_round": 1, "us_per_launch": round(us_round, 2),
+                              "bytes_per_launch": rnd.bytes}
+        rows = dominant_kernel_roofline(rnd, args.steps)
+        result["per_gemm_kernels"] = [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}
+                                      for r in rows]
         if not args.no_sweep:
             sweep = {}
             for M in (7, 14, 28, 42, 56):
                 r = Round(M, args.hidden, args.mlp, args.layers, weights, tables, device)
-                g = r.capture()
+                c = round_chain(r)
+                g = capture_graph(c.run)
                 us = time_graph(g, max(10, args.steps // 2), 3) * 1000.0
                 sweep[str(M)] = {"us": round(us, 1), "gbps": round(r.bytes / (us * 1e-6) / 1e9, 1)}
-                del g, r
+                del g, c, r
             result["m_sweep"] = sweep
             print(f"[bench] M sweep: {sweep}", file=sys.stderr, flush=True)
         if not args.no_verify:

@@ -43,15 +43,21 @@ enum plm_status {
   PLM_ERR_LAUNCH = -5         /* the HIP launch itself failed */
 };
 
+/* Index (in ints) of the error flag inside the counter area: a chained launch sets it to 1 when a
+ * bounded wait for another workgroup gave up (the launch's results are then invalid). */
+#define PLM_WORKSPACE_ERROR_INDEX 2
+
 /*
  * Tile configuration of one GEMM shape: the MI355X counterpart of the reference's
  * {BLOCK_M, BLOCK_N, BLOCK_K, SPLIT_K, num_warps, num_stages} dict (plm/fast_gemm.py:64).
- *   wave_frags : 16-row weight fragments per wavefront; the workgroup's N tile is 16*wave_frags.
- *   k_waves    : wavefronts per workgroup; each takes a contiguous K slice and the slices are
- *                summed through LDS in wave order 0..k_waves-1.
- *   split_k    : workgroups per N tile splitting K further; their fp32 partials are summed in
- *                split order 0..split_k-1 by the last workgroup to finish (no float atomics).
- *   unroll     : 32-wide K steps loaded per batch by each wavefront.
+ *   wave_frags : 16-row weight fragments per tile (1, 2 or 4); the tile is 16*wave_frags rows of W.
+ *   k_waves    : compute wavefronts per workgroup (4); each takes a contiguous K slice of the tile
+ *                and their partials are summed through LDS in wave order. A fifth wavefront runs
+ *                the epilogue.
+ *   split_k    : workgroups splitting K further; their fp32 partials are summed in split order
+ *                0..split_k-1 by the last workgroup of the tile to finish (no float atomics).
+ *   unroll     : 32-wide K steps per weight chunk (1, 2 or 4); each compute wavefront keeps the
+ *                next chunk's loads in flight while it multiplies the current one.
  */
 typedef struct plm_tile {
   int32_t wave_frags;
@@ -79,6 +85,47 @@ int plm_gemm(int32_t dtype, const void* x, int64_t ldx, const void* w, int64_t l
 int plm_gemm_f32out(int32_t dtype, const void* x, int64_t ldx, const void* w, int64_t ldw, float* y, int64_t ldy,
                     int64_t M, int64_t N, int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes,
                     void* stream);
+
+/*
+ * One linear of a chain run by plm_gemm_chain: Y[M,N] = X[M,K] · W[N,K]^T. The first block is the
+ * caller's; plm_gemm_chain_prepare fills the second.
+ */
+typedef struct plm_chain_gemm {
+  const void* x;
+  const void* w;
+  void* y;
+  int64_t ldx, ldw, ldy;
+  int32_t N, K;
+  int32_t split_k;        /* workgroups splitting K (>= 1) */
+  int32_t dep;            /* -1, or the index of an earlier linear whose Y this X is (x == that y,
+                             ldx == its ldy, K <= its N): the linear then waits for those tiles */
+  int32_t out_f32;        /* 1: Y is the fp32 accumulator, 0: Y in the input dtype */
+  /* filled by plm_gemm_chain_prepare */
+  int32_t consumed;       /* 1 when a later linear reads this Y */
+  int32_t arrive_base;    /* counter-area index of this linear's split-K arrival counters */
+  int32_t done_base;      /* counter-area index of this linear's tile-done flags */
+  int64_t partial_offset; /* float offset of this linear's split partials in the workspace */
+} plm_chain_gemm;
+
+/*
+ * Fills the derived fields of gemms[0..count) for the tile configuration (whose split_k is
+ * ignored: each linear has its own) and returns the workspace bytes plm_gemm_chain needs, or a
+ * negative status if the chain is invalid.
+ */
+int64_t plm_gemm_chain_prepare(plm_chain_gemm* gemms, int32_t count, int64_t M, const plm_tile* tile);
+
+/*
+ * Runs a chain of linears in one launch: the round's linears back to back (the reference's replayed
+ * round calls fast_gemm 4L+1 times, plm/decoder.py:312-324). A linear with dep >= 0
+ * starts each of its tiles as soon as the producer tiles covering that tile's K range are written,
+ * so consecutive linears overlap. `host_gemms` is the prepared array, `device_gemms` a copy of it in
+ * device memory (read by the kernel). Requirements as plm_gemm, plus: wave_frags == 4 when any
+ * linear has dep >= 0, a consumed Y is 16-bit, 128-byte aligned with ldy a multiple of 64, and no
+ * Y overlaps another Y or any X or W of the chain except through dep. Workgroups wait on each
+ * other, so the launch needs the device to itself (nothing else running on it).
+ */
+int plm_gemm_chain(int32_t dtype, const plm_chain_gemm* host_gemms, const plm_chain_gemm* device_gemms, int32_t count,
+                   int64_t M, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace bytes plm_gemm needs for this shape and tile (the reference's _partial_buffer,
  * plm/fast_gemm.py:70-79): PLM_WORKSPACE_COUNTER_BYTES plus the fp32 split partials. 0 when

@@ -1,0 +1,10 @@
+// fp16 instantiations of the streaming GEMM (one translation unit per dtype so they build in parallel).
+#include "stream_gemm.h"
+
+namespace plm {
+
+hipError_t stream_dispatch_f16(StreamArgs& a, int nf, int u, int cus, hipStream_t s, bool dry) {
+  return stream_dispatch<DT_F16>(a, nf, u, cus, s, dry);
+}
+
+}  // namespace plm

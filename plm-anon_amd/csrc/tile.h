@@ -23,6 +23,7 @@ namespace plm {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
@@ -57,6 +58,9 @@ __device__ __forceinline__ float round_through(float v, int mode) {
 // `bytes` returns zeros, which masks rows past the end of a tile, padded X rows and the K tail
 // without branches around the loads.
 constexpr uint32_t kOutOfRange = 0x80000000u;
+// Cache-policy bit of the buffer intrinsics that makes an access device-coherent (sc1 on gfx950):
+// stores are written through the XCD's L2, loads never hit a stale L2 line.
+constexpr int kCoherent = 16;
 constexpr int kBufferWord3 = 0x00020000;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {

@@ -226,7 +226,7 @@ __global__ __launch_bounds__(64 * KW) void verify_main_kernel(VerifyArgs a) {
 
 template <int MT, int NF, int U, bool PIPE, int KW>
 constexpr bool verify_compiled() {
-  if (KW != 4 && KW != 8) return false;
+  if (KW != 4) return false;  // the K partition of the streaming GEMM (plm_gemm_f32out gives the same logits)
   if (NF != 2 && NF != 4) return false;
   if (MT < 1 || MT > 4) return false;
   const bool u_ok = PIPE ? (U == 2 || U == 4) : (U == 4 || U == 8);
@@ -279,7 +279,6 @@ hipError_t verify_pick_u(const VerifyArgs& a, const plm_tile& t, bool pipe, int 
 #define PLM_VERIFY_KW(U_, P_)                                                        \
   if (t.unroll == U_ && pipe == P_) {                                                \
     if (t.k_waves == 4) return launch_verify<DT, MT, NF, U_, P_, 4>(a, cu, s, dry);  \
-    if (t.k_waves == 8) return launch_verify<DT, MT, NF, U_, P_, 8>(a, cu, s, dry);  \
   }
   PLM_VERIFY_KW(2, true)
   PLM_VERIFY_KW(4, true)

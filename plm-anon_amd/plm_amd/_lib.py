@@ -20,10 +20,15 @@ DTYPE_CODES = {torch.bfloat16: PLM_BF16, torch.float16: PLM_F16}
 # PLM_WORKSPACE_COUNTER_BYTES: the zero-between-calls counter area at the start of every workspace.
 COUNTER_BYTES = 1 << 18
 
+# PLM_WORKSPACE_ERROR_INDEX: the int in the counter area a chained launch sets when a wait gave up.
+ERROR_INDEX = 2
+
 # Every symbol include/plm_amd.h declares.
 EXPORTS = (
     "plm_gemm",
     "plm_gemm_f32out",
+    "plm_gemm_chain_prepare",
+    "plm_gemm_chain",
     "plm_gemm_workspace_bytes",
     "plm_gemm_tile_supported",
     "plm_lm_head_verify",
@@ -43,6 +48,16 @@ class Tile(ctypes.Structure):
         return cls(int(cfg["wave_frags"]), int(cfg["k_waves"]), int(cfg.get("split_k", 1)), int(cfg["unroll"]))
 
 
+class ChainGemm(ctypes.Structure):
+    """``struct plm_chain_gemm``: one linear of a chain (88 bytes, natural alignment)."""
+
+    _fields_ = [("x", ctypes.c_void_p), ("w", ctypes.c_void_p), ("y", ctypes.c_void_p),
+                ("ldx", ctypes.c_int64), ("ldw", ctypes.c_int64), ("ldy", ctypes.c_int64),
+                ("N", ctypes.c_int32), ("K", ctypes.c_int32), ("split_k", ctypes.c_int32), ("dep", ctypes.c_int32),
+                ("out_f32", ctypes.c_int32), ("consumed", ctypes.c_int32), ("arrive_base", ctypes.c_int32),
+                ("done_base", ctypes.c_int32), ("partial_offset", ctypes.c_int64)]
+
+
 _lib: ctypes.CDLL | None = None
 _lock = threading.Lock()
 
@@ -54,6 +69,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.plm_gemm.restype = ctypes.c_int
     lib.plm_gemm_f32out.argtypes = lib.plm_gemm.argtypes
     lib.plm_gemm_f32out.restype = ctypes.c_int
+    chain_p = ctypes.POINTER(ChainGemm)
+    lib.plm_gemm_chain_prepare.argtypes = [chain_p, c_i32, c_i64, tile_p]
+    lib.plm_gemm_chain_prepare.restype = c_i64
+    lib.plm_gemm_chain.argtypes = [c_i32, chain_p, c_p, c_i32, c_i64, tile_p, c_p, c_sz, c_p]
+    lib.plm_gemm_chain.restype = ctypes.c_int
     lib.plm_gemm_workspace_bytes.argtypes = [c_i64, c_i64, c_i64, tile_p]
     lib.plm_gemm_workspace_bytes.restype = c_sz
     lib.plm_gemm_tile_supported.argtypes = [c_i32, c_i64, c_i64, tile_p]

@@ -1,0 +1,86 @@
+"""A chain of linears in one launch: the round's linears back to back, where a linear may read an
+earlier one's output (``plm_gemm_chain`` in ``include/plm_amd.h``).
+
+The reference replays a round as a CUDA graph of separate ``fast_gemm`` launches, 4L+1 of them
+(plm/decoder.py:312-324, plm/fast_gemm.py:82-97). On MI355X each dependent launch costs about
+1.6 us of idle HBM between kernels; a chain keeps one persistent grid streaming weights across
+the linears and starts each tile of a linear as soon as the producer tiles it reads are written.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from .fast_gemm import Config, HALF_DTYPES, _tile, workspace
+
+
+@dataclass
+class Link:
+    """One linear of a chain: ``y = x @ w.T``. ``dep`` is the index of the earlier link whose ``y``
+    this ``x`` is (its leading ``K`` columns), or -1 when ``x`` comes from outside the chain."""
+
+    x: torch.Tensor
+    w: torch.Tensor
+    y: torch.Tensor
+    dep: int = -1
+    split_k: int = 1
+
+
+class LinearChain:
+    """Validated, prepared chain; ``run()`` launches it on the current stream (graph-capturable
+    once constructed: the descriptor upload and workspace sizing happen here)."""
+
+    def __init__(self, links: list[Link], cfg: Config):
+        if not links:
+            raise ValueError("a chain needs at least one linear")
+        self.links = links
+        self.cfg = dict(cfg)
+        x0 = links[0].x
+        self.device = x0.device
+        self.dtype = x0.dtype
+        self.M = x0.shape[0]
+        if self.dtype not in HALF_DTYPES:
+            raise TypeError(f"chain operands must be bf16 or fp16, got {self.dtype}")
+        arr = (_lib.ChainGemm * len(links))()
+        for i, ln in enumerate(links):
+            for name, t in (("x", ln.x), ("w", ln.w)):
+                if t.dtype != self.dtype or t.device != self.device or t.dim() != 2 or t.stride(1) != 1:
+                    raise ValueError(f"link {i}: {name} must be a row-major {self.dtype} matrix on {self.device}")
+            if ln.x.shape[0] != self.M or ln.y.shape[0] != self.M or ln.x.shape[1] != ln.w.shape[1]:
+                raise ValueError(f"link {i}: shapes x{tuple(ln.x.shape)} w{tuple(ln.w.shape)} y{tuple(ln.y.shape)}")
+            if ln.y.shape[1] != ln.w.shape[0] or ln.y.stride(1) != 1 or ln.y.device != self.device:
+                raise ValueError(f"link {i}: y must be a row-major [{self.M},{ln.w.shape[0]}] matrix")
+            if ln.y.dtype not in (self.dtype, torch.float32):
+                raise TypeError(f"link {i}: y must be {self.dtype} or float32")
+            g = arr[i]
+            g.x, g.w, g.y = ln.x.data_ptr(), ln.w.data_ptr(), ln.y.data_ptr()
+            g.ldx, g.ldw, g.ldy = ln.x.stride(0), ln.w.stride(0), ln.y.stride(0)
+            g.N, g.K = ln.w.shape[0], ln.w.shape[1]
+            g.split_k, g.dep = ln.split_k, ln.dep
+            g.out_f32 = int(ln.y.dtype == torch.float32)
+        self._tile = _tile(self.cfg)
+        lib = _lib.lib()
+        need = int(lib.plm_gemm_chain_prepare(arr, len(links), self.M, self._tile))
+        if need < 0:
+            _lib.check(need, "plm_gemm_chain_prepare")
+        self.host = arr
+        raw = bytes(memoryview(arr).cast("B"))
+        self.table = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(self.device)
+        self.workspace_bytes = need
+        self.ws = workspace(self.device, need)
+
+    def run(self) -> None:
+        lib = _lib.lib()
+        status = lib.plm_gemm_chain(_lib.DTYPE_CODES[self.dtype], self.host, self.table.data_ptr(), len(self.links),
+                                    self.M, self._tile, self.ws.data_ptr(), self.ws.numel(),
+                                    _lib.stream_handle(self.device))
+        _lib.check(status, f"plm_gemm_chain({len(self.links)} linears, M={self.M}, cfg={self.cfg})")
+
+    def error_flag(self) -> int:
+        """The counter area's error flag (1 if a wait for another workgroup gave up); syncs."""
+        torch.cuda.synchronize(self.device)
+        return int(self.ws[: 4 * (_lib.ERROR_INDEX + 1)].view(torch.int32)[_lib.ERROR_INDEX].item())

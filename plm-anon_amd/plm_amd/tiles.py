@@ -1,8 +1,10 @@
 """Tile selection for shapes without a tuned table entry, and the candidate set the tuner sweeps.
 
-A tile is ``{"wave_frags", "k_waves", "split_k", "unroll"}`` (see ``struct plm_tile`` in
-``include/plm_amd.h``). Workgroups = ``ceil(N / (16*wave_frags)) * split_k``; each wavefront takes
-``ceil(ceil(K/32) / (split_k*k_waves))`` 32-wide K steps, loaded in batches of ``unroll``.
+A tile is ``{"wave_frags", "k_waves", "split_k", "unroll"}`` (``struct plm_tile`` in
+``include/plm_amd.h``): tiles of ``16*wave_frags`` weight rows, ``k_waves`` (= 4) compute wavefronts
+splitting each tile's K range, ``split_k`` workgroups splitting K further, and ``unroll`` 32-wide K
+steps per weight chunk. Items (tile x split) = ``ceil(N / (16*wave_frags)) * split_k``; the
+persistent grid has one workgroup per compute unit (two where registers and LDS allow).
 """
 
 from __future__ import annotations
@@ -10,61 +12,77 @@ from __future__ import annotations
 import math
 
 CU_COUNT = 256          # MI355X compute units
-UNROLLS = (2, 4, 8)
+K_WAVES = 4
 WAVE_FRAGS = (1, 2, 4)
-K_WAVES = (4, 8)
-SPLITS = (1, 2, 3, 4, 6, 8, 12, 16)
+UNROLLS = (1, 2, 4)
+SPLITS = (1, 2, 3, 4, 6, 8)
+
+
+def compiled(M: int, cfg: dict) -> bool:
+    """Whether the library has a kernel for this tile at width M (mirrors ``stream_compiled`` in
+    csrc/stream_gemm.h: two LDS spill buffers of 4*NF*MT KiB, and the compute wavefronts'
+    registers (double-buffered weight and X chunks, accumulators) within 256 VGPRs)."""
+    mt, nf, u = math.ceil(M / 16), cfg["wave_frags"], cfg["unroll"]
+    if not (1 <= mt <= 8 and nf in WAVE_FRAGS and u in UNROLLS and cfg["k_waves"] == K_WAVES):
+        return False
+    if K_WAVES * nf * mt > 64:
+        return False
+    return 2 * nf * u * 4 + 2 * mt * u * 4 + nf * mt * 4 + 48 <= 256
+
+
+def items(N: int, cfg: dict) -> int:
+    return math.ceil(N / (16 * cfg["wave_frags"])) * cfg["split_k"]
 
 
 def steps_per_wave(K: int, cfg: dict) -> int:
     return math.ceil(math.ceil(K / 32) / (cfg["split_k"] * cfg["k_waves"]))
 
 
-def workgroups(N: int, cfg: dict) -> int:
-    return math.ceil(N / (16 * cfg["wave_frags"])) * cfg["split_k"]
-
-
 def candidates(M: int, N: int, K: int, supported=None) -> list[dict]:
     """Every sensible tile for ``(M, N, K)``; ``supported(cfg) -> bool`` filters to compiled kernels."""
-    steps = math.ceil(K / 32)
     out = []
     for nf in WAVE_FRAGS:
-        for kw in K_WAVES:
-            for split in SPLITS:
-                if split * kw > steps:
+        for split in SPLITS:
+            for u in UNROLLS:
+                cfg = {"wave_frags": nf, "k_waves": K_WAVES, "split_k": split, "unroll": u}
+                spw = steps_per_wave(K, cfg)
+                if spw < 1 or (u == 4 and spw <= 2):
                     continue
-                for u in UNROLLS:
-                    cfg = {"wave_frags": nf, "k_waves": kw, "split_k": split, "unroll": u}
-                    spw = steps_per_wave(K, cfg)
-                    if u > 2 and spw <= u // 2:      # a smaller batch already covers the slice
-                        continue
-                    wgs = workgroups(N, cfg)
-                    if wgs < CU_COUNT // 4 or wgs > 16 * CU_COUNT:
-                        continue
-                    if supported is not None and not supported(cfg):
-                        continue
-                    out.append(cfg)
+                if items(N, cfg) > 64 * CU_COUNT:
+                    continue
+                if supported is not None and not supported(cfg):
+                    continue
+                out.append(cfg)
     return out
 
 
 def heuristic_tile(M: int, N: int, K: int, supported=None) -> dict:
-    """A reasonable tile without measurement: 32-row tiles, 8 wavefronts, enough K splitting to put
-    about two workgroups on every CU, and a single load batch per wavefront when it fits. With
-    ``supported(cfg) -> bool`` it falls back to 4 wavefronts, then 16-row tiles, until a compiled
-    kernel exists."""
+    """A reasonable tile without measurement: the widest weight tile the registers allow, and
+    enough K splitting to give every compute unit an item while each wavefront keeps at least
+    four K steps per item."""
     steps = math.ceil(K / 32)
-    for nf, kw in ((2, 8), (2, 4), (1, 8), (1, 4)):
-        tiles = math.ceil(N / (16 * nf))
-        split = 1
-        while tiles * split < 2 * CU_COUNT and split * 2 * kw <= steps and split < 16:
-            split *= 2
-        cfg = {"wave_frags": nf, "k_waves": kw, "split_k": split, "unroll": 8}
-        spw = steps_per_wave(K, cfg)
-        cfg["unroll"] = 2 if spw <= 2 else 4 if spw <= 4 else 8 if spw <= 8 else 4
-        if supported is None or supported(cfg):
-            return cfg
-        if spw > 2:
-            cfg["unroll"] = 4 if spw <= 4 or cfg["unroll"] == 8 else 2
-            if supported(cfg):
+    for nf in (4, 2, 1):
+        for u in (4, 2):
+            tiles = math.ceil(N / (16 * nf))
+            split = 1
+            while tiles * split < CU_COUNT and steps // (2 * split * K_WAVES) >= 4 and split < 8:
+                split *= 2
+            cfg = {"wave_frags": nf, "k_waves": K_WAVES, "split_k": split, "unroll": u}
+            if compiled(M, cfg) and (supported is None or supported(cfg)):
                 return cfg
     raise ValueError(f"no compiled tile fits (M={M}, N={N}, K={K})")
+
+
+# Tile of a chained round (plm_gemm_chain): 64-row tiles, as a consumed output needs.
+CHAIN_TILE = {"wave_frags": 4, "k_waves": K_WAVES, "split_k": 1, "unroll": 2}
+
+
+def chain_split(N: int, K: int, cfg: dict = CHAIN_TILE, workgroups: int = CU_COUNT) -> int:
+    """K split of one linear inside a chain: the smallest power of two that gives about one item
+    per resident workgroup, keeping at least two K steps per compute wavefront."""
+    tiles = math.ceil(N / (16 * cfg["wave_frags"]))
+    steps = math.ceil(K / 32)
+    split = 1
+    while tiles * split < workgroups * 3 // 4 and steps // (2 * split * K_WAVES) >= 2 and split < 8:
+        split *= 2
+    return split

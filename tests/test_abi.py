@@ -21,7 +21,7 @@ HEADER = REPO / "include" / "plm_amd.h"
 
 def declared_functions() -> list[str]:
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(plm_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|size_t|const char\*)\s+(plm_\w+)\s*\(", text, re.M)))
 
 
 def test_library_exports_every_declared_symbol():
@@ -42,7 +42,7 @@ def test_status_strings():
 
 def test_argument_validation_happens_before_launch():
     lib = _lib.lib()
-    tile = _lib.Tile(2, 8, 1, 8)
+    tile = _lib.Tile(2, 4, 1, 4)
     fake = 1 << 20  # never dereferenced: every call below fails validation first
     # K not a multiple of 8.
     assert lib.plm_gemm(0, fake, 1024, fake, 1024, fake, 4096, 42, 4096, 1020, tile, None, 0, None) == -1
@@ -54,10 +54,10 @@ def test_argument_validation_happens_before_launch():
     # Unknown dtype.
     assert lib.plm_gemm(7, fake, 1024, fake, 1024, fake, 4096, 42, 4096, 1024, tile, None, 0, None) == -1
     # Split-K without a workspace.
-    split = _lib.Tile(2, 8, 4, 2)
+    split = _lib.Tile(2, 4, 4, 2)
     assert lib.plm_gemm(0, fake, 1024, fake, 1024, fake, 4096, 42, 4096, 1024, split, None, 0, None) == -4
     # A tile with no compiled kernel.
-    odd = _lib.Tile(3, 8, 1, 8)
+    odd = _lib.Tile(3, 4, 1, 4)
     assert lib.plm_gemm(0, fake, 1024, fake, 1024, fake, 4096, 42, 4096, 1024, odd, None, 0, None) == -3
     # Verify: bad round mode, R too large.
     vt = _lib.Tile(2, 4, 1, 4)
@@ -71,9 +71,11 @@ def test_workspace_sizes():
     lib = _lib.lib()
     m = re.search(r"#define PLM_WORKSPACE_COUNTER_BYTES \(1u << (\d+)\)", HEADER.read_text())
     assert m and _lib.COUNTER_BYTES == 1 << int(m.group(1))
-    assert lib.plm_gemm_workspace_bytes(56, 2048, 8192, _lib.Tile(2, 8, 1, 4)) == 0
-    n = lib.plm_gemm_workspace_bytes(56, 2048, 8192, _lib.Tile(2, 8, 4, 4))
+    assert lib.plm_gemm_workspace_bytes(56, 2048, 8192, _lib.Tile(2, 4, 1, 4)) == 0
+    n = lib.plm_gemm_workspace_bytes(56, 2048, 8192, _lib.Tile(2, 4, 4, 4))
     assert n == _lib.COUNTER_BYTES + 4 * 56 * 2048 * 4
+    # Partial planes pad N to a multiple of 4 floats.
+    assert lib.plm_gemm_workspace_bytes(42, 50257, 1024, _lib.Tile(2, 4, 2, 4)) == _lib.COUNTER_BYTES + (2 * 42 * 50260 + 63) // 64 * 64 * 4
     assert lib.plm_lm_head_verify_workspace_bytes(56, 50257, 2048, _lib.Tile(2, 4, 1, 4)) > 56 * 4
 
 
@@ -84,6 +86,13 @@ def test_tile_support_matches_register_budget():
             cfg = tiles.heuristic_tile(w.M, g.N, g.K)
             assert fast_gemm.tile_supported(w.M, g.K, cfg), (g, cfg)
     assert not fast_gemm.tile_supported(56, 2048, {"wave_frags": 4, "k_waves": 8, "split_k": 1, "unroll": 8})
+    # The Python mirror of the compiled set agrees with the library everywhere.
+    for M in (1, 7, 16, 17, 42, 56, 64, 65, 110, 128):
+        for nf in (1, 2, 3, 4):
+            for u in (1, 2, 4, 8):
+                for kw in (4, 8):
+                    cfg = {"wave_frags": nf, "k_waves": kw, "split_k": 1, "unroll": u}
+                    assert tiles.compiled(M, cfg) == fast_gemm.tile_supported(M, 2048, cfg), (M, cfg)
 
 
 # --------------------------------------------------------------------------- tile tables

@@ -1,8 +1,14 @@
 """GPU parity of the HIP skinny GEMM against the CPU oracle (the reference's own F.linear path).
 
-Tolerance: bf16/fp16 outputs within 1e-3 relative / 2e-2 absolute of the oracle, and within one
-output ulp of the exact (fp64) product plus an fp32-accumulation term (a tighter bound that holds
-whatever the summation order)."""
+Tolerance, per output element of the bf16/fp16 result:
+* within one rounding of the exact (fp64) product, up to fp32 accumulation error:
+  |got - exact| <= ulp(exact) + 2^-20 * sum_k |x_k w_k|;
+* against the oracle's own rounded output: within 1e-3 relative / 2e-2 absolute, or one step of
+  the output dtype apart (two correctly rounded values of sums taken in different orders can
+  land on either side of a rounding midpoint; at |y| >= 4 one bf16 step, 2^-5, exceeds the
+  absolute tolerance), with at most 0.1% of the elements one step apart.
+The fp32 accumulator itself (``hip_linear_f32``) is held to 1e-3 relative / 2e-2 absolute and
+tighter."""
 
 from __future__ import annotations
 
@@ -41,14 +47,23 @@ def check_cols(y: torch.Tensor, x: torch.Tensor, w: torch.Tensor, cols: torch.Te
     cols_d = cols.to(w.device)
     got = y[:, cols_d].cpu().float()
     xc, wc = x.cpu(), w[cols_d].cpu()
-    torch.testing.assert_close(got, oracle.linear(xc, wc).float(), rtol=RTOL, atol=ATOL)
-    _within_one_rounding(got, xc, wc)
+    _assert_parity(got, xc, wc)
 
 
 def _ulp(v: torch.Tensor, dtype) -> torch.Tensor:
     bits = 8 if dtype == torch.bfloat16 else 11
     e = torch.floor(torch.log2(v.abs().clamp_min(2.0 ** -14)))
     return 2.0 ** (e - (bits - 1))
+
+
+def _assert_parity(got: torch.Tensor, x: torch.Tensor, w: torch.Tensor) -> None:
+    _within_one_rounding(got, x, w)
+    ref = oracle.linear(x, w).float()
+    diff = (got - ref).abs()
+    in_tol = diff <= ATOL + RTOL * ref.abs()
+    one_step = diff <= _ulp(ref, x.dtype) * 1.0001
+    assert bool((in_tol | one_step).all()), f"max |got - oracle| {diff.max():.4g}"
+    assert int((~in_tol).sum()) <= max(1, got.numel() // 1000), int((~in_tol).sum())
 
 
 def _within_one_rounding(got: torch.Tensor, x: torch.Tensor, w: torch.Tensor) -> None:
@@ -66,9 +81,7 @@ def check(y: torch.Tensor, x: torch.Tensor, w: torch.Tensor):
     """GPU ``y`` against the oracle on the CPU operands x, w."""
     wc = w
     got = y.cpu().float()
-    ref = oracle.linear(x, wc).float()
-    torch.testing.assert_close(got, ref, rtol=RTOL, atol=ATOL)
-    _within_one_rounding(got, x, wc)
+    _assert_parity(got, x, wc)
 
 
 def _run(x, w, cfg, device):
@@ -127,11 +140,11 @@ def test_split_k_is_deterministic_and_consistent(device):
     M, N, K = 56, 2048, 8192
     x, w = _inputs(M, N, K, 6)
     xd, wd = x.to(device), w.to(device)
-    split = {"wave_frags": 2, "k_waves": 8, "split_k": 8, "unroll": 4}
+    split = {"wave_frags": 2, "k_waves": 4, "split_k": 8, "unroll": 2}
     a = hip_linear_f32(xd, wd, split)
     b = hip_linear_f32(xd, wd, split)
     assert torch.equal(a, b)
-    single = hip_linear_f32(xd, wd, {"wave_frags": 2, "k_waves": 8, "split_k": 1, "unroll": 4})
+    single = hip_linear_f32(xd, wd, {"wave_frags": 2, "k_waves": 4, "split_k": 1, "unroll": 2})
     torch.testing.assert_close(a, single, rtol=1e-5, atol=1e-5)
     torch.testing.assert_close(a.cpu(), oracle.linear_fp32(x, w), rtol=1e-4, atol=1e-4)
 
@@ -141,10 +154,10 @@ def test_workspace_shared_across_shapes_and_entry_points(device):
     # each must find the counter area zero whatever the previous call left in the scratch area.
     from plm_amd.verify import lm_head_verify
 
-    cases = [((56, 6144, 2048), {"wave_frags": 2, "k_waves": 8, "split_k": 4, "unroll": 2}),
-             ((56, 8192, 2048), {"wave_frags": 2, "k_waves": 8, "split_k": 2, "unroll": 4}),
+    cases = [((56, 6144, 2048), {"wave_frags": 2, "k_waves": 4, "split_k": 4, "unroll": 2}),
+             ((56, 8192, 2048), {"wave_frags": 2, "k_waves": 4, "split_k": 2, "unroll": 2}),
              ((56, 2048, 2048), {"wave_frags": 1, "k_waves": 4, "split_k": 8, "unroll": 2}),
-             ((56, 8192, 2048), {"wave_frags": 2, "k_waves": 8, "split_k": 2, "unroll": 4})]
+             ((56, 8192, 2048), {"wave_frags": 4, "k_waves": 4, "split_k": 2, "unroll": 2})]
     for i, ((M, N, K), cfg) in enumerate(cases):
         x, w = _inputs(M, N, K, 40 + i)
         check(_run(x, w, cfg, device), x, w)
@@ -155,8 +168,8 @@ def test_workspace_shared_across_shapes_and_entry_points(device):
 def test_fp16(device):
     M, N, K = 56, 3072, 2048
     x, w = _inputs(M, N, K, 7, torch.float16)
-    for cfg in ({"wave_frags": 2, "k_waves": 8, "split_k": 2, "unroll": 4},
-                {"wave_frags": 4, "k_waves": 4, "split_k": 1, "unroll": 4}):
+    for cfg in ({"wave_frags": 2, "k_waves": 4, "split_k": 2, "unroll": 2},
+                {"wave_frags": 4, "k_waves": 4, "split_k": 1, "unroll": 2}):
         check(_run(x, w, cfg, device), x, w)
 
 
@@ -167,7 +180,7 @@ def test_small_integers_are_exact(device):
     w = torch.randint(-1, 2, (N, K), generator=g).bfloat16()
     exact = oracle.linear_fp64(x, w)
     assert abs(exact).max() < 256
-    for cfg in ({"wave_frags": 2, "k_waves": 8, "split_k": 1, "unroll": 8},
+    for cfg in ({"wave_frags": 2, "k_waves": 4, "split_k": 1, "unroll": 2},
                 {"wave_frags": 1, "k_waves": 4, "split_k": 4, "unroll": 4}):
         y = _run(x, w, cfg, device).cpu().double().numpy()
         assert (y == exact).all()
@@ -179,7 +192,7 @@ def test_one_hot_weight_selects_columns(device):
     cols = torch.tensor([0, 5, 1023, 512, 77, 31, 32, 999])
     w = torch.zeros(len(cols), K).bfloat16()
     w[torch.arange(len(cols)), cols] = 1.0
-    y = _run(x, w, {"wave_frags": 1, "k_waves": 4, "split_k": 1, "unroll": 8}, device)
+    y = _run(x, w, {"wave_frags": 1, "k_waves": 4, "split_k": 1, "unroll": 4}, device)
     assert torch.equal(y.cpu(), x[:, cols])
 
 

@@ -16,7 +16,7 @@ import oracle
 from oracle import plm_oracle as po
 from plm_amd import _lib, fast_gemm, workloads
 from plm_amd.fast_gemm import hip_linear_f32
-from plm_amd.verify import VERIFY_CONFIG, lm_head_verify
+from plm_amd.verify import LOGITS_CONFIG, lm_head_verify
 
 pytestmark = pytest.mark.gpu
 
@@ -41,7 +41,7 @@ def _own_logits_from_workspace(R: int, device) -> torch.Tensor:
 def run_case(x, w, pending, p, mode, device, cfg=None, check_cpu=True):
     acc, am = lm_head_verify(x, w, pending, p, mode, cfg)
     acc, am = acc.cpu(), am.cpu()
-    logits = _rounded(hip_linear_f32(x, w, cfg or VERIFY_CONFIG).cpu(), mode)
+    logits = _rounded(hip_linear_f32(x, w, LOGITS_CONFIG).cpu(), mode)
     # The own-logit pass reproduces the main pass's value for each proposal bit for bit.
     own = _own_logits_from_workspace(x.shape[0], device)
     valid = (pending.cpu() >= 0) & (pending.cpu() < w.shape[0])
@@ -55,7 +55,7 @@ def run_case(x, w, pending, p, mode, device, cfg=None, check_cpu=True):
     assert torch.equal(acc, ref_acc), (acc != ref_acc).nonzero()
     if check_cpu:
         cpu = oracle.linear_fp32(x.cpu(), w.cpu())
-        torch.testing.assert_close(hip_linear_f32(x, w, cfg or VERIFY_CONFIG).cpu(), cpu, rtol=1e-3, atol=1e-4)
+        torch.testing.assert_close(hip_linear_f32(x, w, LOGITS_CONFIG).cpu(), cpu, rtol=1e-3, atol=1e-4)
     return acc, am, logits
 
 
@@ -96,9 +96,9 @@ def test_round_widths(device, R):
     run_case(x, w, pending, P, "fp32", device)
 
 
-@pytest.mark.parametrize("cfg", [{"wave_frags": 2, "k_waves": 8, "split_k": 1, "unroll": 2},
+@pytest.mark.parametrize("cfg", [{"wave_frags": 4, "k_waves": 4, "split_k": 1, "unroll": 2},
                                  {"wave_frags": 4, "k_waves": 4, "split_k": 1, "unroll": 4},
-                                 {"wave_frags": 2, "k_waves": 4, "split_k": 1, "unroll": 8}])
+                                 {"wave_frags": 2, "k_waves": 4, "split_k": 1, "unroll": 2}])
 def test_other_tiles(device, cfg):
     x, w, pending = _config5(device, R=56, V=12345, K=1024)
     run_case(x, w, pending, 0.5, "fp32", device, cfg)
@@ -106,7 +106,7 @@ def test_other_tiles(device, cfg):
 
 def test_proposals_at_the_argmax_and_exact_mode(device):
     x, w, _ = _config5(device, R=56, V=9000)
-    am0 = oracle.argmax(hip_linear_f32(x, w, VERIFY_CONFIG).cpu()).to(device)
+    am0 = oracle.argmax(hip_linear_f32(x, w, LOGITS_CONFIG).cpu()).to(device)
     acc, am, _ = run_case(x, w, am0, P, "fp32", device)
     assert bool(acc.all())                       # the maximum is always inside the nucleus
     acc0, _, _ = run_case(x, w, am0, 0.0, "fp32", device)
@@ -124,7 +124,7 @@ def test_uniform_rows_and_ties(device):
     assert bool(acc.all()) and bool((am == 0).all())   # all logits 0: no mass above, argmax index 0
     # Duplicate the best row further down the vocabulary: the tie resolves to the lower index.
     w = (0.05 * torch.randn(V, K, device=device)).bfloat16()
-    logits = hip_linear_f32(x, w, VERIFY_CONFIG).cpu()
+    logits = hip_linear_f32(x, w, LOGITS_CONFIG).cpu()
     best = logits.argmax(-1)
     for r in range(R):
         w[V - 1 - r] = w[int(best[r])]
@@ -134,7 +134,7 @@ def test_uniform_rows_and_ties(device):
 
 def test_pending_outside_vocabulary_is_rejected(device):
     x, w, pending = _config5(device, R=8, V=4000)
-    am_ids = oracle.argmax(hip_linear_f32(x, w, VERIFY_CONFIG).cpu())
+    am_ids = oracle.argmax(hip_linear_f32(x, w, LOGITS_CONFIG).cpu())
     pending = am_ids.clone().to(device)
     pending[1] = -1
     pending[5] = 4000
