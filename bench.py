@@ -209,11 +209,12 @@ def capture_graph(fn):
 def round_chain(rnd):
     """The round's 97 linears as one chained launch (plm_gemm_chain), output-to-input."""
     from plm_amd.chain import Link, LinearChain
-    from plm_amd.tiles import CHAIN_TILE, chain_split
+    from plm_amd.tiles import chain_split, chain_tile
 
-    links = [Link(x, w, y, i - 1, chain_split(g.N, g.K))
+    cfg = chain_tile(rnd.M)
+    links = [Link(x, w, y, i - 1, chain_split(g.N, g.K, cfg))
              for i, (g, x, w, y) in enumerate(zip(rnd.gemms, rnd.inputs, rnd.weights, rnd.outs))]
-    return LinearChain(links, CHAIN_TILE)
+    return LinearChain(links, cfg)
 
 
 def main():
@@ -226,7 +227,7 @@ def main():
 
     from plm_amd import gemm_tables
     from plm_amd.fast_gemm import hip_linear  # noqa: F401  (fails loudly if the library is missing)
-    from plm_amd.tiles import CHAIN_TILE
+    from plm_amd.tiles import chain_tile
     from plm_amd.workloads import GPT2_VOCAB, gpt_block
 
     torch.cuda.set_device(0)
@@ -303,7 +304,7 @@ def main():
                    "M": args.M, "hidden": args.hidden, "mlp": args.mlp, "layers": args.layers,
                    "vocab": GPT2_VOCAB, "gemm_launches": len(gemms), "bytes_per_round": rnd.bytes,
                    "timing": "HIP graph replay, HIP events; value = the round as one chained launch "
-                             "(plm_gemm_chain)", "chain_tile": CHAIN_TILE},
+                             "(plm_gemm_chain)", "chain_tile": chain_tile(args.M)},
         "gbps": round(gbps, 1), "pct_of_hbm_peak": round(100.0 * gbps / HBM_PEAK_GBPS, 2),
         "per_gemm_graph": {"us": round(us_graph, 2), "gbps": round(rnd.bytes / (us_graph * 1e-6) / 1e9, 1),
                            "launches": len(gemms)},

@@ -170,7 +170,9 @@ int plm_gemm_f32out(int32_t dtype, const void* x, int64_t ldx, const void* w, in
 }
 
 int64_t plm_gemm_chain_prepare(plm_chain_gemm* gemms, int32_t count, int64_t M, const plm_tile* tile) {
-  if (gemms == nullptr || count < 1 || count > 4096 || M < 1 || M > plm::kMaxM || tile == nullptr) return PLM_ERR_ARGUMENT;
+  if (gemms == nullptr || count < 1 || plm::table_bytes(count) > plm::kTableReserve || M < 1 || M > plm::kMaxM ||
+      tile == nullptr)
+    return PLM_ERR_ARGUMENT;
   plm_tile t = *tile;
   t.split_k = 1;
   if (!plm::tile_valid(&t)) return PLM_ERR_TILE;
@@ -179,15 +181,13 @@ int64_t plm_gemm_chain_prepare(plm_chain_gemm* gemms, int32_t count, int64_t M, 
 
 int plm_gemm_chain(int32_t dtype, const plm_chain_gemm* host_gemms, const plm_chain_gemm* device_gemms, int32_t count,
                    int64_t M, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream) {
-  if (host_gemms == nullptr || device_gemms == nullptr || count < 1 || count > 4096 || tile == nullptr)
-    return PLM_ERR_ARGUMENT;
+  if (host_gemms == nullptr || device_gemms == nullptr || count < 1 || tile == nullptr) return PLM_ERR_ARGUMENT;
   plm_tile t = *tile;
   t.split_k = 1;
   if (!plm::tile_valid(&t)) return PLM_ERR_TILE;
   if (M < 1 || M > plm::kMaxM) return PLM_ERR_ARGUMENT;
   // The kernel keeps the chain's descriptors in LDS next to its spill buffers.
-  if (plm::table_bytes(count) + 2 * plm::kStreamKW * t.wave_frags * ((M + 15) / 16) * 1024 > plm::kMaxLdsBytes)
-    return PLM_ERR_ARGUMENT;
+  if (plm::table_bytes(count) > plm::kTableReserve) return PLM_ERR_ARGUMENT;
   // The derived fields must be what prepare() computes for this chain.
   std::vector<plm_chain_gemm> check(host_gemms, host_gemms + count);
   const int64_t need = plm::prepare(check.data(), count, M, t);

@@ -189,14 +189,71 @@ __device__ __forceinline__ bool advance(const StreamArgs& a, Cursor<NF>& q, int 
   return false;
 }
 
+// ------------------------------------------------------------------ compute wavefronts
+//
+// Operands travel HBM/L2 -> LDS by DMA (buffer_load ... lds: 16 bytes per lane, written to LDS in
+// lane order, so reading slot + 16*lane back gives every lane exactly the MFMA operand it loaded)
+// and LDS -> VGPRs by ds_read_b128. No vector register is the destination of a load in flight,
+// so the compiler never inserts a vmcnt wait of its own in the compute loop; the single wait per
+// chunk is explicit, and it leaves the weight ring's later chunks in flight.
+//
+// Per compute wavefront (all in LDS):
+//   * weight ring: R slots of one chunk (U steps x NF fragments, 1 KiB each), filled R-1 chunks
+//     ahead of the chunk being multiplied, across item and linear boundaries;
+//   * X ring: 2 slots of one chunk (U steps x MT fragments), filled one chunk ahead (or, for the
+//     first chunk of an item that depends on earlier linears, once the epilogue wavefront
+//     publishes it may be read).
+// The four wavefronts' partial tiles are summed pairwise through a spill area of two tiles:
+// (w0 + w1) + (w2 + w3), the last sum by the epilogue wavefront.
+
+typedef __attribute__((address_space(3))) u32x4 LdsVec;
+typedef __attribute__((address_space(3))) void LdsVoid;
+
+template <int MT, int NF>
+constexpr size_t spill_bytes() {  // two partial tiles
+  return static_cast<size_t>(2) * NF * MT * 64 * sizeof(f32x4);
+}
 template <int NF, int U>
-struct WChunk {
-  u32x4 v[NF][U];
-};
+constexpr size_t wslot_bytes() {
+  return static_cast<size_t>(NF) * U * 1024;
+}
 template <int MT, int U>
-struct XChunk {
-  u32x4 v[MT][U];
+constexpr size_t xslot_bytes() {
+  return static_cast<size_t>(MT) * U * 1024;
+}
+constexpr size_t kTableReserve = 16 * 1024;  // descriptors of a chain of up to 186 linears
+// Weight-ring depth that fits beside the spill area, the X rings and the descriptor reserve.
+template <int MT, int NF, int U>
+constexpr int ring_slots() {
+  const long avail = static_cast<long>(kMaxLdsBytes) - static_cast<long>(kTableReserve) -
+                     static_cast<long>(spill_bytes<MT, NF>()) -
+                     static_cast<long>(kStreamKW * 2 * xslot_bytes<MT, U>());
+  const long r = avail / static_cast<long>(kStreamKW * wslot_bytes<NF, U>());
+  return r > 8 ? 8 : static_cast<int>(r);
+}
+// Dynamic LDS bytes past the descriptor table: spill area, weight rings, X rings.
+template <int MT, int NF, int U>
+constexpr size_t stream_lds_bytes() {
+  return spill_bytes<MT, NF>() + kStreamKW * (ring_slots<MT, NF, U>() * wslot_bytes<NF, U>() + 2 * xslot_bytes<MT, U>());
+}
+
+struct Rings {
+  char* spill;  // two partial tiles, float4 [2][NF][MT][64]
+  char* w;      // this wavefront's weight ring
+  char* x;      // this wavefront's X ring
 };
+
+template <int MT, int NF, int U>
+__device__ __forceinline__ Rings rings_of(float* base, int wave) {
+  constexpr int R = ring_slots<MT, NF, U>();
+  char* b = reinterpret_cast<char*>(base);
+  Rings r;
+  r.spill = b;
+  r.w = b + spill_bytes<MT, NF>() + static_cast<size_t>(wave) * R * wslot_bytes<NF, U>();
+  r.x = b + spill_bytes<MT, NF>() + static_cast<size_t>(kStreamKW) * R * wslot_bytes<NF, U>() +
+        static_cast<size_t>(wave) * 2 * xslot_bytes<MT, U>();
+  return r;
+}
 
 // Steps of chunk q.c that this wavefront owns (0..U).
 template <int NF, int U>
@@ -205,12 +262,15 @@ __device__ __forceinline__ int chunk_steps(const Cursor<NF>& q) {
   return left < 0 ? 0 : (left < U ? left : U);
 }
 
-// Chunk loads are straight-line code: every (step, fragment) load is issued, steps past the
-// wavefront's slice (or past K, or rows past the tile) get an out-of-range offset and read zeros
-// without touching memory. Branch-free loads let the compiler count outstanding loads exactly,
-// so it waits only for the chunk being multiplied, never for the prefetch behind it.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, char* lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (LdsVoid*)(lds), 16, static_cast<int>(off), 0, 0, 0);
+}
+
+// Every (step, fragment) load is issued; steps past the wavefront's slice, K past the end and rows
+// past the tile get an out-of-range offset, which writes zeros and touches no memory. A fixed
+// number of loads per chunk is what makes the explicit wait counts exact.
 template <int NF, int U>
-__device__ __forceinline__ void load_w(WChunk<NF, U>& wc, const Cursor<NF>& q, bool live, int lane) {
+__device__ __forceinline__ void dma_w(char* slot, const Cursor<NF>& q, bool live, int lane) {
   const int n = live ? chunk_steps<NF, U>(q) : 0;
   const auto rsrc = make_rsrc(q.w + static_cast<int64_t>(q.n0) * q.ldw, static_cast<uint32_t>(q.tn * q.ldw * 2));
   const int row = lane & 15;
@@ -224,14 +284,13 @@ __device__ __forceinline__ void load_w(WChunk<NF, U>& wc, const Cursor<NF>& q, b
     for (int f = 0; f < NF; ++f) {
       const int r = 16 * f + row;
       const uint32_t off = (kin && r < q.tn) ? static_cast<uint32_t>((r * q.ldw + k) * 2) : kOutOfRange;
-      wc.v[f][u] = buffer_load16(rsrc, off);
+      dma16(rsrc, slot + (u * NF + f) * 1024, off);
     }
   }
 }
 
 template <int MT, int NF, int U>
-__device__ __forceinline__ void load_x(XChunk<MT, U>& xc, const StreamArgs& a, const Cursor<NF>& q, bool live,
-                                       int lane) {
+__device__ __forceinline__ void dma_x(char* slot, const StreamArgs& a, const Cursor<NF>& q, bool live, int lane) {
   const int n = live ? chunk_steps<NF, U>(q) : 0;
   const auto rsrc = make_rsrc(q.x, static_cast<uint32_t>(a.M * q.ldx * 2));
   const int row = lane & 15;
@@ -245,32 +304,48 @@ __device__ __forceinline__ void load_x(XChunk<MT, U>& xc, const StreamArgs& a, c
     for (int t = 0; t < MT; ++t) {
       const int m = 16 * t + row;
       const uint32_t off = (kin && m < a.M) ? static_cast<uint32_t>((m * q.ldx + k) * 2) : kOutOfRange;
-      xc.v[t][u] = buffer_load16(rsrc, off);
+      dma16(rsrc, slot + (u * MT + t) * 1024, off);
     }
   }
 }
 
-// Steps past the slice multiply zeros: exact, and cheaper than a branch around the MFMAs.
+// vmcnt(n) with the other counters left alone (gfx9 encoding: vmcnt[3:0] | vmcnt_hi[15:14],
+// expcnt[6:4] = 7, lgkmcnt[11:8] = 15).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is six bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Multiplies the chunk in `wslot` / `xslot` into acc.
 template <int DT, int MT, int NF, int U>
-__device__ __forceinline__ void mma(const WChunk<NF, U>& wc, const XChunk<MT, U>& xc, f32x4 (&acc)[NF][MT]) {
+__device__ __forceinline__ void mma_lds(const char* wslot, const char* xslot, f32x4 (&acc)[NF][MT], int lane) {
 #pragma unroll
-  for (int u = 0; u < U; ++u)
+  for (int u = 0; u < U; ++u) {
+    u32x4 wv[NF], xv[MT];
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+      wv[f] = *(const LdsVec*)(wslot + (u * NF + f) * 1024 + lane * 16);
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+      xv[t] = *(const LdsVec*)(xslot + (u * MT + t) * 1024 + lane * 16);
 #pragma unroll
     for (int f = 0; f < NF; ++f)
 #pragma unroll
-      for (int t = 0; t < MT; ++t) acc[f][t] = mfma_16x16x32<DT>(wc.v[f][u], xc.v[t][u], acc[f][t]);
+      for (int t = 0; t < MT; ++t) acc[f][t] = mfma_16x16x32<DT>(wv[f], xv[t], acc[f][t]);
+  }
 }
 
-// Spill layout: float4 slots [buf][wave][f][t][lane]; lane l's acc[f][t] holds weight rows
-// 16f + 4(l/16) .. +3 (four consecutive Y columns) for X row 16t + l%16.
+// Spill slot of tile `half` (0, 1): lane l's acc[f][t] holds weight rows 16f + 4(l/16) .. +3
+// (four consecutive Y columns) for X row 16t + l%16.
 template <int MT, int NF>
-__device__ __forceinline__ f32x4* spill_slot(float* red, int buf, int wave, int f, int t, int lane) {
-  return reinterpret_cast<f32x4*>(red) + (((buf * kStreamKW + wave) * NF + f) * MT + t) * 64 + lane;
+__device__ __forceinline__ f32x4* spill_slot(char* spill, int half, int f, int t, int lane) {
+  return reinterpret_cast<f32x4*>(spill) + ((half * NF + f) * MT + t) * 64 + lane;
 }
 
 // The first X chunk of an item that depends on earlier linears may only be read once the
 // epilogue wavefront has seen the producer tiles finished; it publishes the item's sequence
-// number in `ready` after this workgroup's previous item is through B1.
+// number in `ready` after this workgroup's previous item is through its barriers.
 template <int NF>
 __device__ __forceinline__ bool deferred_x(const Cursor<NF>& q) {
   return q.c == 0 && q.dep >= 0;
@@ -282,77 +357,106 @@ __device__ __forceinline__ void wait_ready(LdsFlag* ready, int seq) {
   for (int i = 0; *ready < seq && i < (1 << 26); ++i) __builtin_amdgcn_s_sleep(2);
 }
 
-// One iteration of a compute wavefront: multiply chunk `q` (weights `wc`, X `xc`, both loaded one
-// iteration earlier) while the next chunk `nq`'s weights and X are in flight into `wn`/`xn`.
-// A deferred X chunk (see deferred_x) is loaded after B1, at the end of the iteration before it.
-template <int DT, int MT, int NF, int U>
-__device__ __forceinline__ void compute_step(const StreamArgs& a, const Cursor<NF>& q, const WChunk<NF, U>& wc,
-                                             const XChunk<MT, U>& xc, const Cursor<NF>& nq, bool has_next,
-                                             WChunk<NF, U>& wn, XChunk<MT, U>& xn, f32x4 (&acc)[NF][MT], int& seq,
-                                             float* red, LdsFlag* ready, int wave, int lane) {
-  // Issue order matters: vmcnt retires loads in issue order, so the loads this iteration
-  // multiplies are all older than the prefetch, and the MFMAs wait for them alone. The prefetch
-  // is issued even past the last chunk (as out-of-range loads that touch no memory): a branch
-  // around it would make the compiler's wait assume the shorter path. The scheduling barriers
-  // keep the compiler from reordering the groups.
-  const bool defer = has_next && deferred_x<NF>(nq);
-  __builtin_amdgcn_sched_barrier(0);
-  load_x<MT, NF, U>(xn, a, nq, has_next && !defer, lane);
-  load_w<NF, U>(wn, nq, has_next, lane);
-  __builtin_amdgcn_sched_barrier(0);
-  mma<DT, MT, NF, U>(wc, xc, acc);
-  if (q.c == q.C - 1) {
+// Workgroup barrier for the item hand-off through LDS: this wavefront's LDS writes are complete,
+// then s_barrier. Unlike __syncthreads() it does not wait for outstanding vector memory
+// operations, so the weight ring's DMA stays in flight across it (a workgroup-scope release
+// fence would also wait for the DMA writes into LDS). The memory clobber keeps the compiler
+// from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// End of an item: the four partial tiles become (w0 + w1) and (w2 + w3) in the spill area.
+//   B1: wavefronts 1 and 3 have spilled; 0 and 2 add them and spill the sums in their place.
+//   B2: both sums are in LDS; the epilogue wavefront reads them.
+//   B3: the epilogue wavefront has read them; the area is free for the next item.
+template <int MT, int NF>
+__device__ __forceinline__ void reduce_item(f32x4 (&acc)[NF][MT], char* spill, int wave, int lane) {
+  const int half = wave >> 1;
+  if (wave & 1) {
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) *spill_slot<MT, NF>(spill, half, f, t, lane) = acc[f][t];
+  }
+  lds_barrier();  // B1
+  if (!(wave & 1)) {
 #pragma unroll
     for (int f = 0; f < NF; ++f)
 #pragma unroll
       for (int t = 0; t < MT; ++t) {
-        *spill_slot<MT, NF>(red, seq & 1, wave, f, t, lane) = acc[f][t];
-        acc[f][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4* slot = spill_slot<MT, NF>(spill, half, f, t, lane);
+        *slot = acc[f][t] + *slot;
       }
-    __syncthreads();  // B1: the item's partials are in LDS
-    ++seq;
   }
-  if (defer) {
-    wait_ready(ready, seq);
-    load_x<MT, NF, U>(xn, a, nq, true, lane);
-  }
+  lds_barrier();  // B2
+#pragma unroll
+  for (int f = 0; f < NF; ++f)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[f][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  lds_barrier();  // B3
 }
 
 template <int DT, int MT, int NF, int U>
-__device__ void compute_role(const StreamArgs& a, int wave, int lane, float* red, LdsFlag* ready) {
-  Cursor<NF> q, nq;
-  WChunk<NF, U> wa, wb;
-  XChunk<MT, U> xa, xb;
+__device__ void compute_role(const StreamArgs& a, int wave, int lane, float* lds, LdsFlag* ready) {
+  constexpr int R = ring_slots<MT, NF, U>();
+  // Loads issued per chunk: X for the next chunk, then weights R-1 chunks ahead. Iteration i
+  // issues X(i+1) and W(i+R-1), so chunk i's X and weights have at least kPerChunk loads issued
+  // after them. When X(i) went out in iteration i-1 ahead of that iteration's weights W(i+R-2),
+  // another NF*U loads follow it, and W(i) itself is older than X(i) only if it was not among
+  // them, i.e. if R >= 3; a two-slot ring always waits for the late count.
+  constexpr int kPerChunk = (MT + NF) * U;
+  constexpr int kWaitLate = kPerChunk > 63 ? 63 : kPerChunk;
+  constexpr int kWaitEarly = R < 3 ? kWaitLate : (kPerChunk + NF * U > 63 ? 63 : kPerChunk + NF * U);
+  const Rings rg = rings_of<MT, NF, U>(lds, wave);
+  Cursor<NF> q, nq, lq;
   f32x4 acc[NF][MT];
 #pragma unroll
   for (int f = 0; f < NF; ++f)
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[f][t] = f32x4{0.f, 0.f, 0.f, 0.f};
   int seq = 0;
-  bool have = first<NF, U>(a, q, wave);
-  if (have) {
-    // The same issue pattern as a step's prefetch, so the loop is entered in the state it loops in.
-    const bool defer = deferred_x<NF>(q);
-    __builtin_amdgcn_sched_barrier(0);
-    load_x<MT, NF, U>(xa, a, q, !defer, lane);
-    load_w<NF, U>(wa, q, true, lane);
-    __builtin_amdgcn_sched_barrier(0);
-    if (defer) {
-      wait_ready(ready, 0);
-      load_x<MT, NF, U>(xa, a, q, true, lane);
-    }
+  if (!first<NF, U>(a, q, wave)) return;
+  // Prologue: weights of the first R-1 chunks, X of the first.
+  lq = q;
+  bool lq_live = true;
+#pragma unroll
+  for (int i = 0; i < R - 1; ++i) {
+    dma_w<NF, U>(rg.w + i * wslot_bytes<NF, U>(), lq, lq_live, lane);
+    if (lq_live) lq_live = advance<NF, U>(a, lq, wave);
   }
-  while (have) {
+  if (deferred_x<NF>(q)) wait_ready(ready, 0);
+  dma_x<MT, NF, U>(rg.x, a, q, true, lane);
+  bool x_late = true;  // X of chunk 0 was issued after every weight load before it
+  for (int i = 0;; ++i) {
     nq = q;
-    bool has_next = advance<NF, U>(a, nq, wave);
-    compute_step<DT, MT, NF, U>(a, q, wa, xa, nq, has_next, wb, xb, acc, seq, red, ready, wave, lane);
+    const bool has_next = advance<NF, U>(a, nq, wave);
+    const bool defer = has_next && deferred_x<NF>(nq);
+    char* xnext = rg.x + ((i + 1) & 1) * xslot_bytes<MT, U>();
+    __builtin_amdgcn_sched_barrier(0);
+    dma_x<MT, NF, U>(xnext, a, nq, has_next && !defer, lane);
+    dma_w<NF, U>(rg.w + ((i + R - 1) % R) * wslot_bytes<NF, U>(), lq, lq_live, lane);
+    if (lq_live) lq_live = advance<NF, U>(a, lq, wave);
+    // This chunk's X and weights are in LDS once at most this many later loads are pending:
+    // this iteration's, plus the previous iteration's weights when X was issued before them.
+    if (x_late)
+      wait_vmcnt<kWaitLate>();
+    else
+      wait_vmcnt<kWaitEarly>();
+    x_late = defer;
+    __builtin_amdgcn_sched_barrier(0);
+    mma_lds<DT, MT, NF, U>(rg.w + (i % R) * wslot_bytes<NF, U>(), rg.x + (i & 1) * xslot_bytes<MT, U>(), acc, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    if (q.c == q.C - 1) {
+      reduce_item<MT, NF>(acc, rg.spill, wave, lane);
+      ++seq;
+    }
     if (!has_next) break;
+    if (defer) {
+      wait_ready(ready, seq);
+      dma_x<MT, NF, U>(xnext, a, nq, true, lane);
+    }
     q = nq;
-    has_next = advance<NF, U>(a, nq, wave);
-    compute_step<DT, MT, NF, U>(a, q, wb, xb, nq, has_next, wa, xa, acc, seq, red, ready, wave, lane);
-    q = nq;
-    have = has_next;
   }
+  wait_vmcnt<0>();  // no DMA into LDS may outlive the wavefront
 }
 
 // ------------------------------------------------------------------ epilogue wavefront
@@ -406,10 +510,12 @@ __device__ __forceinline__ void store_y4(const plm_chain_gemm& g, int m, int n, 
 }
 
 template <int DT, int MT, int NF>
-__device__ void epilogue_role(const StreamArgs& a, int lane, float* red, LdsFlag* ready) {
+__device__ void epilogue_role(const StreamArgs& a, int lane, float* lds, LdsFlag* ready) {
   constexpr int TN = 16 * NF;
   constexpr int GROUPS = TN / 4;         // four-column groups per tile row
   constexpr int ROWS_PER_PASS = 64 / GROUPS;
+  constexpr int PASSES = (16 * MT + ROWS_PER_PASS - 1) / ROWS_PER_PASS;
+  char* spill = reinterpret_cast<char*>(lds);
   const int epoch = a.sync ? lane0_broadcast(lane == 0 ? collect(a.counters + kEpochSlot) : 0) : 0;
   const int cg = lane % GROUPS;          // this lane's column group
   const int f = cg / 4, qd = cg % 4;     // fragment and lane quarter that hold it
@@ -440,41 +546,34 @@ __device__ void epilogue_role(const StreamArgs& a, int lane, float* red, LdsFlag
         }
       }
       if (lane == 0) *ready = seq;
-      __syncthreads();  // B1: the compute wavefronts' partials of this item are in LDS
-      const int buf = seq & 1;
+      lds_barrier();  // B1: wavefronts 1 and 3 have spilled
+      lds_barrier();  // B2: the pair sums are in LDS
       ++seq;
+      // The item's tile is (w0 + w1) + (w2 + w3). Pass p covers rows ROWS_PER_PASS * p + lane /
+      // GROUPS, columns 4 * cg .. +3. Its stores are issued before B3 releases the spill area.
       const bool coherent = g.consumed != 0;
-      if (g.split_k == 1) {
-        for (int m0 = 0; m0 < a.M; m0 += ROWS_PER_PASS) {
-          const int m = m0 + lane / GROUPS;
-          const int n = 4 * cg;
-          if (m < a.M && n < tn) {
-            const int t = m >> 4, l = 16 * qd + (m & 15);
-            f32x4 v = *spill_slot<MT, NF>(red, buf, 0, f, t, l);
+      const int n = 4 * cg;
+      const int Np = (g.N + 3) & ~3;  // split partial planes are [M][Np] fp32
+      const uint32_t plane = static_cast<uint32_t>(a.M) * Np * 4u;
+      const auto prs = make_rsrc(a.partial + g.partial_offset, g.split_k > 1 ? plane * g.split_k : 0u);
 #pragma unroll
-            for (int w = 1; w < kStreamKW; ++w) v += *spill_slot<MT, NF>(red, buf, w, f, t, l);
+      for (int p = 0; p < PASSES; ++p) {
+        const int m = p * ROWS_PER_PASS + lane / GROUPS;
+        if (m < a.M && n < tn) {
+          const int t = m >> 4, l = 16 * qd + (m & 15);
+          const f32x4 v = *spill_slot<MT, NF>(spill, 0, f, t, l) + *spill_slot<MT, NF>(spill, 1, f, t, l);
+          if (g.split_k == 1) {
             store_y4<DT>(g, m, n0 + n, tn - n, v, coherent);
-          }
-        }
-      } else {
-        // Publish this split's partial, then the last of the tile's splits to arrive sums all of
-        // them in split order. Partial planes are [M][Np] fp32 with Np = N rounded up to 4, so
-        // every four-column group is one 16-byte device-coherent access.
-        const int Np = (g.N + 3) & ~3;
-        const uint32_t plane = static_cast<uint32_t>(a.M) * Np * 4u;  // bytes
-        const auto prs = make_rsrc(a.partial + g.partial_offset, plane * g.split_k);
-        for (int m0 = 0; m0 < a.M; m0 += ROWS_PER_PASS) {
-          const int m = m0 + lane / GROUPS;
-          const int n = 4 * cg;
-          if (m < a.M && n < tn) {
-            const int t = m >> 4, l = 16 * qd + (m & 15);
-            f32x4 v = *spill_slot<MT, NF>(red, buf, 0, f, t, l);
-#pragma unroll
-            for (int w = 1; w < kStreamKW; ++w) v += *spill_slot<MT, NF>(red, buf, w, f, t, l);
+          } else {
+            // Every four-column group of a partial is one 16-byte device-coherent store.
             const uint32_t off = s * plane + (static_cast<uint32_t>(m) * Np + n0 + n) * 4u;
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), prs, off, 0, kCoherent);
           }
         }
+      }
+      lds_barrier();  // B3: the spill area is free again
+      if (g.split_k > 1) {
+        // The last of the tile's splits to arrive sums all of them in split order.
         __builtin_amdgcn_s_waitcnt(0);  // the partial is written through before we count in
         int* counter = a.counters + g.arrive_base + tile;
         int before = 0;
@@ -484,41 +583,33 @@ __device__ void epilogue_role(const StreamArgs& a, int lane, float* red, LdsFlag
         }
         before = lane0_broadcast(before);
         if (before != g.split_k - 1) continue;
-        // Rows in blocks of PASSES passes, splits in groups of 8: all loads of a block are issued
-        // before the first add, then summed in split order.
-        constexpr int PASSES = 2;
-        for (int m0 = 0; m0 < a.M; m0 += ROWS_PER_PASS * PASSES) {
-          f32x4 acc4[PASSES];
-          uint32_t off[PASSES];
-          bool live[PASSES];
+        // Four passes at a time, each summing its splits in order; the four passes' loads of one
+        // split are in flight together.
+        constexpr int BATCH = 4;
+        for (int p0 = 0; p0 < PASSES; p0 += BATCH) {
+          f32x4 sum[BATCH];
+          uint32_t off[BATCH];
 #pragma unroll
-          for (int p = 0; p < PASSES; ++p) {
-            const int m = m0 + p * ROWS_PER_PASS + lane / GROUPS;
-            live[p] = m < a.M && 4 * cg < tn;
-            off[p] = live[p] ? (static_cast<uint32_t>(m) * Np + n0 + 4 * cg) * 4u : kOutOfRange;
-            acc4[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+          for (int b = 0; b < BATCH; ++b) {
+            const int m = (p0 + b) * ROWS_PER_PASS + lane / GROUPS;
+            off[b] = (m < a.M && n < tn) ? (static_cast<uint32_t>(m) * Np + n0 + n) * 4u : kOutOfRange;
+            sum[b] = f32x4{0.f, 0.f, 0.f, 0.f};
           }
-          for (int q0 = 0; q0 < g.split_k; q0 += 8) {
-            u32x4 part[8][PASSES];
+          for (int q = 0; q < g.split_k; ++q) {
+            u32x4 part[BATCH];
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
+            for (int b = 0; b < BATCH; ++b)
+              part[b] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      prs, off[b] == kOutOfRange ? kOutOfRange : off[b] + q * plane, 0,
+                                                      kCoherent));
 #pragma unroll
-              for (int p = 0; p < PASSES; ++p)
-                if (q0 + i < g.split_k)
-                  part[i][p] = __builtin_bit_cast(
-                      u32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, off[p] + (q0 + i) * plane, 0, kCoherent));
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-#pragma unroll
-              for (int p = 0; p < PASSES; ++p)
-                if (q0 + i < g.split_k) acc4[p] += __builtin_bit_cast(f32x4, part[i][p]);
+            for (int b = 0; b < BATCH; ++b) sum[b] += __builtin_bit_cast(f32x4, part[b]);
           }
 #pragma unroll
-          for (int p = 0; p < PASSES; ++p)
-            if (live[p]) {
-              const int m = m0 + p * ROWS_PER_PASS + lane / GROUPS;
-              store_y4<DT>(g, m, n0 + 4 * cg, tn - 4 * cg, acc4[p], coherent);
-            }
+          for (int b = 0; b < BATCH; ++b) {
+            const int m = (p0 + b) * ROWS_PER_PASS + lane / GROUPS;
+            if (m < a.M && n < tn) store_y4<DT>(g, m, n0 + n, tn - n, sum[b], coherent);
+          }
         }
       }
       if (g.consumed) {
@@ -551,32 +642,26 @@ __global__ __launch_bounds__(64 * (kStreamKW + 1)) void stream_gemm_kernel(Strea
     const int words = a.count * static_cast<int>(sizeof(plm_chain_gemm) / sizeof(int));
     for (int i = threadIdx.x; i < words; i += blockDim.x) dst[i] = src[i];
   }
-  float* red = stream_lds + table_bytes(a.count) / sizeof(float);
+  float* lds = stream_lds + table_bytes(a.count) / sizeof(float);
   if (threadIdx.x == 0) ready = -1;
   __syncthreads();
   LdsFlag* flag = (LdsFlag*)&ready;
   if (wave < kStreamKW)
-    compute_role<DT, MT, NF, U>(a, wave, lane, red, flag);
+    compute_role<DT, MT, NF, U>(a, wave, lane, lds, flag);
   else
-    epilogue_role<DT, MT, NF>(a, lane, red, flag);
+    epilogue_role<DT, MT, NF>(a, lane, lds, flag);
 }
 
-// Compiled tile set: LDS holds two spill buffers (2 * KW * NF * MT KiB), and the compute
-// wavefronts' registers (double-buffered weight and X chunks, accumulators) fit in 256 VGPRs
-// so that the epilogue wavefront can share a SIMD with a compute wavefront.
+// Compiled tile set: the weight ring is at least two chunks deep beside the spill area and the X
+// rings, and the compute wavefronts' registers (accumulators, one step's operands) fit in 256
+// VGPRs so that the epilogue wavefront can share a SIMD with a compute wavefront.
 template <int MT, int NF, int U>
 constexpr bool stream_compiled() {
   if (MT < 1 || MT > 8) return false;
   if (NF != 1 && NF != 2 && NF != 4) return false;
   if (U != 1 && U != 2 && U != 4) return false;
-  if (kStreamKW * NF * MT > 64) return false;
-  const int vgprs = 2 * NF * U * 4 + 2 * MT * U * 4 + NF * MT * 4 + 48;
-  return vgprs <= 256;
-}
-
-template <int MT, int NF>
-constexpr size_t stream_lds_bytes() {
-  return static_cast<size_t>(2) * kStreamKW * NF * MT * 64 * sizeof(f32x4);
+  if (ring_slots<MT, NF, U>() < 2) return false;
+  return NF * MT * 4 + (NF + MT) * 4 + 64 <= 256;
 }
 
 hipError_t stream_dispatch_bf16(StreamArgs& a, int nf, int u, int cus, hipStream_t s, bool dry);
@@ -590,7 +675,7 @@ hipError_t stream_launch(StreamArgs& a, int cus, hipStream_t stream, bool dry) {
   } else {
     if (dry) return hipSuccess;
     auto kern = stream_gemm_kernel<DT, MT, NF, U>;
-    const size_t lds = table_bytes(a.count) + stream_lds_bytes<MT, NF>();
+    const size_t lds = table_bytes(a.count) + stream_lds_bytes<MT, NF, U>();
     if (lds > kMaxLdsBytes) return hipErrorInvalidConfiguration;
     static size_t lds_allowed = 64 * 1024;  // the default dynamic LDS limit
     if (lds > lds_allowed) {

@@ -9,8 +9,9 @@
 // D[row = 4*(l/16) + r][col = l%16], i.e. weight row n0 + 16f + 4*(l/16) + r and X row 16t + l%16.
 //
 // Bit-identity contract: wave_mma() visits K steps in ascending order and wg_sum() adds the
-// wavefronts' partials in wave order, so any kernel that calls them with the same tile geometry
-// and K partition produces the same fp32 value for an element, whatever the other rows hold.
+// wavefronts' partials in a fixed order, so any kernel that calls them with the same tile
+// geometry and K partition produces the same fp32 value for an element, whatever the other rows
+// hold.
 // The verify step relies on this to recompute a proposal's own logit outside the main pass.
 #pragma once
 
@@ -232,10 +233,14 @@ __device__ __forceinline__ int red_offset(int n_local, int m_local) {
   return ((f * MT + t) * 4 + (i & 3)) * 64 + (i >> 2) * 16 + mm;
 }
 
-// Sum of the k_waves partials of one element, in wave order.
+// Sum of the wavefronts' partials of one element. With four wavefronts it is
+// (w0 + w1) + (w2 + w3), the order the streaming GEMM's pairwise LDS reduction produces, so the
+// verify step's logits are bit for bit plm_gemm_f32out's; otherwise in wave order.
 template <int MT, int NF>
 __device__ __forceinline__ float wg_sum(const float* red, int k_waves, int off) {
   constexpr int per_wave = NF * MT * 256;
+  if (k_waves == 4)
+    return (red[off] + red[per_wave + off]) + (red[2 * per_wave + off] + red[3 * per_wave + off]);
   float s = red[off];
   for (int w = 1; w < k_waves; ++w) s += red[w * per_wave + off];
   return s;

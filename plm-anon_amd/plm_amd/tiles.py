@@ -18,16 +18,25 @@ UNROLLS = (1, 2, 4)
 SPLITS = (1, 2, 3, 4, 6, 8)
 
 
+def ring_slots(M: int, cfg: dict) -> int:
+    """Depth of each compute wavefront's weight ring in LDS (mirrors ``ring_slots`` in
+    csrc/stream_gemm.h): what fits beside the spill area (two partial tiles), the X rings (two
+    chunks per wavefront) and a 16 KiB descriptor reserve, at most 8."""
+    mt, nf, u = math.ceil(M / 16), cfg["wave_frags"], cfg["unroll"]
+    avail = 160 * 1024 - 256 - 16 * 1024 - 2 * nf * mt * 1024 - K_WAVES * 2 * mt * u * 1024
+    return min(8, avail // (K_WAVES * nf * u * 1024))
+
+
 def compiled(M: int, cfg: dict) -> bool:
     """Whether the library has a kernel for this tile at width M (mirrors ``stream_compiled`` in
-    csrc/stream_gemm.h: two LDS spill buffers of 4*NF*MT KiB, and the compute wavefronts'
-    registers (double-buffered weight and X chunks, accumulators) within 256 VGPRs)."""
+    csrc/stream_gemm.h: a weight ring at least two chunks deep, and the compute wavefronts'
+    registers within 256 VGPRs)."""
     mt, nf, u = math.ceil(M / 16), cfg["wave_frags"], cfg["unroll"]
     if not (1 <= mt <= 8 and nf in WAVE_FRAGS and u in UNROLLS and cfg["k_waves"] == K_WAVES):
         return False
-    if K_WAVES * nf * mt > 64:
+    if ring_slots(M, cfg) < 2:
         return False
-    return 2 * nf * u * 4 + 2 * mt * u * 4 + nf * mt * 4 + 48 <= 256
+    return nf * mt * 4 + (nf + mt) * 4 + 64 <= 256
 
 
 def items(N: int, cfg: dict) -> int:
@@ -62,7 +71,7 @@ def heuristic_tile(M: int, N: int, K: int, supported=None) -> dict:
     four K steps per item."""
     steps = math.ceil(K / 32)
     for nf in (4, 2, 1):
-        for u in (4, 2):
+        for u in (4, 2, 1):
             tiles = math.ceil(N / (16 * nf))
             split = 1
             while tiles * split < CU_COUNT and steps // (2 * split * K_WAVES) >= 4 and split < 8:
@@ -75,6 +84,16 @@ def heuristic_tile(M: int, N: int, K: int, supported=None) -> dict:
 
 # Tile of a chained round (plm_gemm_chain): 64-row tiles, as a consumed output needs.
 CHAIN_TILE = {"wave_frags": 4, "k_waves": K_WAVES, "split_k": 1, "unroll": 2}
+
+
+def chain_tile(M: int) -> dict:
+    """CHAIN_TILE at width M, with the unroll lowered until the weight ring fits in LDS (at M > 48
+    two-step chunks leave room for only one ring slot)."""
+    for u in (2, 1):
+        cfg = dict(CHAIN_TILE, unroll=u)
+        if compiled(M, cfg):
+            return cfg
+    raise ValueError(f"no chain tile is compiled at M={M}")
 
 
 def chain_split(N: int, K: int, cfg: dict = CHAIN_TILE, workgroups: int = CU_COUNT) -> int:

@@ -14,11 +14,12 @@ import oracle
 from plm_amd import workloads
 from plm_amd.chain import Link, LinearChain
 from plm_amd.fast_gemm import hip_linear
+from plm_amd.tiles import chain_tile
 
 pytestmark = pytest.mark.gpu
 
 RTOL, ATOL = 1e-3, 2e-2
-CFG = {"wave_frags": 4, "k_waves": 4, "split_k": 1, "unroll": 2}
+CFG = chain_tile(56)
 
 
 def _weights(shapes, seed, device, dtype=torch.bfloat16):
