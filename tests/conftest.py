@@ -13,6 +13,26 @@ for path in (REPO, REPO / "plm-anon_amd"):
         sys.path.insert(0, str(path))
 
 
+GOLDEN = REPO / "tests" / "golden"
+
+
+def load_golden(name: str) -> dict:
+    """A fixture written by tests/golden/make_golden.py: half-precision arrays come back as bf16
+    tensors (they are stored as uint16 bit patterns), everything else as numpy arrays."""
+    import numpy as np
+    import torch
+
+    with np.load(GOLDEN / f"{name}.npz", allow_pickle=False) as z:
+        out = {k: z[k] for k in z.files}
+    for k in ("x", "w"):
+        out[k] = torch.from_numpy(out[k].view(np.int16).copy()).view(torch.bfloat16)
+    return out
+
+
+def golden_names(prefix: str) -> list[str]:
+    return sorted(p.stem for p in GOLDEN.glob(f"{prefix}*.npz"))
+
+
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP kernels)")
 

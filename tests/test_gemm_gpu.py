@@ -18,6 +18,7 @@ import pytest
 import torch
 
 import oracle
+from conftest import golden_names, load_golden
 from plm_amd import fast_gemm, gemm_tables, tiles, tune, workloads
 from plm_amd.fast_gemm import hip_linear, hip_linear_f32
 
@@ -273,3 +274,24 @@ def test_wide_workgroup_count_stays_in_bounds(device):
     assert math.ceil(N / 16) * 2 > 4096
     cols = torch.cat([torch.arange(0, 64), torch.arange(N - 64, N)])
     check_cols(hip_linear(x, w, cfg), x, w, cols)
+
+
+@pytest.mark.parametrize("name", golden_names("gemm_"))
+def test_golden_fixtures(device, name):
+    """The committed fp64 fixtures, through the tile table's kind of tile (heuristic) and a split-K
+    tile: within one rounding of the exact product (bit-exact for the small-integer case)."""
+    z = load_golden(name)
+    x, w = z["x"], z["w"]
+    M, K = x.shape
+    N = w.shape[0]
+    supported = lambda c: fast_gemm.tile_supported(M, K, c)  # noqa: E731
+    for cfg in (tiles.heuristic_tile(M, N, K, supported=supported),
+                {"wave_frags": 1, "k_waves": 4, "split_k": 2, "unroll": 1}):
+        y = _run(x, w, cfg, device).cpu()
+        got = y.view(torch.int16).numpy().view("uint16")
+        if name.endswith("_int"):
+            assert (got == z["y_bf16"]).all(), cfg
+        else:
+            _within_one_rounding(y.float(), x, w)
+            steps = abs(got.astype("int32") - z["y_bf16"].astype("int32"))
+            assert steps.max() <= 1 and (steps > 0).mean() <= 2e-3, (cfg, int((steps > 0).sum()))

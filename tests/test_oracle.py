@@ -9,6 +9,7 @@ import pytest
 import torch
 
 import oracle
+from conftest import golden_names, load_golden
 from oracle import plm_oracle as po
 
 
@@ -238,3 +239,49 @@ def test_planted_mistakes_are_caught():
     for kwargs in ({"ge": True}, {"le": True}):
         assert any(mutant(lg, pd, p, **kwargs).item() != oracle.nucleus_acceptance(lg, pd, p).item()
                    for lg, pd, p in cases), kwargs
+
+
+# --------------------------------------------------------------------------- golden fixtures
+
+
+@pytest.mark.parametrize("name", golden_names("gemm_"))
+def test_golden_gemm(name):
+    """The oracle against the committed fp64 fixtures: the fp32 product within fp32 accumulation
+    error of the exact one, and the bf16 output the correctly rounded value except where fp32
+    accumulation lands on the other side of a rounding midpoint (at most one step, rarely)."""
+    z = load_golden(name)
+    x, w = z["x"], z["w"]
+    exact = z["y_fp64"]
+    absdot = x.double().abs().numpy() @ w.double().abs().numpy().T
+    f32 = oracle.linear_fp32(x, w).double().numpy()
+    assert np.all(np.abs(f32 - exact) <= 2.0 ** -20 * absdot + 1e-30)
+    got = oracle.linear(x, w).contiguous().view(torch.int16).numpy().view(np.uint16)
+    want = z["y_bf16"]
+    if name.endswith("_int"):
+        assert np.array_equal(got, want)
+    else:
+        step = np.abs(got.astype(np.int32) - want.astype(np.int32))
+        assert step.max() <= 1 and (step > 0).mean() <= 1e-3, (step.max(), (step > 0).sum())
+
+
+def test_golden_bf16_rounding_matches_torch():
+    """The fixtures' own fp64 -> bf16 rounding agrees with torch's round-to-nearest-even."""
+    for name in golden_names("gemm_"):
+        z = load_golden(name)
+        torch_bits = torch.from_numpy(z["y_fp64"]).float().bfloat16().view(torch.int16).numpy().view(np.uint16)
+        assert np.array_equal(torch_bits, z["y_bf16"]), name
+
+
+@pytest.mark.parametrize("name", golden_names("verify_"))
+def test_golden_verify(name):
+    z = load_golden(name)
+    pending = torch.from_numpy(z["pending"])
+    logits = oracle.linear_fp32(z["x"], z["w"])
+    acc, am = oracle.verify(logits, pending, float(z["p"]))
+    safe_acc, safe_am = torch.from_numpy(z["safe_accept"]), torch.from_numpy(z["safe_argmax"])
+    assert torch.equal(acc[safe_acc], torch.from_numpy(z["accept"])[safe_acc])
+    assert torch.equal(am[safe_am], torch.from_numpy(z["argmax"])[safe_am])
+    # The fp64 brute force on fp64 logits reproduces every row, safe or not.
+    exact = torch.from_numpy(z["x"].double().numpy() @ z["w"].double().numpy().T)
+    assert np.array_equal(po.nucleus_acceptance_fp64(exact, pending, float(z["p"])), z["accept"])
+    assert 0 < int(z["accept"].sum()) < len(z["accept"])

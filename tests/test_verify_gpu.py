@@ -13,6 +13,7 @@ import pytest
 import torch
 
 import oracle
+from conftest import golden_names, load_golden
 from oracle import plm_oracle as po
 from plm_amd import _lib, fast_gemm, workloads
 from plm_amd.fast_gemm import hip_linear_f32
@@ -167,3 +168,19 @@ def test_graph_capture(device):
         assert torch.equal(acc, eager_acc) and torch.equal(am, eager_am)
         lm_head_verify(x, w, pending, P)
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("name", golden_names("verify_"))
+def test_golden_fixture(device, name):
+    """The committed fp64 fixture: accept bits and argmax ids on every row the fixture marks as
+    clear of rounding-sensitive boundaries."""
+    import numpy as np
+
+    z = load_golden(name)
+    x, w = z["x"].to(device), z["w"].to(device)
+    pending = torch.from_numpy(z["pending"]).to(device)
+    acc, am = lm_head_verify(x, w, pending, float(z["p"]), "fp32")
+    acc, am = acc.cpu().numpy(), am.cpu().numpy()
+    sa, sm = z["safe_accept"], z["safe_argmax"]
+    assert np.array_equal(acc[sa], z["accept"][sa])
+    assert np.array_equal(am[sm], z["argmax"][sm])
