@@ -50,14 +50,14 @@ enum plm_status {
 /*
  * Tile configuration of one GEMM shape: the MI355X counterpart of the reference's
  * {BLOCK_M, BLOCK_N, BLOCK_K, SPLIT_K, num_warps, num_stages} dict (plm/fast_gemm.py:64).
- *   wave_frags : 16-row weight fragments per tile (1, 2 or 4); the tile is 16*wave_frags rows of W.
- *   k_waves    : compute wavefronts per workgroup (4); each takes a contiguous K slice of the tile
- *                and their partials are summed through LDS in wave order. A fifth wavefront runs
- *                the epilogue.
- *   split_k    : workgroups splitting K further; their fp32 partials are summed in split order
+ *   wave_frags : 16-row weight fragments per compute wavefront (1, 2 or 4). A workgroup has four
+ *                compute wavefronts, so a tile is 64*wave_frags rows of W; each wavefront owns its
+ *                rows over the whole K range of the tile (no reduction across wavefronts). A fifth
+ *                wavefront runs the epilogue.
+ *   k_waves    : compute wavefronts per workgroup (4).
+ *   split_k    : workgroups splitting K; their fp32 partials are summed in split order
  *                0..split_k-1 by the last workgroup of the tile to finish (no float atomics).
- *   unroll     : 32-wide K steps per weight chunk (1, 2 or 4); each compute wavefront keeps the
- *                next chunk's loads in flight while it multiplies the current one.
+ *   unroll     : 32-wide K steps per streamed chunk (2: one 128-byte line of every weight row).
  */
 typedef struct plm_tile {
   int32_t wave_frags;
@@ -119,8 +119,8 @@ int64_t plm_gemm_chain_prepare(plm_chain_gemm* gemms, int32_t count, int64_t M, 
  * round calls fast_gemm 4L+1 times, plm/decoder.py:312-324). A linear with dep >= 0
  * starts each of its tiles as soon as the producer tiles covering that tile's K range are written,
  * so consecutive linears overlap. `host_gemms` is the prepared array, `device_gemms` a copy of it in
- * device memory (read by the kernel). Requirements as plm_gemm, plus: wave_frags == 4 when any
- * linear has dep >= 0, a consumed Y is 16-bit, 128-byte aligned with ldy a multiple of 64, and no
+ * device memory (read by the kernel). Requirements as plm_gemm, plus: a consumed Y is 16-bit,
+ * 128-byte aligned with ldy a multiple of 64, and no
  * Y overlaps another Y or any X or W of the chain except through dep. Workgroups wait on each
  * other, so the launch needs the device to itself (nothing else running on it).
  */

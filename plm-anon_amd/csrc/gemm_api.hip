@@ -16,12 +16,12 @@ constexpr int64_t kMaxM = 128;
 
 bool tile_valid(const plm_tile* t) {
   return t != nullptr && (t->wave_frags == 1 || t->wave_frags == 2 || t->wave_frags == 4) &&
-         t->k_waves == kStreamKW && (t->unroll == 1 || t->unroll == 2 || t->unroll == 4) && t->split_k >= 1 && t->split_k <= 64;
+         t->k_waves == kStreamKW && t->unroll == kStreamU && t->split_k >= 1 && t->split_k <= 64;
 }
 
 hipError_t dispatch(int32_t dtype, StreamArgs& a, const plm_tile& t, int cus, hipStream_t s, bool dry) {
-  if (dtype == PLM_BF16) return stream_dispatch_bf16(a, t.wave_frags, t.unroll, cus, s, dry);
-  if (dtype == PLM_F16) return stream_dispatch_f16(a, t.wave_frags, t.unroll, cus, s, dry);
+  if (dtype == PLM_BF16) return stream_dispatch_bf16(a, t.wave_frags, cus, s, dry);
+  if (dtype == PLM_F16) return stream_dispatch_f16(a, t.wave_frags, cus, s, dry);
   return hipErrorInvalidConfiguration;
 }
 
@@ -38,7 +38,8 @@ int device_cus() {
   return cached;
 }
 
-int64_t tiles_of(int64_t N, const plm_tile& t) { return (N + 16 * t.wave_frags - 1) / (16 * t.wave_frags); }
+// Tiles of a linear: 64 * wave_frags weight rows each (16 * wave_frags per compute wavefront).
+int64_t tiles_of(int64_t N, const plm_tile& t) { return (N + 64 * t.wave_frags - 1) / (64 * t.wave_frags); }
 
 // Checks one linear's operands; returns PLM_OK or the status to report.
 int check_linear(int32_t dtype, const plm_chain_gemm& g, int64_t M, const plm_tile& t) {
@@ -47,7 +48,7 @@ int check_linear(int32_t dtype, const plm_chain_gemm& g, int64_t M, const plm_ti
   if (M < 1 || M > kMaxM || g.N < 1 || g.K < 8 || g.K % 8 != 0) return PLM_ERR_ARGUMENT;
   if (g.ldx < g.K || g.ldw < g.K || g.ldy < g.N) return PLM_ERR_ARGUMENT;
   if (g.split_k < 1 || g.split_k > 64 || (g.out_f32 != 0 && g.out_f32 != 1)) return PLM_ERR_ARGUMENT;
-  // Buffer offsets are 31-bit: X and one weight tile must each span less than 2 GiB.
+  // Buffer offsets are 31-bit: X and one wavefront's weight rows must each span less than 2 GiB.
   if (M * g.ldx * 2 >= (int64_t(1) << 31) || 16 * t.wave_frags * g.ldw * 2 >= (int64_t(1) << 31)) return PLM_ERR_ARGUMENT;
   if (g.ldx % 8 != 0 || g.ldw % 8 != 0 || !aligned16_ptr(g.x) || !aligned16_ptr(g.w)) return PLM_ERR_ALIGNMENT;
   return PLM_OK;
@@ -186,7 +187,7 @@ int plm_gemm_chain(int32_t dtype, const plm_chain_gemm* host_gemms, const plm_ch
   t.split_k = 1;
   if (!plm::tile_valid(&t)) return PLM_ERR_TILE;
   if (M < 1 || M > plm::kMaxM) return PLM_ERR_ARGUMENT;
-  // The kernel keeps the chain's descriptors in LDS next to its spill buffers.
+  // The kernel keeps the chain's descriptors in LDS next to its staging area.
   if (plm::table_bytes(count) > plm::kTableReserve) return PLM_ERR_ARGUMENT;
   // The derived fields must be what prepare() computes for this chain.
   std::vector<plm_chain_gemm> check(host_gemms, host_gemms + count);
@@ -212,9 +213,9 @@ int plm_gemm_chain(int32_t dtype, const plm_chain_gemm* host_gemms, const plm_ch
       if (g.x != p.y || g.ldx != p.ldy || g.K > p.N) return PLM_ERR_ARGUMENT;
     }
     if (g.consumed) {
-      // Every 128-byte line of a consumed Y is written by one tile: 64-column tiles of 16-bit values
-      // on 128-byte aligned rows.
-      if (g.out_f32 || t.wave_frags != 4) return PLM_ERR_ARGUMENT;
+      // Every 128-byte line of a consumed Y is written by one tile: tiles of 64 * wave_frags
+      // columns of 16-bit values on 128-byte aligned rows.
+      if (g.out_f32) return PLM_ERR_ARGUMENT;
       if ((reinterpret_cast<uintptr_t>(g.y) & 127) != 0 || g.ldy % 64 != 0) return PLM_ERR_ALIGNMENT;
     }
   }

@@ -3,8 +3,8 @@
 
 namespace plm {
 
-hipError_t stream_dispatch_bf16(StreamArgs& a, int nf, int u, int cus, hipStream_t s, bool dry) {
-  return stream_dispatch<DT_BF16>(a, nf, u, cus, s, dry);
+hipError_t stream_dispatch_bf16(StreamArgs& a, int nf, int cus, hipStream_t s, bool dry) {
+  return stream_dispatch<DT_BF16>(a, nf, cus, s, dry);
 }
 
 }  // namespace plm

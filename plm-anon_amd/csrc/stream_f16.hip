@@ -3,8 +3,8 @@
 
 namespace plm {
 
-hipError_t stream_dispatch_f16(StreamArgs& a, int nf, int u, int cus, hipStream_t s, bool dry) {
-  return stream_dispatch<DT_F16>(a, nf, u, cus, s, dry);
+hipError_t stream_dispatch_f16(StreamArgs& a, int nf, int cus, hipStream_t s, bool dry) {
+  return stream_dispatch<DT_F16>(a, nf, cus, s, dry);
 }
 
 }  // namespace plm

@@ -233,14 +233,12 @@ __device__ __forceinline__ int red_offset(int n_local, int m_local) {
   return ((f * MT + t) * 4 + (i & 3)) * 64 + (i >> 2) * 16 + mm;
 }
 
-// Sum of the wavefronts' partials of one element. With four wavefronts it is
-// (w0 + w1) + (w2 + w3), the order the streaming GEMM's pairwise LDS reduction produces, so the
-// verify step's logits are bit for bit plm_gemm_f32out's; otherwise in wave order.
+// Sum of the wavefronts' partials of one element, in wave order starting from the first: the order
+// in which the streaming GEMM's split-K combine adds the partials of the same K slices, so the
+// verify step's logits are bit for bit plm_gemm_f32out's with split_k = k_waves.
 template <int MT, int NF>
 __device__ __forceinline__ float wg_sum(const float* red, int k_waves, int off) {
   constexpr int per_wave = NF * MT * 256;
-  if (k_waves == 4)
-    return (red[off] + red[per_wave + off]) + (red[2 * per_wave + off] + red[3 * per_wave + off]);
   float s = red[off];
   for (int w = 1; w < k_waves; ++w) s += red[w * per_wave + off];
   return s;

@@ -19,8 +19,8 @@ VOCAB_PADDING = 64   # vLLM's ParallelLMHead pads the vocabulary to this multipl
 WIDEST_TUNED_DOWN_ROUND = 72
 # Above W=72 the `down` projection uses this fixed tile instead of the table entry (the reference's
 # override, plm/gemm_tables.py:17-19, 41-42). On MI355X the split-K combine costs no extra launch,
-# so the fixed tile keeps a 4-way split.
-DOWN_SPLIT_K1 = {"wave_frags": 2, "k_waves": 4, "split_k": 4, "unroll": 4}
+# so the fixed tile splits K 8 ways (256 items at hidden 2048); 64-row tiles are compiled up to M=128.
+DOWN_SPLIT_K1 = {"wave_frags": 1, "k_waves": 4, "split_k": 8, "unroll": 2}
 
 
 def model_shapes(hf_config) -> dict[str, tuple[int, int]]:

@@ -42,7 +42,7 @@ def test_status_strings():
 
 def test_argument_validation_happens_before_launch():
     lib = _lib.lib()
-    tile = _lib.Tile(2, 4, 1, 4)
+    tile = _lib.Tile(2, 4, 1, 2)
     fake = 1 << 20  # never dereferenced: every call below fails validation first
     # K not a multiple of 8.
     assert lib.plm_gemm(0, fake, 1024, fake, 1024, fake, 4096, 42, 4096, 1020, tile, None, 0, None) == -1
@@ -71,11 +71,11 @@ def test_workspace_sizes():
     lib = _lib.lib()
     m = re.search(r"#define PLM_WORKSPACE_COUNTER_BYTES \(1u << (\d+)\)", HEADER.read_text())
     assert m and _lib.COUNTER_BYTES == 1 << int(m.group(1))
-    assert lib.plm_gemm_workspace_bytes(56, 2048, 8192, _lib.Tile(2, 4, 1, 4)) == 0
-    n = lib.plm_gemm_workspace_bytes(56, 2048, 8192, _lib.Tile(2, 4, 4, 4))
+    assert lib.plm_gemm_workspace_bytes(56, 2048, 8192, _lib.Tile(2, 4, 1, 2)) == 0
+    n = lib.plm_gemm_workspace_bytes(56, 2048, 8192, _lib.Tile(2, 4, 4, 2))
     assert n == _lib.COUNTER_BYTES + 4 * 56 * 2048 * 4
     # Partial planes pad N to a multiple of 4 floats.
-    assert lib.plm_gemm_workspace_bytes(42, 50257, 1024, _lib.Tile(2, 4, 2, 4)) == _lib.COUNTER_BYTES + (2 * 42 * 50260 + 63) // 64 * 64 * 4
+    assert lib.plm_gemm_workspace_bytes(42, 50257, 1024, _lib.Tile(2, 4, 2, 2)) == _lib.COUNTER_BYTES + (2 * 42 * 50260 + 63) // 64 * 64 * 4
     assert lib.plm_lm_head_verify_workspace_bytes(56, 50257, 2048, _lib.Tile(2, 4, 1, 4)) > 56 * 4
 
 

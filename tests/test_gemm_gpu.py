@@ -158,7 +158,7 @@ def test_workspace_shared_across_shapes_and_entry_points(device):
     cases = [((56, 6144, 2048), {"wave_frags": 2, "k_waves": 4, "split_k": 4, "unroll": 2}),
              ((56, 8192, 2048), {"wave_frags": 2, "k_waves": 4, "split_k": 2, "unroll": 2}),
              ((56, 2048, 2048), {"wave_frags": 1, "k_waves": 4, "split_k": 8, "unroll": 2}),
-             ((56, 8192, 2048), {"wave_frags": 4, "k_waves": 4, "split_k": 2, "unroll": 1})]
+             ((56, 8192, 2048), {"wave_frags": 1, "k_waves": 4, "split_k": 3, "unroll": 2})]
     for i, ((M, N, K), cfg) in enumerate(cases):
         x, w = _inputs(M, N, K, 40 + i)
         check(_run(x, w, cfg, device), x, w)
@@ -170,7 +170,7 @@ def test_fp16(device):
     M, N, K = 56, 3072, 2048
     x, w = _inputs(M, N, K, 7, torch.float16)
     for cfg in ({"wave_frags": 2, "k_waves": 4, "split_k": 2, "unroll": 2},
-                {"wave_frags": 4, "k_waves": 4, "split_k": 1, "unroll": 1}):
+                {"wave_frags": 1, "k_waves": 4, "split_k": 1, "unroll": 2}):
         check(_run(x, w, cfg, device), x, w)
 
 
@@ -193,7 +193,7 @@ def test_one_hot_weight_selects_columns(device):
     cols = torch.tensor([0, 5, 1023, 512, 77, 31, 32, 999])
     w = torch.zeros(len(cols), K).bfloat16()
     w[torch.arange(len(cols)), cols] = 1.0
-    y = _run(x, w, {"wave_frags": 1, "k_waves": 4, "split_k": 1, "unroll": 4}, device)
+    y = _run(x, w, {"wave_frags": 1, "k_waves": 4, "split_k": 1, "unroll": 2}, device)
     assert torch.equal(y.cpu(), x[:, cols])
 
 
@@ -266,12 +266,12 @@ def test_graph_capture_and_replay(device):
 
 
 def test_wide_workgroup_count_stays_in_bounds(device):
-    # Many tiles (N = 50304 at 16-row tiles) and the largest split: every workgroup index maps to a
-    # real tile and split slot.
+    # Many items (N = 50304 at 64-row tiles, split 8: 6288 items, 24 per workgroup): every
+    # workgroup index maps to a real tile and split slot.
     M, N, K = 42, 50304, 1024
     x, w = _inputs_on_gpu(M, N, K, 15, device)
-    cfg = {"wave_frags": 1, "k_waves": 4, "split_k": 2, "unroll": 4}
-    assert math.ceil(N / 16) * 2 > 4096
+    cfg = {"wave_frags": 1, "k_waves": 4, "split_k": 8, "unroll": 2}
+    assert tiles.items(N, cfg) > 16 * tiles.CU_COUNT
     cols = torch.cat([torch.arange(0, 64), torch.arange(N - 64, N)])
     check_cols(hip_linear(x, w, cfg), x, w, cols)
 
@@ -286,7 +286,7 @@ def test_golden_fixtures(device, name):
     N = w.shape[0]
     supported = lambda c: fast_gemm.tile_supported(M, K, c)  # noqa: E731
     for cfg in (tiles.heuristic_tile(M, N, K, supported=supported),
-                {"wave_frags": 1, "k_waves": 4, "split_k": 2, "unroll": 1}):
+                {"wave_frags": 1, "k_waves": 4, "split_k": 2, "unroll": 2}):
         y = _run(x, w, cfg, device).cpu()
         got = y.view(torch.int16).numpy().view("uint16")
         if name.endswith("_int"):

@@ -42,9 +42,10 @@ def _own_logits_from_workspace(R: int, device) -> torch.Tensor:
 def run_case(x, w, pending, p, mode, device, cfg=None, check_cpu=True):
     acc, am = lm_head_verify(x, w, pending, p, mode, cfg)
     acc, am = acc.cpu(), am.cpu()
+    # Read before the GEMM below reuses the workspace for its split-K partials.
+    own = _own_logits_from_workspace(x.shape[0], device)
     logits = _rounded(hip_linear_f32(x, w, LOGITS_CONFIG).cpu(), mode)
     # The own-logit pass reproduces the main pass's value for each proposal bit for bit.
-    own = _own_logits_from_workspace(x.shape[0], device)
     valid = (pending.cpu() >= 0) & (pending.cpu() < w.shape[0])
     rows = torch.arange(x.shape[0])[valid]
     assert torch.equal(own[rows], logits[rows, pending.cpu()[rows]])
