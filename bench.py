@@ -4,14 +4,15 @@ A step is one full 1.3B-shape round at k=7 (M = 56 rows): 24 GPT-style blocks (Q
 attention-out 2048->2048, MLP up 2048->8192, MLP down 8192->2048) plus the LM head 2048->50257,
 97 linears chained output-to-input as in the model, with random-init bf16 weights
 (~N(0, 0.02^2)) resident in HBM. The round is recorded once as a HIP graph and replayed (the
-reference replays its round as a CUDA graph, plm/decoder.py:414-447), two ways:
-  * the headline: all 97 linears in one chained launch of the streaming kernel (plm_gemm_chain);
-  * the per-GEMM drop-in path: 97 fast_gemm launches (plm_gemm), reported beside it.
+reference replays its round as a CUDA graph, plm/decoder.py:414-447), two ways, both over
+weights packed once into the MFMA fragment layout (as a served model keeps them):
+  * all 97 linears in one chained launch (plm_gemm_chain_packed), checked bit for bit against
+  * the per-GEMM drop-in path: 97 fast_gemm launches (plm_gemm_packed, tuned tile per shape).
 
-Prints one JSON line: ``value`` is microseconds per round (lower is better), plus the round's HBM
-GB/s and fraction of the 8 TB/s peak, the kernel roofline from HIP-event timing, the
-partial-round M sweep, the fused LM-head verify step, and the torch-CPU baseline of the same
-linears timed on this host.
+Prints one JSON line: ``value`` is microseconds per round (lower is better) of the faster of the
+two (both are reported), plus the round's HBM GB/s and fraction of the 8 TB/s peak, the dominant
+kernel's roofline from HIP-event timing, the partial-round M sweep, the fused LM-head verify step,
+and the torch-CPU baseline of the same linears timed on this host.
 """
 
 from __future__ import annotations
@@ -119,8 +120,8 @@ def kernel_class(M, K, cfg):
 
 
 def kernel_name(cls):
-    mt, nf, u = cls
-    return f"stream_gemm_kernel<bf16, MT={mt}, NF={nf}, U={u}>"
+    mt, nf, d = cls
+    return f"packed_gemm_kernel<bf16, MT={mt}, NF={nf}, D={d}>"
 
 
 def dominant_kernel_roofline(rnd, steps):
@@ -206,15 +207,24 @@ def capture_graph(fn):
     return graph
 
 
-def round_chain(rnd):
-    """The round's 97 linears as one chained launch (plm_gemm_chain), output-to-input."""
-    from plm_amd.chain import Link, LinearChain
-    from plm_amd.tiles import chain_split, chain_tile
+# Tile of the packed chained round: 32-row tiles, two-stage pipeline (the fastest measured).
+CHAIN_CFG = {"wave_frags": 2, "k_waves": 4, "split_k": 1, "unroll": 2}
 
-    cfg = chain_tile(rnd.M)
-    links = [Link(x, w, y, i - 1, chain_split(g.N, g.K, cfg))
+
+def round_chain(rnd):
+    """The round's 97 linears as one chained launch over packed weights (plm_gemm_chain_packed),
+    output-to-input, each linear's K split chosen for the resident grid."""
+    from plm_amd import _lib
+    from plm_amd.chain import Link, LinearChain
+    from plm_amd.fast_gemm import _tile
+    from plm_amd.tiles import packed_chain_split
+
+    cfg = dict(CHAIN_CFG)
+    G = _lib.lib().plm_gemm_packed_resident_workgroups(_lib.PLM_BF16, rnd.M, _tile(cfg))
+    _lib.check(min(G, 0), "plm_gemm_packed_resident_workgroups")
+    links = [Link(x, w, y, i - 1, packed_chain_split(g.N, g.K, cfg, G))
              for i, (g, x, w, y) in enumerate(zip(rnd.gemms, rnd.inputs, rnd.weights, rnd.outs))]
-    return LinearChain(links, cfg)
+    return LinearChain(links, cfg, packed=True)
 
 
 def main():
@@ -227,7 +237,6 @@ def main():
 
     from plm_amd import gemm_tables
     from plm_amd.fast_gemm import hip_linear  # noqa: F401  (fails loudly if the library is missing)
-    from plm_amd.tiles import chain_tile
     from plm_amd.workloads import GPT2_VOCAB, gpt_block
 
     torch.cuda.set_device(0)
@@ -295,40 +304,61 @@ def main():
     print(f"[bench] per-GEMM graph round: {us_graph:.1f} us, {rnd.bytes / (us_graph * 1e-6) / 1e9:.0f} GB/s",
           file=sys.stderr, flush=True)
 
+    # value: the faster of the two complete implementations of the round (both verified above:
+    # the chain bit for bit against the per-linear launches, those against the oracle in the tests).
+    chain_wins = us_round <= us_graph
+    us_value = us_round if chain_wins else us_graph
+    gbps_value = rnd.bytes / (us_value * 1e-6) / 1e9
+    timing = ("HIP graph replay, HIP events; value = the round as one chained launch over packed weights "
+              "(plm_gemm_chain_packed)" if chain_wins else
+              "HIP graph replay, HIP events; value = the round as 97 fast_gemm launches (plm_gemm_packed, "
+              "tuned tile per shape) in one graph")
     result = {
-        "metric": METRIC, "value": round(us_round, 2), "unit": "us/round", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (random-init weights ~N(0,0.02^2), seeded)",
+        "metric": METRIC, "value": round(us_value, 2), "unit": "us/round", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(us_value / 1000.0, 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init weights ~N(0,0.02^2), seeded)",
         "config": {"workload": f"{'1.3B' if args.hidden == 2048 else str(args.hidden)}-shape round of linears: "
                                f"{args.layers} GPT-style blocks + LM head, M={args.M} (k=7)",
                    "M": args.M, "hidden": args.hidden, "mlp": args.mlp, "layers": args.layers,
                    "vocab": GPT2_VOCAB, "gemm_launches": len(gemms), "bytes_per_round": rnd.bytes,
-                   "timing": "HIP graph replay, HIP events; value = the round as one chained launch "
-                             "(plm_gemm_chain)", "chain_tile": chain_tile(args.M)},
-        "gbps": round(gbps, 1), "pct_of_hbm_peak": round(100.0 * gbps / HBM_PEAK_GBPS, 2),
+                   "timing": timing, "chain_tile": CHAIN_CFG},
+        "gbps": round(gbps_value, 1), "pct_of_hbm_peak": round(100.0 * gbps_value / HBM_PEAK_GBPS, 2),
+        "chained_round": {"us": round(us_round, 2), "gbps": round(gbps, 1), "launches": 1},
         "per_gemm_graph": {"us": round(us_graph, 2), "gbps": round(rnd.bytes / (us_graph * 1e-6) / 1e9, 1),
                            "launches": len(gemms)},
     }
     if not args.only_round:
-        # The chained launch is the round's only kernel: its HIP-event time per replay is its duration.
-        kernel = "stream_gemm_kernel<bf16, MT=%d, NF=4, U=2> (chained round)" % math.ceil(args.M / 16)
-        achieved = rnd.bytes / (us_round * 1e-6) / 1e9
-        result["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                              "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic_for("chain_round"),
-                              "kernel": kernel, "launches_per_round": 1, "us_per_launch": round(us_round, 2),
-                              "bytes_per_launch": rnd.bytes}
         rows = dominant_kernel_roofline(rnd, args.steps)
         result["per_gemm_kernels"] = [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}
                                       for r in rows]
+        if chain_wins:
+            # The chained launch is the round's only kernel: its HIP-event time per replay is its duration.
+            kernel = "packed_gemm_kernel<bf16, MT=%d, NF=%d, D=%d> (chained round)" % (
+                math.ceil(args.M / 16), CHAIN_CFG["wave_frags"], CHAIN_CFG["unroll"])
+            achieved = rnd.bytes / (us_round * 1e-6) / 1e9
+            result["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                                  "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                                  "traffic": traffic_for("chain_round"), "kernel": kernel, "launches_per_round": 1,
+                                  "us_per_launch": round(us_round, 2), "bytes_per_launch": rnd.bytes}
+        else:
+            # The kernel class with the most time in the round; its launches timed alone as a graph.
+            top = rows[0]
+            achieved = top["bytes_per_launch"] / (top["us_per_launch"] * 1e-6) / 1e9
+            result["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                                  "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                                  "traffic": traffic_for(top["kernel"]), "kernel": top["kernel"],
+                                  "launches_per_round": top["launches"],
+                                  "us_per_launch": round(top["us_per_launch"], 3),
+                                  "bytes_per_launch": round(top["bytes_per_launch"], 1)}
         if not args.no_sweep:
             sweep = {}
             for M in (7, 14, 28, 42, 56):
                 r = Round(M, args.hidden, args.mlp, args.layers, weights, tables, device)
-                c = round_chain(r)
-                g = capture_graph(c.run)
+                g = capture_graph(round_chain(r).run) if chain_wins else r.capture()
                 us = time_graph(g, max(10, args.steps // 2), 3) * 1000.0
                 sweep[str(M)] = {"us": round(us, 1), "gbps": round(r.bytes / (us * 1e-6) / 1e9, 1)}
-                del g, c, r
+                del g, r
             result["m_sweep"] = sweep
             print(f"[bench] M sweep: {sweep}", file=sys.stderr, flush=True)
         if not args.no_verify:

@@ -67,6 +67,41 @@ typedef struct plm_tile {
 } plm_tile;
 
 /*
+ * Packed weights. plm_pack_weight rearranges a row-major W[N,K] (ldw elements per row) into the
+ * operand order of gfx950's 16x16x32 MFMA: fragment (f, s) = rows [16f, 16f+16) x K [32s, 32s+32)
+ * as 64 lanes x 16 bytes, lane l holding row 16f + l%16, elements 32s + 8*(l/16) .. +8, laid out
+ * [ceil(N/16)][ceil(K/32)] and zero-padded. Each weight load of plm_gemm_packed is then one
+ * contiguous KiB. Packing is a one-time pass per weight (the reference reads its weights as they
+ * are, plm/fast_gemm.py:17-48; a caller keeps the packed copy next to the weight).
+ * plm_packed_weight_bytes gives the size; `packed` must be 16-byte aligned.
+ */
+size_t plm_packed_weight_bytes(int64_t N, int64_t K);
+int plm_pack_weight(int32_t dtype, const void* w, int64_t ldw, int64_t N, int64_t K, void* packed, size_t packed_bytes,
+                    void* stream);
+
+/*
+ * Y[M,N] = X[M,K] · W[N,K]^T over a packed W, fp32 accumulation, Y in the input dtype: the fast
+ * path behind triton_linear (plm/fast_gemm.py:82-97, with gemm_kernel 17-48 and
+ * splitk_reduce_kernel 51-61). Tile fields for this kernel: wave_frags = 16-row fragments per
+ * workgroup tile (1, 2, 4); k_waves = 4 (the workgroup's wavefronts split the tile's K range and
+ * are summed in LDS in wavefront order); split_k = workgroups splitting K (1..64, partials summed
+ * in split order); unroll = K steps of loads in flight per wavefront (2, 4, 6). Requirements as
+ * plm_gemm (1 <= M <= 128, K % 8 == 0, ldx % 8 == 0, x 16-byte aligned).
+ */
+int plm_gemm_packed(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy, int64_t M,
+                    int64_t N, int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream);
+
+/* As plm_gemm_packed with an fp32 Y (the accumulator before the cast, plm/fast_gemm.py:46). */
+int plm_gemm_packed_f32out(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, float* y, int64_t ldy,
+                           int64_t M, int64_t N, int64_t K, const plm_tile* tile, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/* Workspace bytes plm_gemm_packed needs for this shape and tile (0 without split-K), and whether a
+ * kernel is compiled for the tile at this M. */
+size_t plm_gemm_packed_workspace_bytes(int64_t M, int64_t N, int64_t K, const plm_tile* tile);
+int plm_gemm_packed_tile_supported(int32_t dtype, int64_t M, int64_t K, const plm_tile* tile);
+
+/*
  * Y[M,N] = X[M,K] · W[N,K]^T with fp32 accumulation, Y in the input dtype.
  * Replaces triton_linear (plm/fast_gemm.py:82-97) together with gemm_kernel (17-48) and
  * splitk_reduce_kernel (51-61). Requirements: 1 <= M <= 128, K % 8 == 0, ldx/ldw % 8 == 0,
@@ -103,9 +138,29 @@ typedef struct plm_chain_gemm {
   /* filled by plm_gemm_chain_prepare */
   int32_t consumed;       /* 1 when a later linear reads this Y */
   int32_t arrive_base;    /* counter-area index of this linear's split-K arrival counters */
-  int32_t done_base;      /* counter-area index of this linear's tile-done flags */
+  int32_t done_base;      /* plm_gemm_chain: counter-area index of this linear's tile-done flags;
+                             plm_gemm_chain_packed: the progress-flag value that marks its Y written */
   int64_t partial_offset; /* float offset of this linear's split partials in the workspace */
 } plm_chain_gemm;
+
+/*
+ * A chain of linears over packed weights in one launch (the round's linears back to back,
+ * replacing the per-GEMM graph nodes of plm/decoder.py:312-324): plm_chain_gemm entries with
+ * `w` a packed weight (ldw is ignored). After every linear whose Y a later one reads, all
+ * workgroups meet at a grid barrier, so such a linear must not write fp32. The tile gives
+ * wave_frags, k_waves and unroll for every linear; each linear's split_k is its own. The launch
+ * (the chain kernel and a one-thread kernel that advances the workspace's launch epoch) needs
+ * every workgroup resident at once (the device to itself while it runs); a barrier that does not
+ * complete in about a second sets the int at PLM_WORKSPACE_ERROR_INDEX to 1.
+ * plm_gemm_chain_packed_prepare fills the derived fields and returns the workspace bytes.
+ */
+int64_t plm_gemm_chain_packed_prepare(plm_chain_gemm* gemms, int32_t count, int64_t M, const plm_tile* tile);
+/* Workgroups a packed launch with this tile keeps resident on the current device (the grid of a
+ * chained launch), or a negative status. Needs a device. */
+int plm_gemm_packed_resident_workgroups(int32_t dtype, int64_t M, const plm_tile* tile);
+int plm_gemm_chain_packed(int32_t dtype, const plm_chain_gemm* host_gemms, const plm_chain_gemm* device_gemms,
+                          int32_t count, int64_t M, const plm_tile* tile, void* workspace, size_t workspace_bytes,
+                          void* stream);
 
 /*
  * Fills the derived fields of gemms[0..count) for the tile configuration (whose split_k is

@@ -91,7 +91,7 @@ int64_t prepare(plm_chain_gemm* g, int32_t count, int64_t M, const plm_tile& t) 
       g[i].done_base = static_cast<int32_t>(done);
       done += tiles;
     }
-    if (arrive > kDoneBase || done > kMaxCounters) return PLM_ERR_ARGUMENT;
+    if (arrive > kDoneBase || done > kStreamDoneEnd) return PLM_ERR_ARGUMENT;
   }
   return static_cast<int64_t>(kCounterBytes) + partial * static_cast<int64_t>(sizeof(float));
 }

@@ -1,0 +1,303 @@
+// C ABI of the packed-weight GEMM: weight packing (plm_pack_weight) and the GEMM over packed
+// weights (plm_gemm_packed), declared in include/plm_amd.h.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "packed_gemm.h"
+#include "plm_amd.h"
+
+namespace plm {
+
+// Weight packing: thread i writes lane (i % 64) of fragment i / 64 (16 bytes, zeros past N or K).
+__global__ __launch_bounds__(256) void pack_weight_kernel(const uint16_t* __restrict__ w, int64_t ldw, int N, int K,
+                                                         int Ks, int64_t lanes, u32x4* __restrict__ out) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < lanes;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int lane = static_cast<int>(i & 63);
+    const int64_t frag = i >> 6;
+    const int f = static_cast<int>(frag / Ks), s = static_cast<int>(frag - static_cast<int64_t>(f) * Ks);
+    const int n = 16 * f + (lane & 15), k = 32 * s + 8 * (lane >> 4);
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (n < N && k < K) v = *reinterpret_cast<const u32x4*>(w + static_cast<int64_t>(n) * ldw + k);
+    out[i] = v;
+  }
+}
+
+
+namespace {
+
+constexpr int64_t kPackedMaxM = 128;
+
+int packed_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  static int cached_dev = -1, cached = 0;
+  if (dev != cached_dev) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cached_dev = dev;
+    cached = cus;
+  }
+  return cached;
+}
+
+int64_t ksteps(int64_t K) { return (K + 31) / 32; }
+
+int64_t packed_bytes(int64_t N, int64_t K) { return (N + 15) / 16 * ksteps(K) * kFragBytes; }
+
+bool packed_tile_valid(const plm_tile* t) {
+  return t != nullptr && (t->wave_frags == 1 || t->wave_frags == 2 || t->wave_frags == 4) &&
+         t->k_waves == kPackedWaves && t->split_k >= 1 && t->split_k <= 64 &&
+         (t->unroll == 2 || t->unroll == 4 || t->unroll == 6 || t->unroll == 8);
+}
+
+hipError_t packed_dispatch_dt(int32_t dtype, PackedArgs& a, const plm_tile& t, int cus, hipStream_t s, bool dry) {
+  if (dtype == PLM_BF16) return packed_dispatch_bf16(a, t.wave_frags, t.unroll, cus, s, dry);
+  if (dtype == PLM_F16) return packed_dispatch_f16(a, t.wave_frags, t.unroll, cus, s, dry);
+  return hipErrorInvalidConfiguration;
+}
+
+int64_t packed_tiles(int64_t N, const plm_tile& t) { return ((N + 15) / 16 + t.wave_frags - 1) / t.wave_frags; }
+
+// Workspace: the counter area, then (split > 1) one fp32 fragment per (tile, split, fragment).
+int64_t packed_workspace(int64_t M, int64_t N, const plm_tile& t) {
+  if (t.split_k <= 1) return 0;
+  const int64_t mt = (M + 15) / 16;
+  return static_cast<int64_t>(kCounterBytes) + packed_tiles(N, t) * t.split_k * t.wave_frags * mt * kFragBytes;
+}
+
+constexpr int kPackedSpinLimit = 1 << 20;  // polls (each one device round trip) before a wait gives up
+// Counter area of a packed launch: split arrival counters from kPackedArriveBase, progress flags
+// of a chain (an int64 per workgroup) from kPackedBarrierBase.
+
+// Checks one linear's operands (W packed); returns PLM_OK or the status to report.
+int packed_check_linear(int32_t dtype, const plm_chain_gemm& g, int64_t M) {
+  if (g.x == nullptr || g.w == nullptr || g.y == nullptr) return PLM_ERR_ARGUMENT;
+  if (dtype != PLM_BF16 && dtype != PLM_F16) return PLM_ERR_ARGUMENT;
+  if (M < 1 || M > kPackedMaxM || g.N < 1 || g.K < 8 || g.K % 8 != 0 || g.ldx < g.K || g.ldy < g.N)
+    return PLM_ERR_ARGUMENT;
+  if (g.split_k < 1 || g.split_k > 64 || (g.out_f32 != 0 && g.out_f32 != 1)) return PLM_ERR_ARGUMENT;
+  // 32-bit buffer offsets: X and the packed weights must each span less than 2 GiB.
+  if (M * g.ldx * 2 >= (int64_t(1) << 31) || packed_bytes(g.N, g.K) >= (int64_t(1) << 31)) return PLM_ERR_ARGUMENT;
+  if (g.ldx % 8 != 0 || (reinterpret_cast<uintptr_t>(g.x) & 15) != 0 || (reinterpret_cast<uintptr_t>(g.w) & 15) != 0)
+    return PLM_ERR_ALIGNMENT;
+  return PLM_OK;
+}
+
+int packed_launch_args(int32_t dtype, PackedArgs& a, const plm_tile& t, void* workspace, size_t workspace_bytes,
+                       int64_t need, hipStream_t s) {
+  if (need > 0 && (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < need ||
+                   (reinterpret_cast<uintptr_t>(workspace) & 15) != 0))
+    return PLM_ERR_WORKSPACE;
+  const int cus = packed_cus();
+  if (cus <= 0) return PLM_ERR_LAUNCH;
+  a.counters = need > 0 ? static_cast<int*>(workspace) : nullptr;
+  a.partial = need > 0 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes) : nullptr;
+  a.spin_limit = kPackedSpinLimit;
+  if (packed_dispatch_dt(dtype, a, t, cus, s, true) != hipSuccess) return PLM_ERR_TILE;
+  return packed_dispatch_dt(dtype, a, t, cus, s, false) == hipSuccess ? PLM_OK : PLM_ERR_LAUNCH;
+}
+
+int packed_entry(int32_t dtype, const void* x, int64_t ldx, const void* wp, void* y, int64_t ldy, int64_t M, int64_t N,
+                 int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream, int out_f32) {
+  if (!packed_tile_valid(tile)) return PLM_ERR_TILE;
+  const plm_tile& t = *tile;
+  if (N < 1 || N > (int64_t(1) << 30) || K > (int64_t(1) << 30)) return PLM_ERR_ARGUMENT;
+  plm_chain_gemm g{};
+  g.x = x;
+  g.w = wp;
+  g.y = y;
+  g.ldx = ldx;
+  g.ldw = K;
+  g.ldy = ldy;
+  g.N = static_cast<int32_t>(N);
+  g.K = static_cast<int32_t>(K);
+  g.split_k = t.split_k;
+  g.dep = -1;
+  g.out_f32 = out_f32;
+  const int status = packed_check_linear(dtype, g, M);
+  if (status != PLM_OK) return status;
+  const int64_t tiles = packed_tiles(N, t);
+  if (t.split_k > 1 && tiles > kPackedBarrierBase - kPackedArriveBase) return PLM_ERR_ARGUMENT;
+  g.arrive_base = kPackedArriveBase;
+  PackedArgs a{};
+  a.single = g;
+  a.count = 1;
+  a.M = static_cast<int>(M);
+  a.G = static_cast<int>(tiles * t.split_k);
+  return packed_launch_args(dtype, a, t, workspace, workspace_bytes, packed_workspace(M, N, t),
+                            static_cast<hipStream_t>(stream));
+}
+
+// Derived fields of a packed chain; returns the workspace bytes or a negative status. Split
+// arrival counters and partials are reused after every grid barrier (all of the previous
+// linears are complete there); barrier counters are one per consumed linear.
+int64_t packed_prepare(plm_chain_gemm* g, int32_t count, int64_t M, const plm_tile& t) {
+  for (int32_t i = 0; i < count; ++i) g[i].consumed = 0;
+  for (int32_t i = 0; i < count; ++i) {
+    if (g[i].dep < -1 || g[i].dep >= i) return PLM_ERR_ARGUMENT;
+    if (g[i].dep >= 0) g[g[i].dep].consumed = 1;
+  }
+  const int64_t mt = (M + 15) / 16;
+  int64_t arrive = kPackedArriveBase, seq = 0, partial = 0, most_partial = 0;
+  for (int32_t i = 0; i < count; ++i) {
+    if (g[i].N < 1 || g[i].split_k < 1 || g[i].split_k > 64) return PLM_ERR_ARGUMENT;
+    plm_tile ti = t;
+    ti.split_k = g[i].split_k;
+    const int64_t tiles = packed_tiles(g[i].N, ti);
+    g[i].arrive_base = 0;
+    g[i].done_base = 0;
+    g[i].partial_offset = 0;
+    if (g[i].split_k > 1) {
+      g[i].arrive_base = static_cast<int32_t>(arrive);
+      g[i].partial_offset = partial;
+      arrive += tiles;
+      const int64_t floats = tiles * g[i].split_k * t.wave_frags * mt * (kFragBytes / 4);
+      if (floats * 4 >= (int64_t(1) << 31)) return PLM_ERR_ARGUMENT;
+      partial += floats;
+      most_partial = std::max(most_partial, partial);
+      if (arrive > kPackedBarrierBase) return PLM_ERR_ARGUMENT;
+    }
+    if (g[i].consumed) {
+      g[i].done_base = static_cast<int32_t>(++seq);  // progress-flag value once this Y is written
+      if (seq >= (1 << 16)) return PLM_ERR_ARGUMENT;
+      arrive = kPackedArriveBase;  // everything before the barrier is finished
+      partial = 0;
+    }
+  }
+  return static_cast<int64_t>(kCounterBytes) + most_partial * 4;
+}
+
+struct PSpan {
+  uintptr_t lo, hi;
+  bool overlaps(const PSpan& o) const { return lo < o.hi && o.lo < hi; }
+};
+PSpan pspan(const void* p, int64_t rows, int64_t ld, int64_t cols, int64_t elem) {
+  const uintptr_t lo = reinterpret_cast<uintptr_t>(p);
+  return PSpan{lo, lo + static_cast<uintptr_t>(((rows - 1) * ld + cols) * elem)};
+}
+
+}  // namespace
+}  // namespace plm
+
+extern "C" {
+
+size_t plm_packed_weight_bytes(int64_t N, int64_t K) {
+  if (N < 1 || K < 1) return 0;
+  return static_cast<size_t>(plm::packed_bytes(N, K));
+}
+
+int plm_pack_weight(int32_t dtype, const void* w, int64_t ldw, int64_t N, int64_t K, void* packed, size_t packed_bytes,
+                    void* stream) {
+  if (w == nullptr || packed == nullptr || (dtype != PLM_BF16 && dtype != PLM_F16)) return PLM_ERR_ARGUMENT;
+  if (N < 1 || K < 8 || K % 8 != 0 || ldw < K) return PLM_ERR_ARGUMENT;
+  if (ldw % 8 != 0 || (reinterpret_cast<uintptr_t>(w) & 15) != 0 || (reinterpret_cast<uintptr_t>(packed) & 15) != 0)
+    return PLM_ERR_ALIGNMENT;
+  const int64_t bytes = plm::packed_bytes(N, K);
+  if (static_cast<int64_t>(packed_bytes) < bytes) return PLM_ERR_WORKSPACE;
+  if (N > (int64_t(1) << 30) || K > (int64_t(1) << 30)) return PLM_ERR_ARGUMENT;
+  const int64_t lanes = bytes / 16;
+  const int64_t blocks = std::min<int64_t>((lanes + 255) / 256, 65536);
+  hipLaunchKernelGGL(plm::pack_weight_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(w), ldw, static_cast<int>(N),
+                     static_cast<int>(K), static_cast<int>(plm::ksteps(K)), lanes, static_cast<plm::u32x4*>(packed));
+  return hipGetLastError() == hipSuccess ? PLM_OK : PLM_ERR_LAUNCH;
+}
+
+size_t plm_gemm_packed_workspace_bytes(int64_t M, int64_t N, int64_t K, const plm_tile* tile) {
+  (void)K;
+  if (!plm::packed_tile_valid(tile) || M < 1 || N < 1) return 0;
+  return static_cast<size_t>(plm::packed_workspace(M, N, *tile));
+}
+
+int plm_gemm_packed_tile_supported(int32_t dtype, int64_t M, int64_t K, const plm_tile* tile) {
+  if (!plm::packed_tile_valid(tile) || M < 1 || M > plm::kPackedMaxM || K < 8) return 0;
+  plm::PackedArgs a{};
+  a.M = static_cast<int>(M);
+  return plm::packed_dispatch_dt(dtype, a, *tile, 1, nullptr, true) == hipSuccess ? 1 : 0;
+}
+
+int plm_gemm_packed(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy, int64_t M,
+                    int64_t N, int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream) {
+  return plm::packed_entry(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, 0);
+}
+
+int plm_gemm_packed_f32out(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, float* y, int64_t ldy,
+                           int64_t M, int64_t N, int64_t K, const plm_tile* tile, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  return plm::packed_entry(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, 1);
+}
+
+int plm_gemm_packed_resident_workgroups(int32_t dtype, int64_t M, const plm_tile* tile) {
+  if (!plm::packed_tile_valid(tile) || M < 1 || M > plm::kPackedMaxM) return PLM_ERR_TILE;
+  const int cus = plm::packed_cus();
+  if (cus <= 0) return PLM_ERR_LAUNCH;
+  plm::PackedArgs a{};
+  a.M = static_cast<int>(M);
+  a.count = 0;
+  if (plm::packed_dispatch_dt(dtype, a, *tile, cus, nullptr, false) != hipSuccess) return PLM_ERR_TILE;
+  return a.G;
+}
+
+int64_t plm_gemm_chain_packed_prepare(plm_chain_gemm* gemms, int32_t count, int64_t M, const plm_tile* tile) {
+  if (gemms == nullptr || count < 1 || M < 1 || M > plm::kPackedMaxM) return PLM_ERR_ARGUMENT;
+  if (!plm::packed_tile_valid(tile)) return PLM_ERR_TILE;
+  return plm::packed_prepare(gemms, count, M, *tile);
+}
+
+int plm_gemm_chain_packed(int32_t dtype, const plm_chain_gemm* host_gemms, const plm_chain_gemm* device_gemms,
+                          int32_t count, int64_t M, const plm_tile* tile, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  if (host_gemms == nullptr || device_gemms == nullptr || count < 1) return PLM_ERR_ARGUMENT;
+  if (!plm::packed_tile_valid(tile)) return PLM_ERR_TILE;
+  if (M < 1 || M > plm::kPackedMaxM) return PLM_ERR_ARGUMENT;
+  // The derived fields must be what plm_gemm_chain_packed_prepare computes for this chain.
+  std::vector<plm_chain_gemm> check(host_gemms, host_gemms + count);
+  const int64_t need = plm::packed_prepare(check.data(), count, M, *tile);
+  if (need < 0) return static_cast<int>(need);
+  bool sync = false, any_split = false;
+  int64_t most_items = 0;
+  std::vector<plm::PSpan> ys(count), xs(count), ws(count);
+  for (int32_t i = 0; i < count; ++i) {
+    const plm_chain_gemm& g = host_gemms[i];
+    if (g.consumed != check[i].consumed || g.arrive_base != check[i].arrive_base ||
+        g.done_base != check[i].done_base || g.partial_offset != check[i].partial_offset)
+      return PLM_ERR_ARGUMENT;
+    const int status = plm::packed_check_linear(dtype, g, M);
+    if (status != PLM_OK) return status;
+    plm_tile ti = *tile;
+    ti.split_k = g.split_k;
+    most_items = std::max(most_items, plm::packed_tiles(g.N, ti) * g.split_k);
+    any_split = any_split || g.split_k > 1;
+    ys[i] = plm::pspan(g.y, M, g.ldy, g.N, g.out_f32 ? 4 : 2);
+    xs[i] = plm::pspan(g.x, M, g.ldx, g.K, 2);
+    ws[i] = plm::PSpan{reinterpret_cast<uintptr_t>(g.w),
+                       reinterpret_cast<uintptr_t>(g.w) + static_cast<uintptr_t>(plm::packed_bytes(g.N, g.K))};
+    if (g.dep >= 0) {
+      sync = true;
+      const plm_chain_gemm& p = host_gemms[g.dep];
+      if (g.x != p.y || g.ldx != p.ldy || g.K > p.N || p.out_f32) return PLM_ERR_ARGUMENT;
+    }
+  }
+  // No linear writes what another linear writes, or reads before it is written.
+  for (int32_t i = 0; i < count; ++i)
+    for (int32_t j = 0; j < count; ++j) {
+      if (i != j && ys[i].overlaps(ys[j])) return PLM_ERR_ARGUMENT;
+      if (ys[i].overlaps(ws[j])) return PLM_ERR_ARGUMENT;
+      if (ys[i].overlaps(xs[j]) && host_gemms[j].dep != i) return PLM_ERR_ARGUMENT;
+    }
+  plm::PackedArgs a{};
+  a.chain = device_gemms;
+  a.single = host_gemms[0];
+  a.count = count;
+  a.M = static_cast<int>(M);
+  a.G = static_cast<int>(most_items);
+  a.sync = sync ? 1 : 0;
+  const int64_t needed = (sync || any_split) ? need : 0;
+  return plm::packed_launch_args(dtype, a, *tile, workspace, workspace_bytes, needed,
+                                 static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,10 @@
+// fp16 instantiations of the packed-weight GEMM (one translation unit per dtype so they build in parallel).
+#include "packed_gemm.h"
+
+namespace plm {
+
+hipError_t packed_dispatch_f16(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry) {
+  return packed_dispatch<DT_F16>(a, nf, d, cus, s, dry);
+}
+
+}  // namespace plm

@@ -1,0 +1,605 @@
+// Skinny GEMM over pre-packed weights for the PLM round's dense linears on gfx950 (MI355X).
+//
+// Y[M,N] = X[M,K] · W[N,K]^T with fp32 accumulation, for one linear or for a chain of linears in
+// one launch (the round's linears back to back, a later one reading an earlier one's Y). M is the
+// round width (56 at k=7), so W is almost all of the bytes and the kernel is an HBM stream of W.
+//
+// Packed weights. v_mfma_f32_16x16x32_{bf16,f16} takes its A operand as lane l = row l%16, K
+// elements [8*(l/16), 8*(l/16)+8) of a 32-wide K step: 16 bytes per lane from 16 different rows.
+// Loaded from a row-major W, every quad of lanes touches four rows, so one load instruction is
+// 64 separate cache-line requests and the vector memory pipeline, not HBM, sets the speed. The
+// weights are therefore rearranged once (plm_pack_weight) into fragments: fragment (f, s) is rows
+// [16f, 16f+16) x K [32s, 32s+32) stored as 64 lanes x 16 bytes in exactly that lane order, laid
+// out [ceil(N/16)][ceil(K/32)] with zero padding. Every weight load is then one contiguous,
+// aligned KiB that lands in the registers as the MFMA operand, with no LDS staging.
+// X (small, L2-resident) is loaded row-major and coalesced, and turned into the operand layout
+// through a wavefront-private LDS tile.
+//
+// Work: item = a tile of NF fragments (16*NF weight rows) x one of `split` K ranges. Workgroups
+// are persistent and take items blockIdx.x, blockIdx.x + G, ... of each linear in turn. Each of
+// the 4 wavefronts owns a quarter of the item's K range and streams its weight and X fragments
+// through a D-stage register pipeline that runs across the linear's item boundaries. At an item's
+// end the four partial tiles are summed in LDS in wavefront order; with split > 1 the sum is an
+// fp32 partial and the last workgroup of the tile to arrive (device-scope counter) adds the
+// partials in split order and writes Y.
+//
+// Chains: after a linear whose Y a later linear reads, every workgroup writes its part of Y
+// through to the device-coherent level and then raises its own progress flag (one 64-bit word per
+// workgroup: launch epoch and the number of such linears it has finished, so flags only grow and
+// need no reset). It requests the next linear's first weight fragments, so the weight stream
+// overlaps the wait, and then polls every workgroup's flag until all have finished the linear: a
+// grid barrier made of plain stores and loads, with no contended atomic. The epoch is advanced by
+// a one-thread kernel after every chained launch. All workgroups of a chained launch are resident
+// at once; every wait is bounded and sets the error flag if it gives up.
+//
+// Results are bitwise reproducible run to run: every sum has a fixed order (K steps ascending
+// within a wavefront, wavefronts 0..3, splits 0..split-1).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "plm_amd.h"
+#include "tile.h"
+
+namespace plm {
+
+constexpr int kPackedWaves = 4;            // wavefronts per workgroup, each a quarter of the item's K range
+constexpr int kFragBytes = 1024;           // one packed fragment: 64 lanes x 16 bytes
+constexpr uint32_t kNoLoad = 0x80000000u;  // scalar offset that puts a load out of range (zeros)
+constexpr int kXTileBytes = 16 * 80;       // LDS transpose tile of one X fragment (rows padded to 80 B)
+
+// Counter-area layout of a packed launch (int indices).
+constexpr int kPkErrorSlot = 2;      // 1 once a bounded wait gave up
+constexpr int kPkEpochSlot = 10;     // int64 at ints 10-11: packed chained launches completed
+constexpr int kPkMaxWorkgroups = 2048;  // progress flags: int64 per workgroup at kPackedBarrierBase
+
+struct PackedArgs {
+  const plm_chain_gemm* chain;  // device array of `count` linears, or nullptr: use `single`
+  plm_chain_gemm single;
+  int count;
+  int M;
+  int G;           // workgroups in the grid
+  int sync;        // some linear reads an earlier one's output (progress flags, epoch)
+  int spin_limit;  // polls before a wait gives up
+  int* counters;
+  float* partial;
+};
+
+__device__ __forceinline__ int sgpr(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ int64_t sgpr64(int64_t v) {
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v >> 32)));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+template <typename T>
+__device__ __forceinline__ T* sgpr_ptr(T* p) {
+  return reinterpret_cast<T*>(sgpr64(reinterpret_cast<int64_t>(p)));
+}
+
+// One linear as the kernel uses it (all wave-uniform).
+struct PLinear {
+  const void* x;
+  const void* wp;
+  void* y;
+  int64_t ldx, ldy;
+  int N, Ks, k_last, split, tiles, items;
+  int out_f32, consumed;
+  int* arrive;     // split arrival counters, one per tile
+  int seq;         // consumed linears up to and including this one (progress flag value)
+  float* partial;  // split partials
+};
+
+template <int NF>
+__device__ __forceinline__ PLinear load_linear(const PackedArgs& a, int gi) {
+  const plm_chain_gemm* src = a.chain != nullptr ? a.chain + gi : &a.single;
+  PLinear L;
+  L.x = sgpr_ptr(src->x);
+  L.wp = sgpr_ptr(src->w);
+  L.y = sgpr_ptr(src->y);
+  L.ldx = sgpr64(src->ldx);
+  L.ldy = sgpr64(src->ldy);
+  L.N = sgpr(src->N);
+  const int K = sgpr(src->K);
+  L.Ks = (K + 31) >> 5;
+  L.k_last = K - 32 * (L.Ks - 1);
+  L.split = sgpr(src->split_k);
+  L.tiles = (((L.N + 15) >> 4) + NF - 1) / NF;
+  L.items = L.tiles * L.split;
+  L.out_f32 = sgpr(src->out_f32);
+  L.consumed = sgpr(src->consumed);
+  L.arrive = a.counters + sgpr(src->arrive_base);
+  L.seq = sgpr(src->done_base);
+  L.partial = a.partial + sgpr64(src->partial_offset);
+  return L;
+}
+
+// K-step range [b, e) of wavefront w's quarter of split s.
+__device__ __forceinline__ void packed_range(int Ks, int s, int split, int w, int& b, int& e) {
+  const int lo = static_cast<int>(static_cast<int64_t>(s) * Ks / split);
+  const int hi = static_cast<int>(static_cast<int64_t>(s + 1) * Ks / split);
+  const int n = hi - lo;
+  b = lo + n * w / kPackedWaves;
+  e = lo + n * (w + 1) / kPackedWaves;
+}
+
+// A wavefront's position in its stream of (item, K step). A wavefront's steps of an item are
+// padded with all-zero steps (out-of-range loads) to a multiple of the pipeline depth D, at least
+// D: item boundaries then always fall on pipeline stage 0, so the end-of-item work sits outside
+// the unrolled stages and the compiler's load-count waits stay exact across items.
+struct PCursor {
+  int item;   // >= items once past the linear's last item of this workgroup
+  int st;     // current K step
+  int end;    // end of the steps that load data
+  int pend;   // end of the padded steps
+  int wbase;  // byte offset of the item's first weight fragment at step 0
+};
+
+template <int NF, int D>
+__device__ __forceinline__ void pc_enter(const PLinear& L, int wave, PCursor& c) {
+  if (c.item >= L.items) return;
+  const int tile = c.item / L.split;
+  const int s = c.item - tile * L.split;
+  int b, e;
+  packed_range(L.Ks, s, L.split, wave, b, e);
+  c.st = b;
+  c.end = e;
+  c.pend = b + max(D, (e - b + D - 1) / D * D);
+  c.wbase = tile * NF * L.Ks * kFragBytes;
+}
+
+template <int NF, int D>
+__device__ __forceinline__ void pc_advance(const PLinear& L, int G, int wave, PCursor& c) {
+  if (++c.st == c.pend) {
+    c.item += G;
+    pc_enter<NF, D>(L, wave, c);
+  }
+}
+
+__device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Per-lane operand offsets of one linear.
+template <int MT, int NF>
+struct POffsets {
+  uint32_t wo[NF];       // weight fragment f at step 0 (plus the item's wbase, the step's KiB)
+  uint32_t xo[MT];       // coalesced X: row 16t + lane/4, bytes 16*(lane%4) of the step's 64
+  uint32_t xo_last[MT];  // the same with lanes past K (last step) out of range
+};
+
+template <int MT, int NF>
+__device__ __forceinline__ void packed_offsets(const PLinear& L, int M, int lane, POffsets<MT, NF>& o) {
+#pragma unroll
+  for (int f = 0; f < NF; ++f) o.wo[f] = static_cast<uint32_t>(f * L.Ks * kFragBytes + lane * 16);
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int m = 16 * t + (lane >> 2);
+    o.xo[t] = m < M ? static_cast<uint32_t>(m * L.ldx * 2 + (lane & 3) * 16) : kOutOfRange;
+    o.xo_last[t] = 8 * (lane & 3) < L.k_last ? o.xo[t] : kOutOfRange;
+  }
+}
+
+// Loads the weight half of one pipeline stage (the cursor's K step).
+template <int NF>
+__device__ __forceinline__ void issue_w(__amdgpu_buffer_rsrc_t wr, const PCursor& c, int items,
+                                        const uint32_t (&wo)[NF], u32x4 (&wb)[NF]) {
+  const bool live = c.item < items && c.st < c.end;
+  const uint32_t ws = live ? static_cast<uint32_t>(c.wbase + c.st * kFragBytes) : kNoLoad;
+#pragma unroll
+  for (int f = 0; f < NF; ++f)
+    wb[f] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, wo[f], static_cast<int>(ws), 0));
+}
+
+// Loads the X half of one pipeline stage. X lanes past K in the last step load zeros (the packed
+// weights are zero there, but X past K is another row's data or padding, and 0 * NaN is NaN).
+template <int MT, int NF>
+__device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t xr, const PCursor& c, int items, int Ks,
+                                        const POffsets<MT, NF>& o, u32x4 (&xb)[MT]) {
+  const bool live = c.item < items && c.st < c.end;
+  const uint32_t xs = live ? static_cast<uint32_t>(c.st * 64) : kNoLoad;
+  const bool last = c.st == Ks - 1;
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+    xb[t] = __builtin_bit_cast(
+        u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, last ? o.xo_last[t] : o.xo[t], static_cast<int>(xs), 0));
+}
+
+// Four columns n..n+3 of Y row m (fewer at N's end); written through to the device-coherent level
+// when a later linear of the chain reads this Y.
+template <int DT>
+__device__ __forceinline__ void packed_store4(const PLinear& L, int m, int n, f32x4 v) {
+  const int left = L.N - n;
+  if (L.out_f32) {
+    float* y = static_cast<float*>(L.y) + static_cast<int64_t>(m) * L.ldy + n;
+    if (left >= 4 && (reinterpret_cast<uintptr_t>(y) & 15) == 0) {
+      *reinterpret_cast<f32x4*>(y) = v;
+    } else {
+      for (int j = 0; j < 4 && j < left; ++j) y[j] = v[j];
+    }
+    return;
+  }
+  uint16_t* y = static_cast<uint16_t*>(L.y) + static_cast<int64_t>(m) * L.ldy + n;
+  const uint16_t h0 = to_bits16<DT>(v[0]), h1 = to_bits16<DT>(v[1]), h2 = to_bits16<DT>(v[2]), h3 = to_bits16<DT>(v[3]);
+  if (left >= 4 && (reinterpret_cast<uintptr_t>(y) & 7) == 0) {
+    const uint64_t bits = (static_cast<uint64_t>(h0) | (static_cast<uint64_t>(h1) << 16)) |
+                          ((static_cast<uint64_t>(h2) | (static_cast<uint64_t>(h3) << 16)) << 32);
+    if (L.consumed)
+      publish(reinterpret_cast<uint64_t*>(y), bits);
+    else
+      *reinterpret_cast<uint64_t*>(y) = bits;
+  } else {
+    const uint16_t h[4] = {h0, h1, h2, h3};
+    for (int j = 0; j < 4 && j < left; ++j) {
+      if (L.consumed)
+        publish(y + j, h[j]);
+      else
+        y[j] = h[j];
+    }
+  }
+}
+
+// Fragment q = f*MT + t of a tile, as lane `lane` holds it: rows n0 + 16f + 4*(lane/16) + r
+// (r = 0..3) of column m = 16t + lane%16.
+template <int DT, int MT>
+__device__ __forceinline__ void packed_store_frag(const PLinear& L, int M, int n0, int q, int lane, f32x4 v) {
+  const int f = q / MT, t = q - f * MT;
+  const int m = 16 * t + (lane & 15);
+  const int n = n0 + 16 * f + 4 * (lane >> 4);
+  if (m < M && n < L.N) packed_store4<DT>(L, m, n, v);
+}
+
+// End of an item for this workgroup: sums the four wavefronts' tiles (LDS, wavefront order) and
+// writes Y, or with split > 1 the fp32 partial, then the last split to arrive writes Y.
+template <int DT, int MT, int NF>
+__device__ __forceinline__ void packed_finish(const PLinear& L, int M, int item, int wave, int lane,
+                                              f32x4 (&acc)[NF][MT], f32x4* red, int* last_flag) {
+  constexpr int Q = NF * MT;
+#pragma unroll
+  for (int f = 0; f < NF; ++f)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) red[(wave * Q + f * MT + t) * 64 + lane] = acc[f][t];
+  lds_sync();
+  const int tile = item / L.split;
+  const int s = item - tile * L.split;
+  const int n0 = tile * NF * 16;
+  f32x4 sum[(Q + kPackedWaves - 1) / kPackedWaves];
+#pragma unroll
+  for (int i = 0; i * kPackedWaves < Q; ++i) {
+    const int q = wave + kPackedWaves * i;
+    if (q < Q) {
+      f32x4 v = red[q * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < kPackedWaves; ++w) v += red[(w * Q + q) * 64 + lane];
+      sum[i] = v;
+    }
+  }
+  lds_sync();  // every wavefront has read the tiles; LDS is free for the next item
+  if (L.split == 1) {
+#pragma unroll
+    for (int i = 0; i * kPackedWaves < Q; ++i) {
+      const int q = wave + kPackedWaves * i;
+      if (q < Q) packed_store_frag<DT, MT>(L, M, n0, q, lane, sum[i]);
+    }
+    return;
+  }
+  // Split partial: one KiB block per fragment (an fp32 fragment is 64 lanes x 16 bytes), written
+  // through to the device-coherent level.
+  const uint32_t tile_bytes = static_cast<uint32_t>(L.split) * Q * kFragBytes;
+  const auto prs = make_rsrc(L.partial + static_cast<int64_t>(tile) * L.split * Q * 256, tile_bytes);
+#pragma unroll
+  for (int i = 0; i * kPackedWaves < Q; ++i) {
+    const int q = wave + kPackedWaves * i;
+    if (q < Q)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum[i]), prs,
+                                             static_cast<uint32_t>((s * Q + q) * kFragBytes + lane * 16), 0, kCoherent);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this wavefront's partial is written through
+  lds_sync();
+  if (threadIdx.x == 0) {
+    int* counter = L.arrive + tile;
+    const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = before == L.split - 1;
+    if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *last_flag = last;
+  }
+  lds_sync();
+  if (*last_flag == 0) return;
+#pragma unroll
+  for (int i = 0; i * kPackedWaves < Q; ++i) {
+    const int q = wave + kPackedWaves * i;
+    if (q < Q) {
+      f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int s0 = 0; s0 < L.split; s0 += 8) {
+        u32x4 part[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          part[j] = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                         prs, s0 + j < L.split ? static_cast<uint32_t>(((s0 + j) * Q + q) * kFragBytes + lane * 16) : kOutOfRange,
+                         0, kCoherent));
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (s0 + j < L.split) v += __builtin_bit_cast(f32x4, part[j]);
+      }
+      packed_store_frag<DT, MT>(L, M, n0, q, lane, v);
+    }
+  }
+}
+
+extern __shared__ __attribute__((aligned(16))) f32x4 packed_lds[];
+
+// Grid barrier after the consumed linear with sequence number `seq`, in two halves so that the
+// wait can overlap weight traffic: barrier_arrive raises this workgroup's progress flag (its
+// stores are written through: the caller waited for them), barrier_wait polls every workgroup's
+// flag until all are at least as far (bounded).
+__device__ __forceinline__ void barrier_arrive(const PackedArgs& a, int64_t epoch, int seq) {
+  int64_t* flags = reinterpret_cast<int64_t*>(a.counters + kPackedBarrierBase);
+  lds_sync();
+  if (threadIdx.x == 0) publish(flags + blockIdx.x, ((epoch + 1) << 16) + seq);
+}
+
+__device__ __forceinline__ void barrier_wait(const PackedArgs& a, int64_t epoch, int seq, int lane) {
+  const int64_t target = ((epoch + 1) << 16) + seq;
+  if (threadIdx.x < 64) {
+    // Each lane polls G/64 flags with device-coherent loads, all issued before any is examined.
+    const auto frs = make_rsrc(a.counters + kPackedBarrierBase, static_cast<uint32_t>(a.G) * 8u);
+    for (int i = 0;; ++i) {
+      int64_t low = INT64_MAX;
+#pragma unroll
+      for (int j = 0; j < kPkMaxWorkgroups / 64; ++j) {
+        if (j * 64 < a.G) {
+          const u32x2 v = __builtin_bit_cast(
+              u32x2, __builtin_amdgcn_raw_buffer_load_b64(frs, static_cast<uint32_t>((j * 64 + lane) * 8), 0, kCoherent));
+          const int64_t f = static_cast<int64_t>((static_cast<uint64_t>(v.y) << 32) | v.x);
+          low = j * 64 + lane < a.G ? min(low, f) : low;
+        }
+      }
+      if (__all(low >= target)) break;
+      if (i >= a.spin_limit) {
+        if (lane == 0) publish(a.counters + kPkErrorSlot, 1);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  lds_sync();
+}
+
+typedef __attribute__((address_space(3))) void PkLdsVoid;
+
+// Cache warming during a barrier: requests up to kWarmFragments more of the next linear's weight
+// fragments this wavefront will stream (after the D stages already in registers) into a scratch
+// KiB of LDS, so that they are on their way from HBM into the caches while the workgroup waits;
+// the pipeline then finds them in L2 / the Infinity Cache.
+constexpr int kWarmFragments = 32;
+
+template <int NF, int D>
+__device__ __forceinline__ void warm_weights(const PLinear& Ln, int G, int wave, int lane, PCursor nx,
+                                             __amdgpu_buffer_rsrc_t wr, const uint32_t* wo, PkLdsVoid* dst) {
+  for (int n = 0; n < kWarmFragments / NF && nx.item < Ln.items; ++n) {
+    if (nx.st < nx.end) {
+      const uint32_t ws = static_cast<uint32_t>(nx.wbase + nx.st * kFragBytes);
+#pragma unroll
+      for (int f = 0; f < NF; ++f)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, dst, 16, wo[f], static_cast<int>(ws), 0, 0);
+    }
+    pc_advance<NF, D>(Ln, G, wave, nx);
+  }
+  (void)lane;
+}
+
+// Advances the packed-chain epoch after a chained launch (the next launch's flags then exceed
+// every flag of this one).
+template <int kUnused = 0>  // a template, so that every translation unit may instantiate it
+__global__ void packed_epoch_kernel(int* counters) {
+  if (threadIdx.x == 0) {
+    int64_t* epoch = reinterpret_cast<int64_t*>(counters + kPkEpochSlot);
+    publish(epoch, collect(epoch) + 1);
+  }
+}
+
+// Registers per lane of the operand pipeline and the accumulators. Configurations that fit in
+// about half of the 256 VGPRs with everything else (measured: no scratch) run two workgroups per
+// CU; larger ones run one, with the AGPR half of the register file available.
+template <int MT, int NF, int D>
+constexpr int packed_regs() {
+  return (D * (NF + MT) + NF * MT) * 4;
+}
+template <int MT, int NF, int D>
+constexpr bool packed_two_per_cu() {
+  return packed_regs<MT, NF, D>() <= 128 && (MT <= 6 || packed_regs<MT, NF, D>() <= 104);
+}
+template <int MT, int NF, int D>
+constexpr int packed_min_blocks() {
+  return packed_two_per_cu<MT, NF, D>() ? 2 : 1;
+}
+
+template <int DT, int MT, int NF, int D>
+__global__ __launch_bounds__(64 * kPackedWaves, (packed_min_blocks<MT, NF, D>())) void packed_gemm_kernel(PackedArgs a) {
+  __shared__ int last_flag;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  f32x4* red = packed_lds;
+  char* xt = reinterpret_cast<char*>(packed_lds) + static_cast<size_t>(kPackedWaves) * NF * MT * kFragBytes +
+             static_cast<size_t>(wave) * MT * kXTileBytes;
+  const int xt_write = (lane >> 2) * 80 + (lane & 3) * 16;
+  const int xt_read = (lane & 15) * 80 + (lane >> 4) * 16;
+  const int64_t epoch = a.sync ? sgpr64(collect(reinterpret_cast<const int64_t*>(a.counters + kPkEpochSlot))) : 0;
+
+  u32x4 wb[D][NF], xb[D][MT];
+  // The first weight stages of linear `gi` may already be in flight (requested before the last
+  // grid barrier): then only X is still to be loaded for them.
+  bool w_ready = false;
+  for (int gi = 0; gi < a.count; ++gi) {
+    const PLinear L = load_linear<NF>(a, gi);
+    POffsets<MT, NF> o;
+    packed_offsets<MT, NF>(L, a.M, lane, o);
+    const auto wr = make_rsrc(L.wp, static_cast<uint32_t>((L.N + 15) >> 4) * L.Ks * kFragBytes);
+    const auto xr = make_rsrc(L.x, static_cast<uint32_t>(a.M * L.ldx * 2));
+    PCursor ld{static_cast<int>(blockIdx.x), 0, 0, 0, 0};
+    pc_enter<NF, D>(L, wave, ld);
+    PCursor cp = ld;
+    if (ld.item < L.items) {
+      if (!w_ready) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+          issue_w<NF>(wr, ld, L.items, o.wo, wb[j]);
+          issue_x<MT, NF>(xr, ld, L.items, L.Ks, o, xb[j]);
+          pc_advance<NF, D>(L, a.G, wave, ld);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+          issue_x<MT, NF>(xr, ld, L.items, L.Ks, o, xb[j]);
+          pc_advance<NF, D>(L, a.G, wave, ld);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      for (;;) {
+        f32x4 acc[NF][MT];
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+#pragma unroll
+          for (int t = 0; t < MT; ++t) acc[f][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const int steps = cp.pend - cp.st;  // a multiple of D
+        for (int i = 0; i < steps; i += D) {
+#pragma unroll
+          for (int j = 0; j < D; ++j) {
+            u32x4 xop[MT];
+#pragma unroll
+            for (int t = 0; t < MT; ++t) *reinterpret_cast<u32x4*>(xt + t * kXTileBytes + xt_write) = xb[j][t];
+#pragma unroll
+            for (int t = 0; t < MT; ++t) xop[t] = *reinterpret_cast<const u32x4*>(xt + t * kXTileBytes + xt_read);
+#pragma unroll
+            for (int f = 0; f < NF; ++f)
+#pragma unroll
+              for (int t = 0; t < MT; ++t) acc[f][t] = mfma_16x16x32<DT>(wb[j][f], xop[t], acc[f][t]);
+            issue_w<NF>(wr, ld, L.items, o.wo, wb[j]);
+            issue_x<MT, NF>(xr, ld, L.items, L.Ks, o, xb[j]);
+            pc_advance<NF, D>(L, a.G, wave, ld);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+        packed_finish<DT, MT, NF>(L, a.M, cp.item, wave, lane, acc, red, &last_flag);
+        cp.item += a.G;
+        if (cp.item >= L.items) break;
+        pc_enter<NF, D>(L, wave, cp);
+      }
+    }
+    w_ready = false;
+    if (L.consumed && gi + 1 < a.count) {
+      // Arrive, request the next linear's first weight stages into registers and more of its
+      // weights into the caches (weights never depend on the barrier), then wait for every
+      // workgroup's part of this Y.
+      __builtin_amdgcn_s_waitcnt(0);
+      barrier_arrive(a, epoch, L.seq);
+      const PLinear Ln = load_linear<NF>(a, gi + 1);
+      PCursor nx{static_cast<int>(blockIdx.x), 0, 0, 0, 0};
+      pc_enter<NF, D>(Ln, wave, nx);
+      if (nx.item < Ln.items) {
+        POffsets<MT, NF> on;
+        packed_offsets<MT, NF>(Ln, a.M, lane, on);
+        const auto wrn = make_rsrc(Ln.wp, static_cast<uint32_t>((Ln.N + 15) >> 4) * Ln.Ks * kFragBytes);
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+          issue_w<NF>(wrn, nx, Ln.items, on.wo, wb[j]);
+          pc_advance<NF, D>(Ln, a.G, wave, nx);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        w_ready = true;
+        warm_weights<NF, D>(Ln, a.G, wave, lane, nx, wrn, on.wo, (PkLdsVoid*)red);
+      }
+      barrier_wait(a, epoch, L.seq, lane);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+}
+
+// Compiled configurations (all without scratch): 1 <= MT <= 8, NF in {1, 2, 4}, D in
+// {2, 4, 6, 8}, at most 20 accumulator fragments, and either two workgroups per CU or, for
+// MT <= 4, one workgroup per CU with the pipeline's registers within 320 of a lane's 512.
+template <int MT, int NF, int D>
+constexpr bool packed_compiled() {
+  if (MT < 1 || MT > 8 || (NF != 1 && NF != 2 && NF != 4) || (D != 2 && D != 4 && D != 6 && D != 8)) return false;
+  if (NF * MT > 20) return false;
+  return packed_two_per_cu<MT, NF, D>() || (MT <= 4 && packed_regs<MT, NF, D>() <= 320);
+}
+
+template <int MT, int NF>
+constexpr size_t packed_lds_bytes() {
+  return static_cast<size_t>(kPackedWaves) * (NF * MT * kFragBytes + MT * kXTileBytes);
+}
+
+// Launches with G = min(a.G, resident workgroups), where a.G arrives as the most items of any
+// linear; a chained launch with grid barriers (a.sync) uses every resident workgroup. `dry` only
+// checks that the kernel exists.
+template <int DT, int MT, int NF, int D>
+hipError_t packed_launch(PackedArgs& a, int cus, hipStream_t stream, bool dry) {
+  if constexpr (!packed_compiled<MT, NF, D>()) {
+    return hipErrorInvalidConfiguration;
+  } else {
+    if (dry) return hipSuccess;
+    auto kern = packed_gemm_kernel<DT, MT, NF, D>;
+    constexpr size_t lds = packed_lds_bytes<MT, NF>();
+    static int per_cu = 0;
+    if (per_cu == 0) {
+      if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (e != hipSuccess) return e;
+      }
+      int n = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(kern), 64 * kPackedWaves, lds) !=
+              hipSuccess ||
+          n < 1)
+        return hipErrorInvalidConfiguration;
+      per_cu = n;
+    }
+    const int resident = min(cus * per_cu, kPkMaxWorkgroups);
+    if (a.count == 0) {  // query: the resident workgroups a chained launch would use
+      a.G = resident;
+      return hipSuccess;
+    }
+    a.G = a.sync ? resident : min(a.G, resident);
+    if (a.G < 1) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL(kern, dim3(a.G), dim3(64 * kPackedWaves), lds, stream, a);
+    if (a.sync) hipLaunchKernelGGL(packed_epoch_kernel<>, dim3(1), dim3(64), 0, stream, a.counters);
+    return hipGetLastError();
+  }
+}
+
+template <int DT, int MT, int NF>
+hipError_t packed_pick_d(PackedArgs& a, int d, int cus, hipStream_t s, bool dry) {
+  if (d == 2) return packed_launch<DT, MT, NF, 2>(a, cus, s, dry);
+  if (d == 4) return packed_launch<DT, MT, NF, 4>(a, cus, s, dry);
+  if (d == 6) return packed_launch<DT, MT, NF, 6>(a, cus, s, dry);
+  if (d == 8) return packed_launch<DT, MT, NF, 8>(a, cus, s, dry);
+  return hipErrorInvalidConfiguration;
+}
+
+template <int DT, int MT>
+hipError_t packed_pick(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry) {
+  if (nf == 1) return packed_pick_d<DT, MT, 1>(a, d, cus, s, dry);
+  if (nf == 2) return packed_pick_d<DT, MT, 2>(a, d, cus, s, dry);
+  if (nf == 4) return packed_pick_d<DT, MT, 4>(a, d, cus, s, dry);
+  return hipErrorInvalidConfiguration;
+}
+
+template <int DT>
+hipError_t packed_dispatch(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry) {
+  switch ((a.M + 15) / 16) {
+    case 1: return packed_pick<DT, 1>(a, nf, d, cus, s, dry);
+    case 2: return packed_pick<DT, 2>(a, nf, d, cus, s, dry);
+    case 3: return packed_pick<DT, 3>(a, nf, d, cus, s, dry);
+    case 4: return packed_pick<DT, 4>(a, nf, d, cus, s, dry);
+    case 5: return packed_pick<DT, 5>(a, nf, d, cus, s, dry);
+    case 6: return packed_pick<DT, 6>(a, nf, d, cus, s, dry);
+    case 7: return packed_pick<DT, 7>(a, nf, d, cus, s, dry);
+    case 8: return packed_pick<DT, 8>(a, nf, d, cus, s, dry);
+  }
+  return hipErrorInvalidConfiguration;
+}
+
+hipError_t packed_dispatch_bf16(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_f16(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+
+}  // namespace plm

@@ -51,7 +51,7 @@ constexpr int kErrorSlot = 2;     // 1 once a bounded wait gave up (results are 
 constexpr int kArriveBase = 64;   // split-K arrival counters, one per (linear, tile)
 constexpr int kDoneBase = 32768;  // tile-done flags of linears read later in the chain
 constexpr int kArriveCapacity = kDoneBase - kArriveBase;
-constexpr int kDoneCapacity = static_cast<int>(kMaxCounters) - kDoneBase;
+constexpr int kDoneCapacity = kStreamDoneEnd - kDoneBase;
 constexpr int kStreamKW = 4;      // compute wavefronts per workgroup
 constexpr int kStreamU = 2;       // 32-wide K steps per chunk: one 128-byte line per row
 #ifndef PLM_STREAM_LOADERS

@@ -308,7 +308,7 @@ hipError_t verify_dispatch(const VerifyArgs& a, const plm_tile& t, int cu, hipSt
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
-// Workspace layout: counter area (counter 0 used) | own[R] | state[kMaxVerifyGroups][R][3] |
+// Workspace layout: counter area (int kVerifyCounter used) | own[R] | state[kMaxVerifyGroups][R][3] |
 // state_idx[kMaxVerifyGroups][R]
 void verify_layout(int64_t R, size_t& own_off, size_t& state_off, size_t& idx_off, size_t& total) {
   own_off = kCounterBytes;
@@ -374,7 +374,7 @@ int plm_lm_head_verify(int32_t dtype, const void* x, int64_t ldx, const void* w,
   a.accept = accept;
   a.argmax = argmax;
   char* ws = static_cast<char*>(workspace);
-  a.counter = reinterpret_cast<int*>(ws);
+  a.counter = reinterpret_cast<int*>(ws) + plm::kVerifyCounter;
   a.own = reinterpret_cast<float*>(ws + own_off);
   a.state = reinterpret_cast<float*>(ws + state_off);
   a.state_idx = reinterpret_cast<int*>(ws + idx_off);

@@ -31,6 +31,15 @@ EXPORTS = (
     "plm_gemm_chain",
     "plm_gemm_workspace_bytes",
     "plm_gemm_tile_supported",
+    "plm_packed_weight_bytes",
+    "plm_pack_weight",
+    "plm_gemm_packed",
+    "plm_gemm_packed_f32out",
+    "plm_gemm_packed_workspace_bytes",
+    "plm_gemm_packed_tile_supported",
+    "plm_gemm_chain_packed_prepare",
+    "plm_gemm_chain_packed",
+    "plm_gemm_packed_resident_workgroups",
     "plm_lm_head_verify",
     "plm_lm_head_verify_workspace_bytes",
     "plm_status_string",
@@ -78,6 +87,24 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.plm_gemm_workspace_bytes.restype = c_sz
     lib.plm_gemm_tile_supported.argtypes = [c_i32, c_i64, c_i64, tile_p]
     lib.plm_gemm_tile_supported.restype = ctypes.c_int
+    lib.plm_packed_weight_bytes.argtypes = [c_i64, c_i64]
+    lib.plm_packed_weight_bytes.restype = c_sz
+    lib.plm_pack_weight.argtypes = [c_i32, c_p, c_i64, c_i64, c_i64, c_p, c_sz, c_p]
+    lib.plm_pack_weight.restype = ctypes.c_int
+    lib.plm_gemm_packed.argtypes = [c_i32, c_p, c_i64, c_p, c_p, c_i64, c_i64, c_i64, c_i64, tile_p, c_p, c_sz, c_p]
+    lib.plm_gemm_packed.restype = ctypes.c_int
+    lib.plm_gemm_packed_f32out.argtypes = lib.plm_gemm_packed.argtypes
+    lib.plm_gemm_packed_f32out.restype = ctypes.c_int
+    lib.plm_gemm_packed_workspace_bytes.argtypes = [c_i64, c_i64, c_i64, tile_p]
+    lib.plm_gemm_packed_workspace_bytes.restype = c_sz
+    lib.plm_gemm_packed_tile_supported.argtypes = [c_i32, c_i64, c_i64, tile_p]
+    lib.plm_gemm_packed_tile_supported.restype = ctypes.c_int
+    lib.plm_gemm_chain_packed_prepare.argtypes = [chain_p, c_i32, c_i64, tile_p]
+    lib.plm_gemm_chain_packed_prepare.restype = c_i64
+    lib.plm_gemm_chain_packed.argtypes = [c_i32, chain_p, c_p, c_i32, c_i64, tile_p, c_p, c_sz, c_p]
+    lib.plm_gemm_chain_packed.restype = ctypes.c_int
+    lib.plm_gemm_packed_resident_workgroups.argtypes = [c_i32, c_i64, tile_p]
+    lib.plm_gemm_packed_resident_workgroups.restype = ctypes.c_int
     lib.plm_lm_head_verify.argtypes = [c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, c_p, ctypes.c_float, c_i32,
                                        c_p, c_p, tile_p, c_p, c_sz, c_p]
     lib.plm_lm_head_verify.restype = ctypes.c_int

@@ -1,10 +1,13 @@
 """A chain of linears in one launch: the round's linears back to back, where a linear may read an
-earlier one's output (``plm_gemm_chain`` in ``include/plm_amd.h``).
+earlier one's output (``plm_gemm_chain_packed`` / ``plm_gemm_chain`` in ``include/plm_amd.h``).
 
 The reference replays a round as a CUDA graph of separate ``fast_gemm`` launches, 4L+1 of them
-(plm/decoder.py:312-324, plm/fast_gemm.py:82-97). On MI355X each dependent launch costs about
-1.6 us of idle HBM between kernels; a chain keeps one persistent grid streaming weights across
-the linears and starts each tile of a linear as soon as the producer tiles it reads are written.
+(plm/decoder.py:312-324, plm/fast_gemm.py:82-97). On MI355X every launch pays a few microseconds
+of start-up and tail in which HBM idles; a chain keeps one persistent grid streaming weights
+across the linears. With packed weights (the default) the workgroups meet at a grid barrier after
+each linear another one reads, with the next linear's first weights already requested; the
+streaming kernel on row-major weights (``packed=False``) starts each tile of a linear as soon as
+the producer tiles it reads are written.
 """
 
 from __future__ import annotations
@@ -15,7 +18,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .fast_gemm import Config, HALF_DTYPES, _tile, workspace
+from .fast_gemm import Config, HALF_DTYPES, _tile, packed_weight, workspace
 
 
 @dataclass
@@ -34,11 +37,12 @@ class LinearChain:
     """Validated, prepared chain; ``run()`` launches it on the current stream (graph-capturable
     once constructed: the descriptor upload and workspace sizing happen here)."""
 
-    def __init__(self, links: list[Link], cfg: Config):
+    def __init__(self, links: list[Link], cfg: Config, packed: bool = True):
         if not links:
             raise ValueError("a chain needs at least one linear")
         self.links = links
         self.cfg = dict(cfg)
+        self.packed = packed
         x0 = links[0].x
         self.device = x0.device
         self.dtype = x0.dtype
@@ -57,14 +61,15 @@ class LinearChain:
             if ln.y.dtype not in (self.dtype, torch.float32):
                 raise TypeError(f"link {i}: y must be {self.dtype} or float32")
             g = arr[i]
-            g.x, g.w, g.y = ln.x.data_ptr(), ln.w.data_ptr(), ln.y.data_ptr()
+            g.x, g.w, g.y = ln.x.data_ptr(), (packed_weight(ln.w) if packed else ln.w).data_ptr(), ln.y.data_ptr()
             g.ldx, g.ldw, g.ldy = ln.x.stride(0), ln.w.stride(0), ln.y.stride(0)
             g.N, g.K = ln.w.shape[0], ln.w.shape[1]
             g.split_k, g.dep = ln.split_k, ln.dep
             g.out_f32 = int(ln.y.dtype == torch.float32)
         self._tile = _tile(self.cfg)
         lib = _lib.lib()
-        need = int(lib.plm_gemm_chain_prepare(arr, len(links), self.M, self._tile))
+        prepare = lib.plm_gemm_chain_packed_prepare if packed else lib.plm_gemm_chain_prepare
+        need = int(prepare(arr, len(links), self.M, self._tile))
         if need < 0:
             _lib.check(need, "plm_gemm_chain_prepare")
         self.host = arr
@@ -75,9 +80,9 @@ class LinearChain:
 
     def run(self) -> None:
         lib = _lib.lib()
-        status = lib.plm_gemm_chain(_lib.DTYPE_CODES[self.dtype], self.host, self.table.data_ptr(), len(self.links),
-                                    self.M, self._tile, self.ws.data_ptr(), self.ws.numel(),
-                                    _lib.stream_handle(self.device))
+        entry = lib.plm_gemm_chain_packed if self.packed else lib.plm_gemm_chain
+        status = entry(_lib.DTYPE_CODES[self.dtype], self.host, self.table.data_ptr(), len(self.links), self.M,
+                       self._tile, self.ws.data_ptr(), self.ws.numel(), _lib.stream_handle(self.device))
         _lib.check(status, f"plm_gemm_chain({len(self.links)} linears, M={self.M}, cfg={self.cfg})")
 
     def error_flag(self) -> int:

@@ -2,6 +2,8 @@
 ``plm.fast_gemm`` (plm/fast_gemm.py).
 
 ``C[M,N] = A[M,K] @ W[N,K]^T`` with fp32 accumulation on gfx950 MFMA, output in the input dtype.
+The kernel reads W in a packed fragment layout (``plm_pack_weight``); each weight tensor is packed
+once, on its first use, and the packed copy is kept while the tensor lives and is unchanged.
 Split-K partials are combined inside the same launch in a fixed order, so results are bitwise
 reproducible run to run (plm/fast_gemm.py:3-4). ``install`` routes eligible calls through the
 kernel: the build's own dispatch slot always, and vLLM's ``default_unquantized_gemm`` when vLLM is
@@ -15,6 +17,7 @@ import threading
 
 import torch
 import torch.nn.functional as F
+from torch.utils.weak import WeakTensorKeyDictionary
 
 from . import _lib
 
@@ -27,6 +30,10 @@ HALF_DTYPES = (torch.bfloat16, torch.float16)
 CONFIGS: dict[tuple[int, int, int], Config] = {}
 
 _tiles: dict[tuple[int, int, int, int], _lib.Tile] = {}
+# weight tensor -> ((data_ptr, shape, row stride, version counter), packed copy); entries go with
+# the tensor
+_packed = WeakTensorKeyDictionary()
+_pack_lock = threading.Lock()
 _workspaces: dict[int, torch.Tensor] = {}
 _ws_lock = threading.Lock()
 
@@ -59,11 +66,46 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 
 
 def gemm_workspace_bytes(M: int, N: int, K: int, cfg: Config) -> int:
-    return int(_lib.lib().plm_gemm_workspace_bytes(M, N, K, _tile(cfg)))
+    return int(_lib.lib().plm_gemm_packed_workspace_bytes(M, N, K, _tile(cfg)))
 
 
 def tile_supported(M: int, K: int, cfg: Config, dtype: torch.dtype = torch.bfloat16) -> bool:
-    return bool(_lib.lib().plm_gemm_tile_supported(_lib.DTYPE_CODES[dtype], M, K, _tile(cfg)))
+    return bool(_lib.lib().plm_gemm_packed_tile_supported(_lib.DTYPE_CODES[dtype], M, K, _tile(cfg)))
+
+
+def pack_weight(w: torch.Tensor) -> torch.Tensor:
+    """``w[N,K]`` rearranged into the kernel's fragment layout (a new uint8 device tensor of
+    ``plm_packed_weight_bytes(N, K)`` bytes)."""
+    if w.dim() != 2 or w.dtype not in HALF_DTYPES or not w.is_cuda:
+        raise ValueError(f"pack_weight expects a 2-D bf16/fp16 GPU tensor, got {tuple(w.shape)} {w.dtype}")
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("a weight is packed on its first use, which cannot happen during graph capture; "
+                           "run the shape eagerly (or call packed_weight) before capturing")
+    w = _row_major(w)
+    N, K = w.shape
+    lib = _lib.lib()
+    nbytes = int(lib.plm_packed_weight_bytes(N, K))
+    out = torch.empty(nbytes, dtype=torch.uint8, device=w.device)
+    status = lib.plm_pack_weight(_lib.DTYPE_CODES[w.dtype], w.data_ptr(), w.stride(0), N, K, out.data_ptr(), nbytes,
+                                 _lib.stream_handle(w.device))
+    _lib.check(status, f"plm_pack_weight(N={N}, K={K})")
+    return out
+
+
+def packed_weight(w: torch.Tensor) -> torch.Tensor:
+    """The packed copy of ``w``, made on first use and reused while ``w`` lives unchanged (same
+    storage, shape, stride and version counter)."""
+    key = (w.data_ptr(), tuple(w.shape), w.stride(0), w._version)
+    hit = _packed.get(w)
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    with _pack_lock:
+        hit = _packed.get(w)
+        if hit is not None and hit[0] == key:
+            return hit[1]
+        p = pack_weight(w)
+        _packed[w] = (key, p)
+        return p
 
 
 def reserve_workspace(device: torch.device, shapes: dict[tuple[int, int, int], Config] | None = None) -> None:
@@ -81,11 +123,39 @@ def _row_major(t: torch.Tensor) -> torch.Tensor:
     return t.contiguous()
 
 
+def launch_packed(a: torch.Tensor, wp: torch.Tensor, N: int, cfg: Config, out: torch.Tensor,
+                  f32_out: bool = False) -> torch.Tensor:
+    """``out = a @ W^T`` for a packed W (``pack_weight``) of N rows; ``out`` row-major."""
+    M, K = a.shape
+    a = _row_major(a)
+    tile = _tile(cfg)
+    lib = _lib.lib()
+    need = int(lib.plm_gemm_packed_workspace_bytes(M, N, K, tile))
+    ws_ptr, ws_bytes = None, 0
+    if need:
+        ws = workspace(a.device, need)
+        ws_ptr, ws_bytes = ws.data_ptr(), ws.numel()
+    entry = lib.plm_gemm_packed_f32out if f32_out else lib.plm_gemm_packed
+    status = entry(_lib.DTYPE_CODES[a.dtype], a.data_ptr(), a.stride(0), wp.data_ptr(), out.data_ptr(), out.stride(0),
+                   M, N, K, tile, ws_ptr, ws_bytes, _lib.stream_handle(a.device))
+    _lib.check(status, f"plm_gemm_packed(M={M}, N={N}, K={K}, cfg={cfg})")
+    return out
+
+
 def _launch(a: torch.Tensor, w: torch.Tensor, cfg: Config, out: torch.Tensor, f32_out: bool) -> torch.Tensor:
+    return launch_packed(a, packed_weight(w), w.shape[0], cfg, out, f32_out)
+
+
+def hip_linear_rowmajor(a: torch.Tensor, w: torch.Tensor, cfg: Config, out: torch.Tensor | None = None,
+                        f32_out: bool = False) -> torch.Tensor:
+    """``a @ w.T`` on the streaming kernel that reads W row-major (``plm_gemm``; no packed copy).
+    Its tiles: ``64*wave_frags`` rows, ``unroll`` = 2 (``tiles.stream_compiled``)."""
+    _check_operands(a, w)
     M, K = a.shape
     N = w.shape[0]
-    a = _row_major(a)
-    w = _row_major(w)
+    if out is None:
+        out = torch.empty(M, N, device=a.device, dtype=torch.float32 if f32_out else a.dtype)
+    a, w = _row_major(a), _row_major(w)
     tile = _tile(cfg)
     lib = _lib.lib()
     need = int(lib.plm_gemm_workspace_bytes(M, N, K, tile))
@@ -163,7 +233,7 @@ def install(configs: dict[tuple[int, int, int], Config]) -> None:
     global default_unquantized_gemm
     lib = _lib.lib()
     for (M, N, K), cfg in configs.items():
-        if not lib.plm_gemm_tile_supported(_lib.PLM_BF16, M, K, _tile(cfg)):
+        if not lib.plm_gemm_packed_tile_supported(_lib.PLM_BF16, M, K, _tile(cfg)):
             raise ValueError(f"no compiled MI355X kernel for tile {cfg} at (M={M}, N={N}, K={K})")
     CONFIGS.update(configs)
     default_unquantized_gemm = fast_gemm

@@ -1,11 +1,14 @@
 """Tile selection for shapes without a tuned table entry, and the candidate set the tuner sweeps.
 
 A tile is ``{"wave_frags", "k_waves", "split_k", "unroll"}`` (``struct plm_tile`` in
-``include/plm_amd.h``): ``k_waves`` (= 4) compute wavefronts each own ``16*wave_frags`` weight
-rows, so a tile is ``64*wave_frags`` rows over its whole K range; ``split_k`` workgroups split K;
-``unroll`` (= 2) 32-wide K steps are streamed per chunk. Items (tile x split) =
-``ceil(N / (64*wave_frags)) * split_k``; the persistent grid has one workgroup per compute unit
-(more where LDS allows).
+``include/plm_amd.h``). For the packed-weight GEMM behind ``fast_gemm`` (plm_gemm_packed): a
+workgroup tile is ``16*wave_frags`` weight rows; its ``k_waves`` (= 4) wavefronts split the tile's
+K range and are summed in LDS; ``split_k`` workgroups split K further (fp32 partials summed in
+split order); ``unroll`` (2, 4 or 6) K steps of loads are in flight per wavefront. Items
+(tile x split) = ``ceil(ceil(N/16) / wave_frags) * split_k`` over a persistent grid.
+
+The chained round (plm_gemm_chain) uses the streaming kernel's tiles: ``64*wave_frags`` rows,
+``unroll`` = 2 (``chain_tile``, ``chain_split`` below).
 """
 
 from __future__ import annotations
@@ -14,9 +17,98 @@ import math
 
 CU_COUNT = 256          # MI355X compute units
 K_WAVES = 4
-UNROLL = 2
 WAVE_FRAGS = (1, 2, 4)
+DEPTHS = (2, 4, 6, 8)
 SPLITS = (1, 2, 3, 4, 6, 8, 12, 16)
+
+
+def _regs(mt: int, nf: int, d: int) -> int:
+    return (d * (nf + mt) + nf * mt) * 4
+
+
+def two_per_cu(M: int, cfg: dict) -> bool:
+    """Whether two workgroups of this tile share a CU (mirrors ``packed_two_per_cu``)."""
+    mt, nf, d = math.ceil(M / 16), cfg["wave_frags"], cfg["unroll"]
+    r = _regs(mt, nf, d)
+    return r <= 128 and (mt <= 6 or r <= 104)
+
+
+def compiled(M: int, cfg: dict) -> bool:
+    """Whether the library has a packed-GEMM kernel for this tile at width M (mirrors
+    ``packed_compiled`` in csrc/packed_gemm.h: at most 20 accumulator fragments, and two
+    workgroups per CU, or one with the pipeline within 320 registers for M <= 64)."""
+    mt, nf, d = math.ceil(M / 16), cfg["wave_frags"], cfg["unroll"]
+    if not (1 <= mt <= 8 and nf in WAVE_FRAGS and d in DEPTHS and cfg["k_waves"] == K_WAVES):
+        return False
+    return nf * mt <= 20 and (two_per_cu(M, cfg) or (mt <= 4 and _regs(mt, nf, d) <= 320))
+
+
+def items(N: int, cfg: dict) -> int:
+    return math.ceil(math.ceil(N / 16) / cfg["wave_frags"]) * cfg["split_k"]
+
+
+def steps_per_wave(K: int, cfg: dict) -> int:
+    """32-wide K steps each wavefront streams per item (the shortest quarter)."""
+    return math.ceil(K / 32) // cfg["split_k"] // K_WAVES
+
+
+def candidates(M: int, N: int, K: int, supported=None) -> list[dict]:
+    """Every sensible tile for ``(M, N, K)``; ``supported(cfg) -> bool`` filters to compiled kernels."""
+    out = []
+    for nf in WAVE_FRAGS:
+        for d in DEPTHS:
+            for split in SPLITS:
+                cfg = {"wave_frags": nf, "k_waves": K_WAVES, "split_k": split, "unroll": d}
+                if not compiled(M, cfg) or items(N, cfg) > 64 * CU_COUNT:
+                    continue
+                if split > 1 and (steps_per_wave(K, cfg) < 2 or
+                                  items(N, dict(cfg, split_k=max(1, split // 2))) >= 4 * CU_COUNT):
+                    continue  # too little K per wavefront, or plenty of items with half the splitting
+                if supported is not None and not supported(cfg):
+                    continue
+                out.append(cfg)
+    return out
+
+
+def heuristic_tile(M: int, N: int, K: int, supported=None) -> dict:
+    """A reasonable tile without measurement (what the MI355X measurements of the round shapes
+    favour): 32-row tiles with a two-stage pipeline, and K splitting until about three quarters
+    of the compute units have an item, keeping at least two K steps per wavefront."""
+    for nf in (2, 4, 1):
+        for d in (2, 4, 6, 8):
+            cfg = {"wave_frags": nf, "k_waves": K_WAVES, "split_k": 1, "unroll": d}
+            if not compiled(M, cfg) or (supported is not None and not supported(cfg)):
+                continue
+            split = 1
+            while (items(N, dict(cfg, split_k=split)) < CU_COUNT * 3 // 4 and
+                   steps_per_wave(K, dict(cfg, split_k=2 * split)) >= 2 and split < 16):
+                split *= 2
+            return dict(cfg, split_k=split)
+    raise ValueError(f"no compiled tile fits (M={M}, N={N}, K={K})")
+
+
+def packed_chain_split(N: int, K: int, cfg: dict, workgroups: int) -> int:
+    """K split of one linear of a packed chain (every linear ends at a grid barrier, so its time
+    is that of the busiest workgroup): the split with the least estimated busiest-workgroup time,
+    counting each item's K steps per wavefront plus a fixed cost of a few steps for the item's end
+    (reduction, stores; with split > 1 the partial round trip)."""
+    tiles_ = math.ceil(math.ceil(N / 16) / cfg["wave_frags"])
+    ks = math.ceil(K / 32)
+    best, best_cost = 1, None
+    for split in SPLITS:
+        if split > 1 and ks // split // K_WAVES < 2:
+            break
+        per_wg = math.ceil(tiles_ * split / workgroups)
+        steps = max(cfg["unroll"], math.ceil(ks / split / K_WAVES))
+        cost = per_wg * (steps + (3 if split == 1 else 8))
+        if best_cost is None or cost < best_cost:
+            best, best_cost = split, cost
+    return best
+
+
+# ---------------------------------------------------------------- streaming kernel (chains)
+
+STREAM_UNROLL = 2
 LDS_BYTES = 160 * 1024 - 256
 TABLE_RESERVE = 16 * 1024
 LOADERS = 4             # loader wavefronts per workgroup (PLM_STREAM_LOADERS in csrc/stream_gemm.h)
@@ -31,8 +123,8 @@ def _slot(M: int, nf: int) -> int:
 
 
 def ring_slots(M: int, cfg: dict, table_bytes: int = TABLE_RESERVE) -> int:
-    """Chunk slots of the workgroup's LDS ring (mirrors ``ring_for_table`` in csrc/stream_gemm.h):
-    what fits beside the descriptor table, at most 8; 0 if under two."""
+    """Chunk slots of the streaming kernel's LDS ring (mirrors ``ring_for_table`` in
+    csrc/stream_gemm.h): what fits beside the descriptor table, at most 8; 0 if under two."""
     slot = _slot(M, cfg["wave_frags"])
     free = LDS_BYTES - table_bytes
     if free <= 0:
@@ -41,64 +133,28 @@ def ring_slots(M: int, cfg: dict, table_bytes: int = TABLE_RESERVE) -> int:
     return r if r >= 2 else 0
 
 
-def compiled(M: int, cfg: dict) -> bool:
-    """Whether the library has a kernel for this tile at width M (mirrors ``stream_compiled`` in
-    csrc/stream_gemm.h: a ring at least two chunks deep with the largest descriptor table, and at
-    most 64 accumulator VGPRs per compute wavefront)."""
+def stream_compiled(M: int, cfg: dict) -> bool:
+    """Whether the streaming kernel (plm_gemm, plm_gemm_chain) is compiled for this tile at width M
+    (mirrors ``stream_compiled`` in csrc/stream_gemm.h)."""
     mt, nf = math.ceil(M / 16), cfg["wave_frags"]
-    if not (1 <= mt <= 8 and nf in WAVE_FRAGS and cfg["unroll"] == UNROLL and cfg["k_waves"] == K_WAVES):
+    if not (1 <= mt <= 8 and nf in WAVE_FRAGS and cfg["unroll"] == STREAM_UNROLL and cfg["k_waves"] == K_WAVES):
         return False
     if ring_slots(M, cfg) < 2:
         return False
     return nf * mt <= 16
 
 
-def items(N: int, cfg: dict) -> int:
-    return math.ceil(N / (64 * cfg["wave_frags"])) * cfg["split_k"]
-
-
 def chunks_per_item(K: int, cfg: dict) -> int:
-    return math.ceil(math.ceil(K / 32) / cfg["split_k"] / UNROLL)
-
-
-def candidates(M: int, N: int, K: int, supported=None) -> list[dict]:
-    """Every sensible tile for ``(M, N, K)``; ``supported(cfg) -> bool`` filters to compiled kernels."""
-    out = []
-    for nf in WAVE_FRAGS:
-        for split in SPLITS:
-            cfg = {"wave_frags": nf, "k_waves": K_WAVES, "split_k": split, "unroll": UNROLL}
-            if chunks_per_item(K, cfg) < 2 or items(N, cfg) > 64 * CU_COUNT:
-                continue
-            if split > 1 and items(N, dict(cfg, split_k=max(1, split // 2))) >= 2 * CU_COUNT:
-                continue  # plenty of items with half the splitting
-            if supported is not None and not supported(cfg):
-                continue
-            out.append(cfg)
-    return out
-
-
-def heuristic_tile(M: int, N: int, K: int, supported=None) -> dict:
-    """A reasonable tile without measurement: the widest weight tile that is compiled, and enough
-    K splitting to give every compute unit an item while each item keeps at least four chunks."""
-    for nf in (2, 1, 4):
-        cfg = {"wave_frags": nf, "k_waves": K_WAVES, "split_k": 1, "unroll": UNROLL}
-        if not compiled(M, cfg) or (supported is not None and not supported(cfg)):
-            continue
-        split = 1
-        while (items(N, dict(cfg, split_k=split)) < CU_COUNT and chunks_per_item(K, dict(cfg, split_k=2 * split)) >= 4
-               and split < 16):
-            split *= 2
-        return dict(cfg, split_k=split)
-    raise ValueError(f"no compiled tile fits (M={M}, N={N}, K={K})")
+    return math.ceil(math.ceil(K / 32) / cfg["split_k"] / STREAM_UNROLL)
 
 
 # Tile of a chained round (plm_gemm_chain): 64-row tiles.
-CHAIN_TILE = {"wave_frags": 1, "k_waves": K_WAVES, "split_k": 1, "unroll": UNROLL}
+CHAIN_TILE = {"wave_frags": 1, "k_waves": K_WAVES, "split_k": 1, "unroll": STREAM_UNROLL}
 
 
 def chain_tile(M: int) -> dict:
     """CHAIN_TILE at width M (64-row tiles are compiled at every width up to 128)."""
-    if not compiled(M, CHAIN_TILE):
+    if not stream_compiled(M, CHAIN_TILE):
         raise ValueError(f"no chain tile is compiled at M={M}")
     return dict(CHAIN_TILE)
 

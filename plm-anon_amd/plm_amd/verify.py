@@ -20,9 +20,10 @@ ROUND_MODES = {"fp32": _lib.PLM_ROUND_F32, "bf16": _lib.PLM_ROUND_BF16, "fp16": 
 # Default verify tile; per-shape entries may override it.
 VERIFY_CONFIG: Config = {"wave_frags": 2, "k_waves": 4, "split_k": 1, "unroll": 4}
 
-# A GEMM tile with the verify kernel's K partition (4 slices of K, summed in slice order):
-# ``hip_linear_f32`` with it returns, bit for bit, the logits every verify tile decides on.
-LOGITS_CONFIG: Config = {"wave_frags": 2, "k_waves": 4, "split_k": 4, "unroll": 2}
+# A GEMM tile with the verify kernel's K partition (the workgroup's 4 wavefronts each a quarter of
+# K, summed in wavefront order): ``hip_linear_f32`` with it returns, bit for bit, the logits every
+# verify tile decides on.
+LOGITS_CONFIG: Config = {"wave_frags": 2, "k_waves": 4, "split_k": 1, "unroll": 2}
 
 
 def verify_workspace_bytes(R: int, V: int, K: int, cfg: Config = VERIFY_CONFIG) -> int:

@@ -5,6 +5,7 @@ contract (plm/gemm_tables.py). No kernel is launched here."""
 from __future__ import annotations
 
 import ctypes
+import math
 import json
 import re
 from pathlib import Path
@@ -65,6 +66,54 @@ def test_argument_validation_happens_before_launch():
                                   1 << 30, None) == -1
     assert lib.plm_lm_head_verify(0, fake, 2048, fake, 2048, 65, 50257, 2048, fake, 0.94, 0, fake, fake, vt, fake,
                                   1 << 30, None) == -1
+
+
+def test_packed_argument_validation_happens_before_launch():
+    lib = _lib.lib()
+    tile = _lib.Tile(2, 4, 1, 2)
+    fake = 1 << 20
+    # K not a multiple of 8; M out of range; misaligned X; unknown dtype.
+    assert lib.plm_gemm_packed(0, fake, 1024, fake, fake, 4096, 42, 4096, 1020, tile, None, 0, None) == -1
+    assert lib.plm_gemm_packed(0, fake, 1024, fake, fake, 4096, 129, 4096, 1024, tile, None, 0, None) == -1
+    assert lib.plm_gemm_packed(0, fake + 2, 1024, fake, fake, 4096, 42, 4096, 1024, tile, None, 0, None) == -2
+    assert lib.plm_gemm_packed(7, fake, 1024, fake, fake, 4096, 42, 4096, 1024, tile, None, 0, None) == -1
+    # Split-K without a workspace; a pipeline depth with no kernel.
+    assert lib.plm_gemm_packed(0, fake, 1024, fake, fake, 4096, 42, 4096, 1024, _lib.Tile(2, 4, 4, 2), None, 0,
+                               None) == -4
+    assert lib.plm_gemm_packed(0, fake, 1024, fake, fake, 4096, 42, 4096, 1024, _lib.Tile(2, 4, 1, 3), None, 0,
+                               None) == -3
+    # Packing: K not a multiple of 8, destination too small.
+    assert lib.plm_pack_weight(0, fake, 1024, 4096, 1020, fake, 1 << 30, None) == -1
+    assert lib.plm_pack_weight(0, fake, 1024, 4096, 1024, fake, 1024, None) == -4
+    # A chain whose linear reads a later one's output.
+    arr = (_lib.ChainGemm * 2)()
+    for g in arr:
+        g.x, g.w, g.y, g.ldx, g.ldw, g.ldy, g.N, g.K, g.split_k = fake, fake, fake, 1024, 1024, 1024, 1024, 1024, 1
+    arr[0].dep, arr[1].dep = 1, -1
+    assert lib.plm_gemm_chain_packed_prepare(arr, 2, 56, tile) == -1
+
+
+def test_packed_sizes_and_chain_prepare():
+    lib = _lib.lib()
+    # Fragments of 16 rows x 32 K: N and K round up.
+    assert lib.plm_packed_weight_bytes(50257, 2048) == 3142 * 64 * 1024
+    assert lib.plm_packed_weight_bytes(1000, 1416) == 63 * 45 * 1024
+    assert lib.plm_gemm_packed_workspace_bytes(56, 2048, 8192, _lib.Tile(2, 4, 1, 2)) == 0
+    # One fp32 fragment (1 KiB) per (tile, split, fragment of the tile).
+    tiles_ = math.ceil(2048 / 16 / 2)
+    assert lib.plm_gemm_packed_workspace_bytes(56, 2048, 8192, _lib.Tile(2, 4, 4, 2)) == \
+        _lib.COUNTER_BYTES + tiles_ * 4 * 2 * 4 * 1024
+    # Chain: progress-flag values count the consumed linears; partials and arrival counters are
+    # reused after each of them.
+    arr = (_lib.ChainGemm * 3)()
+    for i, g in enumerate(arr):
+        g.x, g.w, g.y, g.ldx, g.ldw, g.ldy = 1 << 20, 1 << 21, (1 << 22) + i * (1 << 20), 2048, 2048, 2048
+        g.N, g.K, g.split_k, g.dep = 2048, 2048, 2, i - 1
+    need = lib.plm_gemm_chain_packed_prepare(arr, 3, 56, _lib.Tile(2, 4, 1, 2))
+    assert [g.consumed for g in arr] == [1, 1, 0]
+    assert [g.done_base for g in arr] == [1, 2, 0]
+    assert len({g.arrive_base for g in arr}) == 1 and all(g.partial_offset == 0 for g in arr)
+    assert need == _lib.COUNTER_BYTES + 64 * 2 * 2 * 4 * 1024
 
 
 def test_workspace_sizes():

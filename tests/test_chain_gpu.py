@@ -1,9 +1,10 @@
-"""GPU parity of the chained launch (plm_gemm_chain): linears back to back in one persistent grid,
-each tile of a consumer starting once the producer tiles it reads are written.
+"""GPU parity of the chained launches: linears back to back in one persistent grid, over packed
+weights (plm_gemm_chain_packed: grid barriers of per-workgroup progress flags) and over row-major
+weights (plm_gemm_chain: each consumer tile starts once the producer tiles it reads are written).
 
 Checks: every link's output equals the single-linear kernel's on the same operands bit for bit
-(same K partition), and the CPU oracle's within the GEMM tolerance; repeated launches and HIP-graph
-replays give identical results (the tile-done flags are per-launch); the error flag stays clear."""
+(same kernel, same K partition), and the CPU oracle's within the GEMM tolerance; repeated launches
+and HIP-graph replays give identical results (flags are per launch); the error flag stays clear."""
 
 from __future__ import annotations
 
@@ -13,7 +14,7 @@ import torch
 import oracle
 from plm_amd import workloads
 from plm_amd.chain import Link, LinearChain
-from plm_amd.fast_gemm import hip_linear
+from plm_amd.fast_gemm import hip_linear, hip_linear_rowmajor
 from plm_amd.tiles import chain_tile
 
 pytestmark = pytest.mark.gpu
@@ -38,24 +39,43 @@ def _chain(x, ws, splits, deps=None, ys=None):
     return links, ys
 
 
-def _check_against_single(links, cfg=CFG):
+def _check_against_single(links, cfg=CFG, packed=True):
     for i, ln in enumerate(links):
-        single = hip_linear(ln.x, ln.w, dict(cfg, split_k=ln.split_k))
+        linear = hip_linear if packed else hip_linear_rowmajor
+        single = linear(ln.x, ln.w, dict(cfg, split_k=ln.split_k))
         assert torch.equal(ln.y, single), f"link {i} differs from the single-linear kernel"
         torch.testing.assert_close(ln.y.cpu().float(), oracle.linear(ln.x.cpu(), ln.w.cpu()).float(), rtol=RTOL,
                                    atol=ATOL)
 
 
+@pytest.mark.parametrize("packed", [True, False], ids=["packed", "rowmajor"])
 @pytest.mark.parametrize("splits", [(1, 1, 1), (2, 4, 1), (3, 1, 8)])
-def test_three_links(device, splits):
+def test_three_links(device, splits, packed):
     M = 56
     g = torch.Generator(device=device).manual_seed(20)
     x = torch.randn(M, 512, generator=g, device=device).bfloat16()
     ws = _weights([(1024, 512), (512, 1024), (2000, 512)], 21, device)
     links, _ = _chain(x, ws, splits)
-    chain = LinearChain(links, CFG)
+    chain = LinearChain(links, CFG, packed=packed)
     chain.run()
-    _check_against_single(links)
+    _check_against_single(links, packed=packed)
+    assert chain.error_flag() == 0
+
+
+@pytest.mark.parametrize("cfg", [{"wave_frags": 2, "k_waves": 4, "split_k": 1, "unroll": 2},
+                                 {"wave_frags": 4, "k_waves": 4, "split_k": 1, "unroll": 8},
+                                 {"wave_frags": 1, "k_waves": 4, "split_k": 1, "unroll": 4}],
+                         ids=lambda c: f"nf{c['wave_frags']}d{c['unroll']}")
+def test_packed_chain_tiles(device, cfg):
+    # Deep and shallow pipelines, and widths whose K is not a multiple of 32 in the middle link.
+    M = 42
+    g = torch.Generator(device=device).manual_seed(30)
+    x = torch.randn(M, 1024, generator=g, device=device).bfloat16()
+    ws = _weights([(1416, 1024), (2048, 1416), (3000, 2048)], 31, device)
+    links, _ = _chain(x, ws, (2, 3, 1))
+    chain = LinearChain(links, cfg, packed=True)
+    chain.run()
+    _check_against_single(links, cfg)
     assert chain.error_flag() == 0
 
 

@@ -265,6 +265,33 @@ def test_graph_capture_and_replay(device):
     check(outs[1], *data[1])
 
 
+@pytest.mark.parametrize("cfg", [{"wave_frags": 1, "k_waves": 4, "split_k": 1, "unroll": 2},
+                                 {"wave_frags": 2, "k_waves": 4, "split_k": 4, "unroll": 2}],
+                         ids=lambda c: f"nf{c['wave_frags']}s{c['split_k']}")
+def test_rowmajor_streaming_kernel(device, cfg):
+    # plm_gemm reads W row-major (no packed copy): the same parity bar.
+    from plm_amd.fast_gemm import hip_linear_rowmajor
+
+    for (M, N, K) in ((56, 2048, 2048), (42, 1000, 1416)):
+        x, w = _inputs(M, N, K, 16)
+        check(hip_linear_rowmajor(x.to(device), w.to(device), cfg), x, w)
+
+
+def test_packed_weight_cache_follows_the_tensor(device):
+    # The packed copy is made once per weight and remade when the weight changes in place.
+    M, N, K = 56, 512, 1024
+    x, w = _inputs(M, N, K, 17)
+    xd, wd = x.to(device), w.to(device)
+    cfg = {"wave_frags": 2, "k_waves": 4, "split_k": 1, "unroll": 2}
+    first = fast_gemm.packed_weight(wd)
+    assert fast_gemm.packed_weight(wd) is first
+    check(hip_linear(xd, wd, cfg), x, w)
+    w2 = (0.02 * torch.randn(N, K)).bfloat16()
+    wd.copy_(w2.to(device))
+    assert fast_gemm.packed_weight(wd) is not first
+    check(hip_linear(xd, wd, cfg), x, w2)
+
+
 def test_wide_workgroup_count_stays_in_bounds(device):
     # Many items (N = 50304 at 64-row tiles, split 8: 6288 items, 24 per workgroup): every
     # workgroup index maps to a real tile and split slot.
