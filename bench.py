@@ -115,13 +115,13 @@ def time_graph(graph, steps, warmup):
 
 
 def kernel_class(M, K, cfg):
-    """The compiled kernel a GEMM launches: (MT, wave_frags, unroll)."""
-    return (math.ceil(M / 16), cfg["wave_frags"], cfg["unroll"])
+    """The compiled kernel a GEMM launches: (MT, wave_frags, unroll, k_waves)."""
+    return (math.ceil(M / 16), cfg["wave_frags"], cfg["unroll"], cfg["k_waves"])
 
 
 def kernel_name(cls):
-    mt, nf, d = cls
-    return f"packed_gemm_kernel<bf16, MT={mt}, NF={nf}, D={d}>"
+    mt, nf, d, kw = cls
+    return f"packed_gemm_kernel<bf16, MT={mt}, NF={nf}, D={d}, KW={kw}>"
 
 
 def dominant_kernel_roofline(rnd, steps):
@@ -334,8 +334,8 @@ def main():
                                       for r in rows]
         if chain_wins:
             # The chained launch is the round's only kernel: its HIP-event time per replay is its duration.
-            kernel = "packed_gemm_kernel<bf16, MT=%d, NF=%d, D=%d> (chained round)" % (
-                math.ceil(args.M / 16), CHAIN_CFG["wave_frags"], CHAIN_CFG["unroll"])
+            kernel = "packed_gemm_kernel<bf16, MT=%d, NF=%d, D=%d, KW=%d> (chained round)" % (
+                math.ceil(args.M / 16), CHAIN_CFG["wave_frags"], CHAIN_CFG["unroll"], CHAIN_CFG["k_waves"])
             achieved = rnd.bytes / (us_round * 1e-6) / 1e9
             result["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                                   "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),

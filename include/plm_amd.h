@@ -83,10 +83,12 @@ int plm_pack_weight(int32_t dtype, const void* w, int64_t ldw, int64_t N, int64_
  * Y[M,N] = X[M,K] · W[N,K]^T over a packed W, fp32 accumulation, Y in the input dtype: the fast
  * path behind triton_linear (plm/fast_gemm.py:82-97, with gemm_kernel 17-48 and
  * splitk_reduce_kernel 51-61). Tile fields for this kernel: wave_frags = 16-row fragments per
- * workgroup tile (1, 2, 4); k_waves = 4 (the workgroup's wavefronts split the tile's K range and
- * are summed in LDS in wavefront order); split_k = workgroups splitting K (1..64, partials summed
- * in split order); unroll = K steps of loads in flight per wavefront (2, 4, 6). Requirements as
- * plm_gemm (1 <= M <= 128, K % 8 == 0, ldx % 8 == 0, x 16-byte aligned).
+ * wavefront (1, 2, 4); k_waves = 4: a workgroup tile is 16*wave_frags rows and its four
+ * wavefronts split the tile's K range (summed in LDS in wavefront order), or k_waves = 1: a
+ * workgroup tile is 64*wave_frags rows, each wavefront owns 16*wave_frags of them over the whole
+ * K range, and the four share one copy of X through LDS; split_k = workgroups splitting K (1..64,
+ * partials summed in split order); unroll = K steps of loads in flight per wavefront (2, 4, 6,
+ * 8). Requirements as plm_gemm (1 <= M <= 128, K % 8 == 0, ldx % 8 == 0, x 16-byte aligned).
  */
 int plm_gemm_packed(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy, int64_t M,
                     int64_t N, int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream);

@@ -47,25 +47,35 @@ int64_t ksteps(int64_t K) { return (K + 31) / 32; }
 
 int64_t packed_bytes(int64_t N, int64_t K) { return (N + 15) / 16 * ksteps(K) * kFragBytes; }
 
+// k_waves = 4: the workgroup's four wavefronts split the tile's K range (tile = 16*wave_frags
+// rows); k_waves = 1: each wavefront takes its own 16*wave_frags rows (tile = 64*wave_frags rows).
 bool packed_tile_valid(const plm_tile* t) {
   return t != nullptr && (t->wave_frags == 1 || t->wave_frags == 2 || t->wave_frags == 4) &&
-         t->k_waves == kPackedWaves && t->split_k >= 1 && t->split_k <= 64 &&
+         (t->k_waves == kPackedWaves || t->k_waves == 1) && t->split_k >= 1 && t->split_k <= 64 &&
          (t->unroll == 2 || t->unroll == 4 || t->unroll == 6 || t->unroll == 8);
 }
 
 hipError_t packed_dispatch_dt(int32_t dtype, PackedArgs& a, const plm_tile& t, int cus, hipStream_t s, bool dry) {
-  if (dtype == PLM_BF16) return packed_dispatch_bf16(a, t.wave_frags, t.unroll, cus, s, dry);
-  if (dtype == PLM_F16) return packed_dispatch_f16(a, t.wave_frags, t.unroll, cus, s, dry);
+  const bool rows = t.k_waves == 1;
+  if (dtype == PLM_BF16)
+    return rows ? packed_dispatch_bf16_k1(a, t.wave_frags, t.unroll, cus, s, dry)
+                : packed_dispatch_bf16_k4(a, t.wave_frags, t.unroll, cus, s, dry);
+  if (dtype == PLM_F16)
+    return rows ? packed_dispatch_f16_k1(a, t.wave_frags, t.unroll, cus, s, dry)
+                : packed_dispatch_f16_k4(a, t.wave_frags, t.unroll, cus, s, dry);
   return hipErrorInvalidConfiguration;
 }
 
-int64_t packed_tiles(int64_t N, const plm_tile& t) { return ((N + 15) / 16 + t.wave_frags - 1) / t.wave_frags; }
+// Weight fragments (16 rows each) of one workgroup tile.
+int64_t tile_fragments(const plm_tile& t) { return t.k_waves == 1 ? kPackedWaves * t.wave_frags : t.wave_frags; }
+
+int64_t packed_tiles(int64_t N, const plm_tile& t) { return ((N + 15) / 16 + tile_fragments(t) - 1) / tile_fragments(t); }
 
 // Workspace: the counter area, then (split > 1) one fp32 fragment per (tile, split, fragment).
 int64_t packed_workspace(int64_t M, int64_t N, const plm_tile& t) {
   if (t.split_k <= 1) return 0;
   const int64_t mt = (M + 15) / 16;
-  return static_cast<int64_t>(kCounterBytes) + packed_tiles(N, t) * t.split_k * t.wave_frags * mt * kFragBytes;
+  return static_cast<int64_t>(kCounterBytes) + packed_tiles(N, t) * t.split_k * tile_fragments(t) * mt * kFragBytes;
 }
 
 constexpr int kPackedSpinLimit = 1 << 20;  // polls (each one device round trip) before a wait gives up
@@ -154,7 +164,7 @@ int64_t packed_prepare(plm_chain_gemm* g, int32_t count, int64_t M, const plm_ti
       g[i].arrive_base = static_cast<int32_t>(arrive);
       g[i].partial_offset = partial;
       arrive += tiles;
-      const int64_t floats = tiles * g[i].split_k * t.wave_frags * mt * (kFragBytes / 4);
+      const int64_t floats = tiles * g[i].split_k * tile_fragments(t) * mt * (kFragBytes / 4);
       if (floats * 4 >= (int64_t(1) << 31)) return PLM_ERR_ARGUMENT;
       partial += floats;
       most_partial = std::max(most_partial, partial);

@@ -15,13 +15,20 @@
 // X (small, L2-resident) is loaded row-major and coalesced, and turned into the operand layout
 // through a wavefront-private LDS tile.
 //
-// Work: item = a tile of NF fragments (16*NF weight rows) x one of `split` K ranges. Workgroups
-// are persistent and take items blockIdx.x, blockIdx.x + G, ... of each linear in turn. Each of
-// the 4 wavefronts owns a quarter of the item's K range and streams its weight and X fragments
-// through a D-stage register pipeline that runs across the linear's item boundaries. At an item's
-// end the four partial tiles are summed in LDS in wavefront order; with split > 1 the sum is an
-// fp32 partial and the last workgroup of the tile to arrive (device-scope counter) adds the
-// partials in split order and writes Y.
+// Work: item = a tile x one of `split` K ranges. Workgroups are persistent and take items
+// blockIdx.x, blockIdx.x + G, ... of each linear in turn. Two workgroup layouts (KW):
+//   * KW = 4: a tile is NF fragments (16*NF weight rows); each of the 4 wavefronts owns a quarter
+//     of the item's K range, and at the item's end the four partial tiles are summed in LDS in
+//     wavefront order (the verify kernel's K partition, so its logits can be reproduced).
+//   * KW = 1: a tile is 4*NF fragments; each wavefront owns NF of them over the item's whole K
+//     range, and the workgroup shares one copy of X: per K step each wavefront loads a quarter of
+//     the X fragments, writes them into a double-buffered LDS tile, and after a barrier reads all
+//     of them. Four times fewer X loads per weight byte: the vector-memory pipeline, not HBM, is
+//     what a wavefront's load rate runs into (about one KiB load per 60 ns per wavefront).
+// Each wavefront streams its weight (and X) fragments through a D-stage register pipeline that
+// runs across the linear's item boundaries. With split > 1 a tile's result is an fp32 partial and
+// the last workgroup of the tile to arrive (device-scope counter) adds the partials in split
+// order and writes Y.
 //
 // Chains: after a linear whose Y a later linear reads, every workgroup writes its part of Y
 // through to the device-coherent level and then raises its own progress flag (one 64-bit word per
@@ -43,7 +50,7 @@
 
 namespace plm {
 
-constexpr int kPackedWaves = 4;            // wavefronts per workgroup, each a quarter of the item's K range
+constexpr int kPackedWaves = 4;            // wavefronts per workgroup
 constexpr int kFragBytes = 1024;           // one packed fragment: 64 lanes x 16 bytes
 constexpr uint32_t kNoLoad = 0x80000000u;  // scalar offset that puts a load out of range (zeros)
 constexpr int kXTileBytes = 16 * 80;       // LDS transpose tile of one X fragment (rows padded to 80 B)
@@ -82,14 +89,20 @@ struct PLinear {
   const void* wp;
   void* y;
   int64_t ldx, ldy;
-  int N, Ks, k_last, split, tiles, items;
+  int N, Ks, k_last, split, tiles, items;  // tiles of 16*NF (KW = 4) or 64*NF (KW = 1) rows
   int out_f32, consumed;
   int* arrive;     // split arrival counters, one per tile
   int seq;         // consumed linears up to and including this one (progress flag value)
   float* partial;  // split partials
 };
 
-template <int NF>
+// Weight fragments of a tile.
+template <int NF, int KW>
+constexpr int tile_frags() {
+  return KW == 4 ? NF : 4 * NF;
+}
+
+template <int NF, int KW>
 __device__ __forceinline__ PLinear load_linear(const PackedArgs& a, int gi) {
   const plm_chain_gemm* src = a.chain != nullptr ? a.chain + gi : &a.single;
   PLinear L;
@@ -103,7 +116,7 @@ __device__ __forceinline__ PLinear load_linear(const PackedArgs& a, int gi) {
   L.Ks = (K + 31) >> 5;
   L.k_last = K - 32 * (L.Ks - 1);
   L.split = sgpr(src->split_k);
-  L.tiles = (((L.N + 15) >> 4) + NF - 1) / NF;
+  L.tiles = (((L.N + 15) >> 4) + tile_frags<NF, KW>() - 1) / tile_frags<NF, KW>();
   L.items = L.tiles * L.split;
   L.out_f32 = sgpr(src->out_f32);
   L.consumed = sgpr(src->consumed);
@@ -113,13 +126,19 @@ __device__ __forceinline__ PLinear load_linear(const PackedArgs& a, int gi) {
   return L;
 }
 
-// K-step range [b, e) of wavefront w's quarter of split s.
+// K-step range [b, e) of split s: wavefront w's quarter of it (KW = 4) or all of it (KW = 1).
+template <int KW>
 __device__ __forceinline__ void packed_range(int Ks, int s, int split, int w, int& b, int& e) {
   const int lo = static_cast<int>(static_cast<int64_t>(s) * Ks / split);
   const int hi = static_cast<int>(static_cast<int64_t>(s + 1) * Ks / split);
-  const int n = hi - lo;
-  b = lo + n * w / kPackedWaves;
-  e = lo + n * (w + 1) / kPackedWaves;
+  if constexpr (KW == 1) {
+    b = lo;
+    e = hi;
+  } else {
+    const int n = hi - lo;
+    b = lo + n * w / kPackedWaves;
+    e = lo + n * (w + 1) / kPackedWaves;
+  }
 }
 
 // A wavefront's position in its stream of (item, K step). A wavefront's steps of an item are
@@ -134,46 +153,55 @@ struct PCursor {
   int wbase;  // byte offset of the item's first weight fragment at step 0
 };
 
-template <int NF, int D>
+template <int NF, int D, int KW>
 __device__ __forceinline__ void pc_enter(const PLinear& L, int wave, PCursor& c) {
   if (c.item >= L.items) return;
   const int tile = c.item / L.split;
   const int s = c.item - tile * L.split;
   int b, e;
-  packed_range(L.Ks, s, L.split, wave, b, e);
+  packed_range<KW>(L.Ks, s, L.split, wave, b, e);
   c.st = b;
   c.end = e;
   c.pend = b + max(D, (e - b + D - 1) / D * D);
-  c.wbase = tile * NF * L.Ks * kFragBytes;
+  c.wbase = (tile * tile_frags<NF, KW>() + (KW == 1 ? wave * NF : 0)) * L.Ks * kFragBytes;
 }
 
-template <int NF, int D>
+template <int NF, int D, int KW>
 __device__ __forceinline__ void pc_advance(const PLinear& L, int G, int wave, PCursor& c) {
   if (++c.st == c.pend) {
     c.item += G;
-    pc_enter<NF, D>(L, wave, c);
+    pc_enter<NF, D, KW>(L, wave, c);
   }
 }
 
 __device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// X fragments a wavefront loads per K step: all MT (KW = 4), or fragments wave, wave + 4, ...
+// (KW = 1: the workgroup's four wavefronts load one copy between them).
+template <int MT, int KW>
+constexpr int x_per_wave() {
+  return KW == 4 ? MT : (MT + 3) / 4;
+}
+
 // Per-lane operand offsets of one linear.
-template <int MT, int NF>
+template <int MT, int NF, int XN>
 struct POffsets {
   uint32_t wo[NF];       // weight fragment f at step 0 (plus the item's wbase, the step's KiB)
-  uint32_t xo[MT];       // coalesced X: row 16t + lane/4, bytes 16*(lane%4) of the step's 64
-  uint32_t xo_last[MT];  // the same with lanes past K (last step) out of range
+  uint32_t xo[XN];       // coalesced X: row 16t + lane/4, bytes 16*(lane%4) of the step's 64
+  uint32_t xo_last[XN];  // the same with lanes past K (last step) out of range
 };
 
-template <int MT, int NF>
-__device__ __forceinline__ void packed_offsets(const PLinear& L, int M, int lane, POffsets<MT, NF>& o) {
+template <int MT, int NF, int KW>
+__device__ __forceinline__ void packed_offsets(const PLinear& L, int M, int lane, int wave,
+                                               POffsets<MT, NF, x_per_wave<MT, KW>()>& o) {
 #pragma unroll
   for (int f = 0; f < NF; ++f) o.wo[f] = static_cast<uint32_t>(f * L.Ks * kFragBytes + lane * 16);
 #pragma unroll
-  for (int t = 0; t < MT; ++t) {
+  for (int i = 0; i < x_per_wave<MT, KW>(); ++i) {
+    const int t = KW == 4 ? i : wave + 4 * i;
     const int m = 16 * t + (lane >> 2);
-    o.xo[t] = m < M ? static_cast<uint32_t>(m * L.ldx * 2 + (lane & 3) * 16) : kOutOfRange;
-    o.xo_last[t] = 8 * (lane & 3) < L.k_last ? o.xo[t] : kOutOfRange;
+    o.xo[i] = (t < MT && m < M) ? static_cast<uint32_t>(m * L.ldx * 2 + (lane & 3) * 16) : kOutOfRange;
+    o.xo_last[i] = 8 * (lane & 3) < L.k_last ? o.xo[i] : kOutOfRange;
   }
 }
 
@@ -190,14 +218,14 @@ __device__ __forceinline__ void issue_w(__amdgpu_buffer_rsrc_t wr, const PCursor
 
 // Loads the X half of one pipeline stage. X lanes past K in the last step load zeros (the packed
 // weights are zero there, but X past K is another row's data or padding, and 0 * NaN is NaN).
-template <int MT, int NF>
+template <int MT, int NF, int XN>
 __device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t xr, const PCursor& c, int items, int Ks,
-                                        const POffsets<MT, NF>& o, u32x4 (&xb)[MT]) {
+                                        const POffsets<MT, NF, XN>& o, u32x4 (&xb)[XN]) {
   const bool live = c.item < items && c.st < c.end;
   const uint32_t xs = live ? static_cast<uint32_t>(c.st * 64) : kNoLoad;
   const bool last = c.st == Ks - 1;
 #pragma unroll
-  for (int t = 0; t < MT; ++t)
+  for (int t = 0; t < XN; ++t)
     xb[t] = __builtin_bit_cast(
         u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, last ? o.xo_last[t] : o.xo[t], static_cast<int>(xs), 0));
 }
@@ -324,6 +352,67 @@ __device__ __forceinline__ void packed_finish(const PLinear& L, int M, int item,
   }
 }
 
+// End of an item for a row-split workgroup (KW = 1): each wavefront owns its NF fragments of the
+// tile outright and writes them (Y, or with split > 1 its fp32 partials; the last split of the
+// tile to arrive sums each wavefront's partials in split order and writes Y).
+template <int DT, int MT, int NF>
+__device__ __forceinline__ void packed_finish_rows(const PLinear& L, int M, int item, int wave, int lane,
+                                                   f32x4 (&acc)[NF][MT], int* last_flag) {
+  constexpr int QW = NF * MT;               // fragments of one wavefront
+  constexpr int Q = kPackedWaves * QW;      // fragments of the tile
+  const int tile = item / L.split;
+  const int s = item - tile * L.split;
+  const int n0 = (tile * 4 + wave) * NF * 16;
+  if (L.split == 1) {
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) packed_store_frag<DT, MT>(L, M, n0, f * MT + t, lane, acc[f][t]);
+    return;
+  }
+  const uint32_t tile_bytes = static_cast<uint32_t>(L.split) * Q * kFragBytes;
+  const auto prs = make_rsrc(L.partial + static_cast<int64_t>(tile) * L.split * Q * 256, tile_bytes);
+#pragma unroll
+  for (int f = 0; f < NF; ++f)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int q = wave * QW + f * MT + t;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[f][t]), prs,
+                                             static_cast<uint32_t>((s * Q + q) * kFragBytes + lane * 16), 0, kCoherent);
+    }
+  __builtin_amdgcn_s_waitcnt(0);  // this wavefront's partial is written through
+  lds_sync();
+  if (threadIdx.x == 0) {
+    int* counter = L.arrive + tile;
+    const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = before == L.split - 1;
+    if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *last_flag = last;
+  }
+  lds_sync();
+  if (*last_flag == 0) return;
+  // A rolled loop over the wavefront's fragments: unrolled, the compiler would keep every
+  // fragment's partial loads in flight at once and run out of registers.
+#pragma unroll 1
+  for (int qw = 0; qw < QW; ++qw) {
+    const int q = wave * QW + qw;
+    f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < L.split; s0 += 8) {
+      u32x4 part[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        part[j] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       prs, s0 + j < L.split ? static_cast<uint32_t>(((s0 + j) * Q + q) * kFragBytes + lane * 16) : kOutOfRange,
+                       0, kCoherent));
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (s0 + j < L.split) v += __builtin_bit_cast(f32x4, part[j]);
+    }
+    packed_store_frag<DT, MT>(L, M, n0, qw, lane, v);
+  }
+}
+
 extern __shared__ __attribute__((aligned(16))) f32x4 packed_lds[];
 
 // Grid barrier after the consumed linear with sequence number `seq`, in two halves so that the
@@ -371,7 +460,7 @@ typedef __attribute__((address_space(3))) void PkLdsVoid;
 // the pipeline then finds them in L2 / the Infinity Cache.
 constexpr int kWarmFragments = 32;
 
-template <int NF, int D>
+template <int NF, int D, int KW>
 __device__ __forceinline__ void warm_weights(const PLinear& Ln, int G, int wave, int lane, PCursor nx,
                                              __amdgpu_buffer_rsrc_t wr, const uint32_t* wo, PkLdsVoid* dst) {
   for (int n = 0; n < kWarmFragments / NF && nx.item < Ln.items; ++n) {
@@ -381,7 +470,7 @@ __device__ __forceinline__ void warm_weights(const PLinear& Ln, int G, int wave,
       for (int f = 0; f < NF; ++f)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, dst, 16, wo[f], static_cast<int>(ws), 0, 0);
     }
-    pc_advance<NF, D>(Ln, G, wave, nx);
+    pc_advance<NF, D, KW>(Ln, G, wave, nx);
   }
   (void)lane;
 }
@@ -396,61 +485,67 @@ __global__ void packed_epoch_kernel(int* counters) {
   }
 }
 
-// Registers per lane of the operand pipeline and the accumulators. Configurations that fit in
-// about half of the 256 VGPRs with everything else (measured: no scratch) run two workgroups per
-// CU; larger ones run one, with the AGPR half of the register file available.
-template <int MT, int NF, int D>
+// Registers per lane of the operand pipeline and the accumulators (with KW = 1 also the MT X
+// operands read back from the shared tile, which cannot reuse the pipeline's X registers).
+// Configurations below a measured bound (the largest without scratch at 256 VGPRs) run two
+// workgroups per CU; larger ones run one, with the AGPR half of the register file available.
+template <int MT, int NF, int D, int KW>
 constexpr int packed_regs() {
-  return (D * (NF + MT) + NF * MT) * 4;
+  return (D * (NF + x_per_wave<MT, KW>()) + NF * MT + (KW == 1 ? MT : 0)) * 4;
 }
-template <int MT, int NF, int D>
+template <int MT, int NF, int D, int KW>
 constexpr bool packed_two_per_cu() {
-  return packed_regs<MT, NF, D>() <= 128 && (MT <= 6 || packed_regs<MT, NF, D>() <= 104);
+  if constexpr (KW == 1) return packed_regs<MT, NF, D, KW>() <= 100;
+  return packed_regs<MT, NF, D, KW>() <= 128 && (MT <= 6 || packed_regs<MT, NF, D, KW>() <= 104);
 }
-template <int MT, int NF, int D>
+template <int MT, int NF, int D, int KW>
 constexpr int packed_min_blocks() {
-  return packed_two_per_cu<MT, NF, D>() ? 2 : 1;
+  return packed_two_per_cu<MT, NF, D, KW>() ? 2 : 1;
 }
 
-template <int DT, int MT, int NF, int D>
-__global__ __launch_bounds__(64 * kPackedWaves, (packed_min_blocks<MT, NF, D>())) void packed_gemm_kernel(PackedArgs a) {
+template <int DT, int MT, int NF, int D, int KW>
+__global__ __launch_bounds__(64 * kPackedWaves, (packed_min_blocks<MT, NF, D, KW>())) void packed_gemm_kernel(PackedArgs a) {
+  constexpr int XN = x_per_wave<MT, KW>();
   __shared__ int last_flag;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // LDS: KW = 4: the four wavefronts' fp32 tiles (reduction), then a private X transpose tile set
+  // per wavefront; KW = 1: two shared X tile sets (double-buffered by K step).
   f32x4* red = packed_lds;
-  char* xt = reinterpret_cast<char*>(packed_lds) + static_cast<size_t>(kPackedWaves) * NF * MT * kFragBytes +
-             static_cast<size_t>(wave) * MT * kXTileBytes;
+  char* xt = KW == 4 ? reinterpret_cast<char*>(packed_lds) + static_cast<size_t>(kPackedWaves) * NF * MT * kFragBytes +
+                           static_cast<size_t>(wave) * MT * kXTileBytes
+                     : reinterpret_cast<char*>(packed_lds);
   const int xt_write = (lane >> 2) * 80 + (lane & 3) * 16;
   const int xt_read = (lane & 15) * 80 + (lane >> 4) * 16;
   const int64_t epoch = a.sync ? sgpr64(collect(reinterpret_cast<const int64_t*>(a.counters + kPkEpochSlot))) : 0;
 
-  u32x4 wb[D][NF], xb[D][MT];
+  u32x4 wb[D][NF], xb[D][XN];
   // The first weight stages of linear `gi` may already be in flight (requested before the last
   // grid barrier): then only X is still to be loaded for them.
   bool w_ready = false;
   for (int gi = 0; gi < a.count; ++gi) {
-    const PLinear L = load_linear<NF>(a, gi);
-    POffsets<MT, NF> o;
-    packed_offsets<MT, NF>(L, a.M, lane, o);
+    const PLinear L = load_linear<NF, KW>(a, gi);
+    POffsets<MT, NF, XN> o;
+    packed_offsets<MT, NF, KW>(L, a.M, lane, wave, o);
     const auto wr = make_rsrc(L.wp, static_cast<uint32_t>((L.N + 15) >> 4) * L.Ks * kFragBytes);
     const auto xr = make_rsrc(L.x, static_cast<uint32_t>(a.M * L.ldx * 2));
     PCursor ld{static_cast<int>(blockIdx.x), 0, 0, 0, 0};
-    pc_enter<NF, D>(L, wave, ld);
+    pc_enter<NF, D, KW>(L, wave, ld);
     PCursor cp = ld;
     if (ld.item < L.items) {
       if (!w_ready) {
 #pragma unroll
         for (int j = 0; j < D; ++j) {
           issue_w<NF>(wr, ld, L.items, o.wo, wb[j]);
-          issue_x<MT, NF>(xr, ld, L.items, L.Ks, o, xb[j]);
-          pc_advance<NF, D>(L, a.G, wave, ld);
+          issue_x<MT, NF, XN>(xr, ld, L.items, L.Ks, o, xb[j]);
+          pc_advance<NF, D, KW>(L, a.G, wave, ld);
           __builtin_amdgcn_sched_barrier(0);
         }
       } else {
 #pragma unroll
         for (int j = 0; j < D; ++j) {
-          issue_x<MT, NF>(xr, ld, L.items, L.Ks, o, xb[j]);
-          pc_advance<NF, D>(L, a.G, wave, ld);
+          issue_x<MT, NF, XN>(xr, ld, L.items, L.Ks, o, xb[j]);
+          pc_advance<NF, D, KW>(L, a.G, wave, ld);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
@@ -465,24 +560,39 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_min_blocks<MT, NF, D>())
 #pragma unroll
           for (int j = 0; j < D; ++j) {
             u32x4 xop[MT];
+            if constexpr (KW == 4) {
 #pragma unroll
-            for (int t = 0; t < MT; ++t) *reinterpret_cast<u32x4*>(xt + t * kXTileBytes + xt_write) = xb[j][t];
+              for (int t = 0; t < MT; ++t) *reinterpret_cast<u32x4*>(xt + t * kXTileBytes + xt_write) = xb[j][t];
 #pragma unroll
-            for (int t = 0; t < MT; ++t) xop[t] = *reinterpret_cast<const u32x4*>(xt + t * kXTileBytes + xt_read);
+              for (int t = 0; t < MT; ++t) xop[t] = *reinterpret_cast<const u32x4*>(xt + t * kXTileBytes + xt_read);
+            } else {
+              // Stage j's X tile set (j alternates parity: D is even and items pad to a multiple).
+              char* xs = xt + (j & 1) * MT * kXTileBytes;
+#pragma unroll
+              for (int i = 0; i < XN; ++i)
+                if (wave + 4 * i < MT)
+                  *reinterpret_cast<u32x4*>(xs + (wave + 4 * i) * kXTileBytes + xt_write) = xb[j][i];
+              lds_sync();
+#pragma unroll
+              for (int t = 0; t < MT; ++t) xop[t] = *reinterpret_cast<const u32x4*>(xs + t * kXTileBytes + xt_read);
+            }
 #pragma unroll
             for (int f = 0; f < NF; ++f)
 #pragma unroll
               for (int t = 0; t < MT; ++t) acc[f][t] = mfma_16x16x32<DT>(wb[j][f], xop[t], acc[f][t]);
             issue_w<NF>(wr, ld, L.items, o.wo, wb[j]);
-            issue_x<MT, NF>(xr, ld, L.items, L.Ks, o, xb[j]);
-            pc_advance<NF, D>(L, a.G, wave, ld);
+            issue_x<MT, NF, XN>(xr, ld, L.items, L.Ks, o, xb[j]);
+            pc_advance<NF, D, KW>(L, a.G, wave, ld);
             __builtin_amdgcn_sched_barrier(0);
           }
         }
-        packed_finish<DT, MT, NF>(L, a.M, cp.item, wave, lane, acc, red, &last_flag);
+        if constexpr (KW == 4)
+          packed_finish<DT, MT, NF>(L, a.M, cp.item, wave, lane, acc, red, &last_flag);
+        else
+          packed_finish_rows<DT, MT, NF>(L, a.M, cp.item, wave, lane, acc, &last_flag);
         cp.item += a.G;
         if (cp.item >= L.items) break;
-        pc_enter<NF, D>(L, wave, cp);
+        pc_enter<NF, D, KW>(L, wave, cp);
       }
     }
     w_ready = false;
@@ -492,21 +602,21 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_min_blocks<MT, NF, D>())
       // workgroup's part of this Y.
       __builtin_amdgcn_s_waitcnt(0);
       barrier_arrive(a, epoch, L.seq);
-      const PLinear Ln = load_linear<NF>(a, gi + 1);
+      const PLinear Ln = load_linear<NF, KW>(a, gi + 1);
       PCursor nx{static_cast<int>(blockIdx.x), 0, 0, 0, 0};
-      pc_enter<NF, D>(Ln, wave, nx);
+      pc_enter<NF, D, KW>(Ln, wave, nx);
       if (nx.item < Ln.items) {
-        POffsets<MT, NF> on;
-        packed_offsets<MT, NF>(Ln, a.M, lane, on);
+        POffsets<MT, NF, XN> on;
+        packed_offsets<MT, NF, KW>(Ln, a.M, lane, wave, on);
         const auto wrn = make_rsrc(Ln.wp, static_cast<uint32_t>((Ln.N + 15) >> 4) * Ln.Ks * kFragBytes);
 #pragma unroll
         for (int j = 0; j < D; ++j) {
           issue_w<NF>(wrn, nx, Ln.items, on.wo, wb[j]);
-          pc_advance<NF, D>(Ln, a.G, wave, nx);
+          pc_advance<NF, D, KW>(Ln, a.G, wave, nx);
           __builtin_amdgcn_sched_barrier(0);
         }
         w_ready = true;
-        warm_weights<NF, D>(Ln, a.G, wave, lane, nx, wrn, on.wo, (PkLdsVoid*)red);
+        warm_weights<NF, D, KW>(Ln, a.G, wave, lane, nx, wrn, on.wo, (PkLdsVoid*)red);
       }
       barrier_wait(a, epoch, L.seq, lane);
     }
@@ -517,29 +627,30 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_min_blocks<MT, NF, D>())
 // Compiled configurations (all without scratch): 1 <= MT <= 8, NF in {1, 2, 4}, D in
 // {2, 4, 6, 8}, at most 20 accumulator fragments, and either two workgroups per CU or, for
 // MT <= 4, one workgroup per CU with the pipeline's registers within 320 of a lane's 512.
-template <int MT, int NF, int D>
+template <int MT, int NF, int D, int KW>
 constexpr bool packed_compiled() {
   if (MT < 1 || MT > 8 || (NF != 1 && NF != 2 && NF != 4) || (D != 2 && D != 4 && D != 6 && D != 8)) return false;
-  if (NF * MT > 20) return false;
-  return packed_two_per_cu<MT, NF, D>() || (MT <= 4 && packed_regs<MT, NF, D>() <= 320);
+  if ((KW != 1 && KW != 4) || NF * MT > 20) return false;
+  return packed_two_per_cu<MT, NF, D, KW>() || (MT <= 4 && packed_regs<MT, NF, D, KW>() <= 320);
 }
 
-template <int MT, int NF>
+template <int MT, int NF, int KW>
 constexpr size_t packed_lds_bytes() {
-  return static_cast<size_t>(kPackedWaves) * (NF * MT * kFragBytes + MT * kXTileBytes);
+  return KW == 4 ? static_cast<size_t>(kPackedWaves) * (NF * MT * kFragBytes + MT * kXTileBytes)
+                 : static_cast<size_t>(2) * MT * kXTileBytes;
 }
 
 // Launches with G = min(a.G, resident workgroups), where a.G arrives as the most items of any
 // linear; a chained launch with grid barriers (a.sync) uses every resident workgroup. `dry` only
 // checks that the kernel exists.
-template <int DT, int MT, int NF, int D>
+template <int DT, int MT, int NF, int D, int KW>
 hipError_t packed_launch(PackedArgs& a, int cus, hipStream_t stream, bool dry) {
-  if constexpr (!packed_compiled<MT, NF, D>()) {
+  if constexpr (!packed_compiled<MT, NF, D, KW>()) {
     return hipErrorInvalidConfiguration;
   } else {
     if (dry) return hipSuccess;
-    auto kern = packed_gemm_kernel<DT, MT, NF, D>;
-    constexpr size_t lds = packed_lds_bytes<MT, NF>();
+    auto kern = packed_gemm_kernel<DT, MT, NF, D, KW>;
+    constexpr size_t lds = packed_lds_bytes<MT, NF, KW>();
     static int per_cu = 0;
     if (per_cu == 0) {
       if (lds > 64 * 1024) {
@@ -567,39 +678,42 @@ hipError_t packed_launch(PackedArgs& a, int cus, hipStream_t stream, bool dry) {
   }
 }
 
-template <int DT, int MT, int NF>
+template <int DT, int MT, int NF, int KW>
 hipError_t packed_pick_d(PackedArgs& a, int d, int cus, hipStream_t s, bool dry) {
-  if (d == 2) return packed_launch<DT, MT, NF, 2>(a, cus, s, dry);
-  if (d == 4) return packed_launch<DT, MT, NF, 4>(a, cus, s, dry);
-  if (d == 6) return packed_launch<DT, MT, NF, 6>(a, cus, s, dry);
-  if (d == 8) return packed_launch<DT, MT, NF, 8>(a, cus, s, dry);
+  if (d == 2) return packed_launch<DT, MT, NF, 2, KW>(a, cus, s, dry);
+  if (d == 4) return packed_launch<DT, MT, NF, 4, KW>(a, cus, s, dry);
+  if (d == 6) return packed_launch<DT, MT, NF, 6, KW>(a, cus, s, dry);
+  if (d == 8) return packed_launch<DT, MT, NF, 8, KW>(a, cus, s, dry);
   return hipErrorInvalidConfiguration;
 }
 
-template <int DT, int MT>
+template <int DT, int MT, int KW>
 hipError_t packed_pick(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry) {
-  if (nf == 1) return packed_pick_d<DT, MT, 1>(a, d, cus, s, dry);
-  if (nf == 2) return packed_pick_d<DT, MT, 2>(a, d, cus, s, dry);
-  if (nf == 4) return packed_pick_d<DT, MT, 4>(a, d, cus, s, dry);
+  if (nf == 1) return packed_pick_d<DT, MT, 1, KW>(a, d, cus, s, dry);
+  if (nf == 2) return packed_pick_d<DT, MT, 2, KW>(a, d, cus, s, dry);
+  if (nf == 4) return packed_pick_d<DT, MT, 4, KW>(a, d, cus, s, dry);
   return hipErrorInvalidConfiguration;
 }
 
-template <int DT>
-hipError_t packed_dispatch(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry) {
+template <int DT, int KW>
+hipError_t packed_dispatch_kw(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry) {
   switch ((a.M + 15) / 16) {
-    case 1: return packed_pick<DT, 1>(a, nf, d, cus, s, dry);
-    case 2: return packed_pick<DT, 2>(a, nf, d, cus, s, dry);
-    case 3: return packed_pick<DT, 3>(a, nf, d, cus, s, dry);
-    case 4: return packed_pick<DT, 4>(a, nf, d, cus, s, dry);
-    case 5: return packed_pick<DT, 5>(a, nf, d, cus, s, dry);
-    case 6: return packed_pick<DT, 6>(a, nf, d, cus, s, dry);
-    case 7: return packed_pick<DT, 7>(a, nf, d, cus, s, dry);
-    case 8: return packed_pick<DT, 8>(a, nf, d, cus, s, dry);
+    case 1: return packed_pick<DT, 1, KW>(a, nf, d, cus, s, dry);
+    case 2: return packed_pick<DT, 2, KW>(a, nf, d, cus, s, dry);
+    case 3: return packed_pick<DT, 3, KW>(a, nf, d, cus, s, dry);
+    case 4: return packed_pick<DT, 4, KW>(a, nf, d, cus, s, dry);
+    case 5: return packed_pick<DT, 5, KW>(a, nf, d, cus, s, dry);
+    case 6: return packed_pick<DT, 6, KW>(a, nf, d, cus, s, dry);
+    case 7: return packed_pick<DT, 7, KW>(a, nf, d, cus, s, dry);
+    case 8: return packed_pick<DT, 8, KW>(a, nf, d, cus, s, dry);
   }
   return hipErrorInvalidConfiguration;
 }
 
-hipError_t packed_dispatch_bf16(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
-hipError_t packed_dispatch_f16(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+// One translation unit per (dtype, workgroup layout) so that they build in parallel.
+hipError_t packed_dispatch_bf16_k4(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_bf16_k1(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_f16_k4(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_f16_k1(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
 
 }  // namespace plm

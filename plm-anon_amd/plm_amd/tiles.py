@@ -1,11 +1,13 @@
 """Tile selection for shapes without a tuned table entry, and the candidate set the tuner sweeps.
 
 A tile is ``{"wave_frags", "k_waves", "split_k", "unroll"}`` (``struct plm_tile`` in
-``include/plm_amd.h``). For the packed-weight GEMM behind ``fast_gemm`` (plm_gemm_packed): a
-workgroup tile is ``16*wave_frags`` weight rows; its ``k_waves`` (= 4) wavefronts split the tile's
-K range and are summed in LDS; ``split_k`` workgroups split K further (fp32 partials summed in
-split order); ``unroll`` (2, 4 or 6) K steps of loads are in flight per wavefront. Items
-(tile x split) = ``ceil(ceil(N/16) / wave_frags) * split_k`` over a persistent grid.
+``include/plm_amd.h``). For the packed-weight GEMM behind ``fast_gemm`` (plm_gemm_packed), each
+of a workgroup's four wavefronts streams ``16*wave_frags`` weight rows, and either
+``k_waves`` = 4: the four split the K range of one ``16*wave_frags``-row tile (summed in LDS), or
+``k_waves`` = 1: the four take adjacent rows of a ``64*wave_frags``-row tile over the whole K range
+and share one copy of X through LDS. ``split_k`` workgroups split K further (fp32 partials summed
+in split order); ``unroll`` (2, 4, 6 or 8) K steps of loads are in flight per wavefront. Items
+(tile x split) = ``ceil(ceil(N/16) / tile_frags) * split_k`` over a persistent grid.
 
 The chained round (plm_gemm_chain) uses the streaming kernel's tiles: ``64*wave_frags`` rows,
 ``unroll`` = 2 (``chain_tile``, ``chain_split`` below).
@@ -16,20 +18,24 @@ from __future__ import annotations
 import math
 
 CU_COUNT = 256          # MI355X compute units
-K_WAVES = 4
+K_WAVES = 4             # wavefronts per workgroup
+LAYOUTS = (4, 1)        # k_waves: K split across the wavefronts, or rows split across them
 WAVE_FRAGS = (1, 2, 4)
 DEPTHS = (2, 4, 6, 8)
 SPLITS = (1, 2, 3, 4, 6, 8, 12, 16)
 
 
-def _regs(mt: int, nf: int, d: int) -> int:
-    return (d * (nf + mt) + nf * mt) * 4
+def _regs(mt: int, nf: int, d: int, kw: int) -> int:
+    xn = mt if kw == K_WAVES else (mt + 3) // 4
+    return (d * (nf + xn) + nf * mt + (mt if kw == 1 else 0)) * 4
 
 
 def two_per_cu(M: int, cfg: dict) -> bool:
     """Whether two workgroups of this tile share a CU (mirrors ``packed_two_per_cu``)."""
-    mt, nf, d = math.ceil(M / 16), cfg["wave_frags"], cfg["unroll"]
-    r = _regs(mt, nf, d)
+    mt, nf, d, kw = math.ceil(M / 16), cfg["wave_frags"], cfg["unroll"], cfg["k_waves"]
+    r = _regs(mt, nf, d, kw)
+    if kw == 1:
+        return r <= 100
     return r <= 128 and (mt <= 6 or r <= 104)
 
 
@@ -37,46 +43,55 @@ def compiled(M: int, cfg: dict) -> bool:
     """Whether the library has a packed-GEMM kernel for this tile at width M (mirrors
     ``packed_compiled`` in csrc/packed_gemm.h: at most 20 accumulator fragments, and two
     workgroups per CU, or one with the pipeline within 320 registers for M <= 64)."""
-    mt, nf, d = math.ceil(M / 16), cfg["wave_frags"], cfg["unroll"]
-    if not (1 <= mt <= 8 and nf in WAVE_FRAGS and d in DEPTHS and cfg["k_waves"] == K_WAVES):
+    mt, nf, d, kw = math.ceil(M / 16), cfg["wave_frags"], cfg["unroll"], cfg["k_waves"]
+    if not (1 <= mt <= 8 and nf in WAVE_FRAGS and d in DEPTHS and kw in LAYOUTS):
         return False
-    return nf * mt <= 20 and (two_per_cu(M, cfg) or (mt <= 4 and _regs(mt, nf, d) <= 320))
+    return nf * mt <= 20 and (two_per_cu(M, cfg) or (mt <= 4 and _regs(mt, nf, d, kw) <= 320))
+
+
+def tile_frags(cfg: dict) -> int:
+    """16-row weight fragments of one workgroup tile."""
+    return cfg["wave_frags"] * (K_WAVES if cfg["k_waves"] == 1 else 1)
 
 
 def items(N: int, cfg: dict) -> int:
-    return math.ceil(math.ceil(N / 16) / cfg["wave_frags"]) * cfg["split_k"]
+    return math.ceil(math.ceil(N / 16) / tile_frags(cfg)) * cfg["split_k"]
 
 
 def steps_per_wave(K: int, cfg: dict) -> int:
-    """32-wide K steps each wavefront streams per item (the shortest quarter)."""
-    return math.ceil(K / 32) // cfg["split_k"] // K_WAVES
+    """32-wide K steps each wavefront streams per item (k_waves = 4: the shortest quarter)."""
+    return math.ceil(K / 32) // cfg["split_k"] // (K_WAVES if cfg["k_waves"] == K_WAVES else 1)
 
 
 def candidates(M: int, N: int, K: int, supported=None) -> list[dict]:
     """Every sensible tile for ``(M, N, K)``; ``supported(cfg) -> bool`` filters to compiled kernels."""
     out = []
-    for nf in WAVE_FRAGS:
-        for d in DEPTHS:
-            for split in SPLITS:
-                cfg = {"wave_frags": nf, "k_waves": K_WAVES, "split_k": split, "unroll": d}
-                if not compiled(M, cfg) or items(N, cfg) > 64 * CU_COUNT:
-                    continue
-                if split > 1 and (steps_per_wave(K, cfg) < 2 or
-                                  items(N, dict(cfg, split_k=max(1, split // 2))) >= 4 * CU_COUNT):
-                    continue  # too little K per wavefront, or plenty of items with half the splitting
-                if supported is not None and not supported(cfg):
-                    continue
-                out.append(cfg)
+    for kw in LAYOUTS:
+        for nf in WAVE_FRAGS:
+            for d in DEPTHS:
+                for split in SPLITS:
+                    cfg = {"wave_frags": nf, "k_waves": kw, "split_k": split, "unroll": d}
+                    if not compiled(M, cfg) or items(N, cfg) > 64 * CU_COUNT:
+                        continue
+                    if split > 1 and (steps_per_wave(K, cfg) < 2 or
+                                      items(N, dict(cfg, split_k=max(1, split // 2))) >= 4 * CU_COUNT):
+                        continue  # too little K per wavefront, or plenty of items with half the splitting
+                    if supported is not None and not supported(cfg):
+                        continue
+                    out.append(cfg)
     return out
 
 
 def heuristic_tile(M: int, N: int, K: int, supported=None) -> dict:
     """A reasonable tile without measurement (what the MI355X measurements of the round shapes
-    favour): 32-row tiles with a two-stage pipeline, and K splitting until about three quarters
-    of the compute units have an item, keeping at least two K steps per wavefront."""
+    favour): 32 rows per wavefront with a two-stage pipeline; rows split across the wavefronts
+    (128-row tiles) when that alone gives every compute unit a tile (the LM head: one round of
+    tiles instead of three and a fraction), else K split across them, and K splitting until about
+    three quarters of the compute units have an item, keeping at least two K steps per wavefront."""
     for nf in (2, 4, 1):
+        kw = 1 if math.ceil(N / 16) // (K_WAVES * nf) >= CU_COUNT else K_WAVES
         for d in (2, 4, 6, 8):
-            cfg = {"wave_frags": nf, "k_waves": K_WAVES, "split_k": 1, "unroll": d}
+            cfg = {"wave_frags": nf, "k_waves": kw, "split_k": 1, "unroll": d}
             if not compiled(M, cfg) or (supported is not None and not supported(cfg)):
                 continue
             split = 1
@@ -92,14 +107,15 @@ def packed_chain_split(N: int, K: int, cfg: dict, workgroups: int) -> int:
     is that of the busiest workgroup): the split with the least estimated busiest-workgroup time,
     counting each item's K steps per wavefront plus a fixed cost of a few steps for the item's end
     (reduction, stores; with split > 1 the partial round trip)."""
-    tiles_ = math.ceil(math.ceil(N / 16) / cfg["wave_frags"])
+    tiles_ = math.ceil(math.ceil(N / 16) / tile_frags(cfg))
     ks = math.ceil(K / 32)
+    kw = K_WAVES if cfg["k_waves"] == K_WAVES else 1
     best, best_cost = 1, None
     for split in SPLITS:
-        if split > 1 and ks // split // K_WAVES < 2:
+        if split > 1 and ks // split // kw < 2:
             break
         per_wg = math.ceil(tiles_ * split / workgroups)
-        steps = max(cfg["unroll"], math.ceil(ks / split / K_WAVES))
+        steps = max(cfg["unroll"], math.ceil(ks / split / kw))
         cost = per_wg * (steps + (3 if split == 1 else 8))
         if best_cost is None or cost < best_cost:
             best, best_cost = split, cost

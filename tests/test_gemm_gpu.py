@@ -132,7 +132,9 @@ def test_round_widths_edge_cases(device, M):
     x, w = _inputs(M, N, K, 5)
     supported = lambda c: fast_gemm.tile_supported(M, K, c)  # noqa: E731
     for cfg in (tiles.heuristic_tile(M, N, K, supported=supported),
-                {"wave_frags": 1, "k_waves": 4, "split_k": 3, "unroll": 2}):
+                {"wave_frags": 1, "k_waves": 4, "split_k": 3, "unroll": 2},
+                {"wave_frags": 1, "k_waves": 1, "split_k": 1, "unroll": 2},
+                {"wave_frags": 2, "k_waves": 1, "split_k": 3, "unroll": 4}):
         if supported(cfg):
             check(_run(x, w, cfg, device), x, w)
 
@@ -170,7 +172,8 @@ def test_fp16(device):
     M, N, K = 56, 3072, 2048
     x, w = _inputs(M, N, K, 7, torch.float16)
     for cfg in ({"wave_frags": 2, "k_waves": 4, "split_k": 2, "unroll": 2},
-                {"wave_frags": 1, "k_waves": 4, "split_k": 1, "unroll": 2}):
+                {"wave_frags": 1, "k_waves": 4, "split_k": 1, "unroll": 2},
+                {"wave_frags": 2, "k_waves": 1, "split_k": 2, "unroll": 2}):
         check(_run(x, w, cfg, device), x, w)
 
 
@@ -182,7 +185,9 @@ def test_small_integers_are_exact(device):
     exact = oracle.linear_fp64(x, w)
     assert abs(exact).max() < 256
     for cfg in ({"wave_frags": 2, "k_waves": 4, "split_k": 1, "unroll": 2},
-                {"wave_frags": 1, "k_waves": 4, "split_k": 4, "unroll": 2}):
+                {"wave_frags": 1, "k_waves": 4, "split_k": 4, "unroll": 2},
+                {"wave_frags": 1, "k_waves": 1, "split_k": 1, "unroll": 8},
+                {"wave_frags": 2, "k_waves": 1, "split_k": 4, "unroll": 2}):
         y = _run(x, w, cfg, device).cpu().double().numpy()
         assert (y == exact).all()
 
