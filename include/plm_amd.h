@@ -88,7 +88,8 @@ int plm_pack_weight(int32_t dtype, const void* w, int64_t ldw, int64_t N, int64_
  * workgroup tile is 64*wave_frags rows, each wavefront owns 16*wave_frags of them over the whole
  * K range, and the four share one copy of X through LDS; split_k = workgroups splitting K (1..64,
  * partials summed in split order); unroll = K steps of loads in flight per wavefront (2, 4, 6,
- * 8). Requirements as plm_gemm (1 <= M <= 128, K % 8 == 0, ldx % 8 == 0, x 16-byte aligned).
+ * 8). Requirements as plm_gemm (1 <= M <= 128, K % 8 == 0, K <= 2^24, ldx % 8 == 0, x 16-byte
+ * aligned).
  */
 int plm_gemm_packed(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy, int64_t M,
                     int64_t N, int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream);

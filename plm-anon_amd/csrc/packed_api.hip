@@ -47,22 +47,33 @@ int64_t ksteps(int64_t K) { return (K + 31) / 32; }
 
 int64_t packed_bytes(int64_t N, int64_t K) { return (N + 15) / 16 * ksteps(K) * kFragBytes; }
 
-// k_waves = 4: the workgroup's four wavefronts split the tile's K range (tile = 16*wave_frags
-// rows); k_waves = 1: each wavefront takes its own 16*wave_frags rows (tile = 64*wave_frags rows).
+// k_waves = 4, 8, 16: the workgroup's k_waves wavefronts split the tile's K range (tile =
+// 16*wave_frags rows); k_waves = 1: each of four wavefronts takes its own 16*wave_frags rows
+// (tile = 64*wave_frags rows).
 bool packed_tile_valid(const plm_tile* t) {
   return t != nullptr && (t->wave_frags == 1 || t->wave_frags == 2 || t->wave_frags == 4) &&
-         (t->k_waves == kPackedWaves || t->k_waves == 1) && t->split_k >= 1 && t->split_k <= 64 &&
+         (t->k_waves == 1 || t->k_waves == 4 || t->k_waves == 8 || t->k_waves == 16) && t->split_k >= 1 &&
+         t->split_k <= 64 &&
          (t->unroll == 2 || t->unroll == 4 || t->unroll == 6 || t->unroll == 8);
 }
 
 hipError_t packed_dispatch_dt(int32_t dtype, PackedArgs& a, const plm_tile& t, int cus, hipStream_t s, bool dry) {
-  const bool rows = t.k_waves == 1;
-  if (dtype == PLM_BF16)
-    return rows ? packed_dispatch_bf16_k1(a, t.wave_frags, t.unroll, cus, s, dry)
-                : packed_dispatch_bf16_k4(a, t.wave_frags, t.unroll, cus, s, dry);
-  if (dtype == PLM_F16)
-    return rows ? packed_dispatch_f16_k1(a, t.wave_frags, t.unroll, cus, s, dry)
-                : packed_dispatch_f16_k4(a, t.wave_frags, t.unroll, cus, s, dry);
+  const int nf = t.wave_frags, d = t.unroll;
+  if (dtype == PLM_BF16) {
+    switch (t.k_waves) {
+      case 1: return packed_dispatch_bf16_k1(a, nf, d, cus, s, dry);
+      case 4: return packed_dispatch_bf16_k4(a, nf, d, cus, s, dry);
+      case 8: return packed_dispatch_bf16_k8(a, nf, d, cus, s, dry);
+      case 16: return packed_dispatch_bf16_k16(a, nf, d, cus, s, dry);
+    }
+  } else if (dtype == PLM_F16) {
+    switch (t.k_waves) {
+      case 1: return packed_dispatch_f16_k1(a, nf, d, cus, s, dry);
+      case 4: return packed_dispatch_f16_k4(a, nf, d, cus, s, dry);
+      case 8: return packed_dispatch_f16_k8(a, nf, d, cus, s, dry);
+      case 16: return packed_dispatch_f16_k16(a, nf, d, cus, s, dry);
+    }
+  }
   return hipErrorInvalidConfiguration;
 }
 
@@ -86,7 +97,8 @@ constexpr int kPackedSpinLimit = 1 << 20;  // polls (each one device round trip)
 int packed_check_linear(int32_t dtype, const plm_chain_gemm& g, int64_t M) {
   if (g.x == nullptr || g.w == nullptr || g.y == nullptr) return PLM_ERR_ARGUMENT;
   if (dtype != PLM_BF16 && dtype != PLM_F16) return PLM_ERR_ARGUMENT;
-  if (M < 1 || M > kPackedMaxM || g.N < 1 || g.K < 8 || g.K % 8 != 0 || g.ldx < g.K || g.ldy < g.N)
+  if (M < 1 || M > kPackedMaxM || g.N < 1 || g.K < 8 || g.K > (1 << 24) || g.K % 8 != 0 || g.ldx < g.K ||
+      g.ldy < g.N)
     return PLM_ERR_ARGUMENT;
   if (g.split_k < 1 || g.split_k > 64 || (g.out_f32 != 0 && g.out_f32 != 1)) return PLM_ERR_ARGUMENT;
   // 32-bit buffer offsets: X and the packed weights must each span less than 2 GiB.

@@ -1,5 +1,5 @@
 // f16 instantiations of the packed-weight GEMM with workgroup layout KW = 4
-// (K split across the four wavefronts); one translation unit per (dtype, layout) so that they build in parallel.
+// (K split across four wavefronts); one translation unit per (dtype, layout) so that they build in parallel.
 #include "packed_gemm.h"
 
 namespace plm {

@@ -50,7 +50,7 @@
 
 namespace plm {
 
-constexpr int kPackedWaves = 4;            // wavefronts per workgroup
+constexpr int kPackedWaves = 4;            // wavefronts per workgroup of the row-split layout (KW = 1)
 constexpr int kFragBytes = 1024;           // one packed fragment: 64 lanes x 16 bytes
 constexpr uint32_t kNoLoad = 0x80000000u;  // scalar offset that puts a load out of range (zeros)
 constexpr int kXTileBytes = 16 * 80;       // LDS transpose tile of one X fragment (rows padded to 80 B)
@@ -96,48 +96,95 @@ struct PLinear {
   float* partial;  // split partials
 };
 
+// Wavefronts per workgroup: KW for the K-split layouts, four for the row-split one.
+template <int KW>
+constexpr int packed_waves() {
+  return KW == 1 ? kPackedWaves : KW;
+}
+
 // Weight fragments of a tile.
 template <int NF, int KW>
 constexpr int tile_frags() {
-  return KW == 4 ? NF : 4 * NF;
+  return KW == 1 ? kPackedWaves * NF : NF;
 }
 
+// A load through the constant address space: the chain table does not change while the kernel
+// runs, so its fields can be fetched with scalar loads.
+template <typename T>
+__device__ __forceinline__ T const_load(const T* p) {
+  return *((const __attribute__((address_space(4))) T*)p);
+}
+
+// A linear's descriptor: a chain's from its table, a single linear's from the kernel arguments.
 template <int NF, int KW>
 __device__ __forceinline__ PLinear load_linear(const PackedArgs& a, int gi) {
-  const plm_chain_gemm* src = a.chain != nullptr ? a.chain + gi : &a.single;
+  plm_chain_gemm g = a.single;
+  if (a.chain != nullptr) {
+    const plm_chain_gemm* c = a.chain + gi;
+    g.x = const_load(&c->x);
+    g.w = const_load(&c->w);
+    g.y = const_load(&c->y);
+    g.ldx = const_load(&c->ldx);
+    g.ldy = const_load(&c->ldy);
+    g.N = const_load(&c->N);
+    g.K = const_load(&c->K);
+    g.split_k = const_load(&c->split_k);
+    g.out_f32 = const_load(&c->out_f32);
+    g.consumed = const_load(&c->consumed);
+    g.arrive_base = const_load(&c->arrive_base);
+    g.done_base = const_load(&c->done_base);
+    g.partial_offset = const_load(&c->partial_offset);
+  }
   PLinear L;
-  L.x = sgpr_ptr(src->x);
-  L.wp = sgpr_ptr(src->w);
-  L.y = sgpr_ptr(src->y);
-  L.ldx = sgpr64(src->ldx);
-  L.ldy = sgpr64(src->ldy);
-  L.N = sgpr(src->N);
-  const int K = sgpr(src->K);
+  L.x = sgpr_ptr(g.x);
+  L.wp = sgpr_ptr(g.w);
+  L.y = sgpr_ptr(g.y);
+  L.ldx = sgpr64(g.ldx);
+  L.ldy = sgpr64(g.ldy);
+  L.N = sgpr(g.N);
+  const int K = sgpr(g.K);
   L.Ks = (K + 31) >> 5;
   L.k_last = K - 32 * (L.Ks - 1);
-  L.split = sgpr(src->split_k);
+  L.split = sgpr(g.split_k);
   L.tiles = (((L.N + 15) >> 4) + tile_frags<NF, KW>() - 1) / tile_frags<NF, KW>();
   L.items = L.tiles * L.split;
-  L.out_f32 = sgpr(src->out_f32);
-  L.consumed = sgpr(src->consumed);
-  L.arrive = a.counters + sgpr(src->arrive_base);
-  L.seq = sgpr(src->done_base);
-  L.partial = a.partial + sgpr64(src->partial_offset);
+  L.out_f32 = sgpr(g.out_f32);
+  L.consumed = sgpr(g.consumed);
+  L.arrive = a.counters + sgpr(g.arrive_base);
+  L.seq = sgpr(g.done_base);
+  L.partial = a.partial + sgpr64(g.partial_offset);
   return L;
 }
 
-// K-step range [b, e) of split s: wavefront w's quarter of it (KW = 4) or all of it (KW = 1).
+// K-step range [b, e) of split s: wavefront w's share of it (K-split layouts: 1/KW) or all of it
+// (KW = 1).
+// 32-bit unsigned arithmetic (K <= 2^24, split <= 64), without a division when split == 1 and
+// with shifts for the power-of-two KW: this runs once per item and is on the critical path.
 template <int KW>
 __device__ __forceinline__ void packed_range(int Ks, int s, int split, int w, int& b, int& e) {
-  const int lo = static_cast<int>(static_cast<int64_t>(s) * Ks / split);
-  const int hi = static_cast<int>(static_cast<int64_t>(s + 1) * Ks / split);
+  int lo = 0, hi = Ks;
+  if (split != 1) {
+    lo = static_cast<int>(static_cast<uint32_t>(s * Ks) / static_cast<uint32_t>(split));
+    hi = static_cast<int>(static_cast<uint32_t>((s + 1) * Ks) / static_cast<uint32_t>(split));
+  }
   if constexpr (KW == 1) {
     b = lo;
     e = hi;
   } else {
-    const int n = hi - lo;
-    b = lo + n * w / kPackedWaves;
-    e = lo + n * (w + 1) / kPackedWaves;
+    const uint32_t n = static_cast<uint32_t>(hi - lo);
+    b = lo + static_cast<int>(n * static_cast<uint32_t>(w) / KW);
+    e = lo + static_cast<int>(n * static_cast<uint32_t>(w + 1) / KW);
+  }
+}
+
+// Item -> (tile, split index), without a division when split == 1.
+__device__ __forceinline__ void item_tile(int item, int split, int& tile, int& s) {
+  if (split == 1) {
+    tile = item;
+    s = 0;
+  } else {
+    tile = static_cast<int>(static_cast<uint32_t>(item) / static_cast<uint32_t>(split));
+    s = item - tile * split;
   }
 }
 
@@ -156,8 +203,8 @@ struct PCursor {
 template <int NF, int D, int KW>
 __device__ __forceinline__ void pc_enter(const PLinear& L, int wave, PCursor& c) {
   if (c.item >= L.items) return;
-  const int tile = c.item / L.split;
-  const int s = c.item - tile * L.split;
+  int tile, s;
+  item_tile(c.item, L.split, tile, s);
   int b, e;
   packed_range<KW>(L.Ks, s, L.split, wave, b, e);
   c.st = b;
@@ -180,7 +227,7 @@ __device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\
 // (KW = 1: the workgroup's four wavefronts load one copy between them).
 template <int MT, int KW>
 constexpr int x_per_wave() {
-  return KW == 4 ? MT : (MT + 3) / 4;
+  return KW == 1 ? (MT + 3) / 4 : MT;
 }
 
 // Per-lane operand offsets of one linear.
@@ -198,7 +245,7 @@ __device__ __forceinline__ void packed_offsets(const PLinear& L, int M, int lane
   for (int f = 0; f < NF; ++f) o.wo[f] = static_cast<uint32_t>(f * L.Ks * kFragBytes + lane * 16);
 #pragma unroll
   for (int i = 0; i < x_per_wave<MT, KW>(); ++i) {
-    const int t = KW == 4 ? i : wave + 4 * i;
+    const int t = KW == 1 ? wave + 4 * i : i;
     const int m = 16 * t + (lane >> 2);
     o.xo[i] = (t < MT && m < M) ? static_cast<uint32_t>(m * L.ldx * 2 + (lane & 3) * 16) : kOutOfRange;
     o.xo_last[i] = 8 * (lane & 3) < L.k_last ? o.xo[i] : kOutOfRange;
@@ -274,36 +321,39 @@ __device__ __forceinline__ void packed_store_frag(const PLinear& L, int M, int n
   if (m < M && n < L.N) packed_store4<DT>(L, m, n, v);
 }
 
-// End of an item for this workgroup: sums the four wavefronts' tiles (LDS, wavefront order) and
-// writes Y, or with split > 1 the fp32 partial, then the last split to arrive writes Y.
-template <int DT, int MT, int NF>
+// End of an item for a K-split workgroup: sums the KW wavefronts' tiles (LDS, wavefront order)
+// and writes Y, or with split > 1 the fp32 partial, then the last split to arrive writes Y. With
+// KW > 4 the tiles overlay the wavefronts' X transpose tiles, so the workgroup first waits until
+// every wavefront is past its last K step.
+template <int DT, int MT, int NF, int KW>
 __device__ __forceinline__ void packed_finish(const PLinear& L, int M, int item, int wave, int lane,
                                               f32x4 (&acc)[NF][MT], f32x4* red, int* last_flag) {
   constexpr int Q = NF * MT;
+  if constexpr (KW > 4) lds_sync();
 #pragma unroll
   for (int f = 0; f < NF; ++f)
 #pragma unroll
     for (int t = 0; t < MT; ++t) red[(wave * Q + f * MT + t) * 64 + lane] = acc[f][t];
   lds_sync();
-  const int tile = item / L.split;
-  const int s = item - tile * L.split;
+  int tile, s;
+  item_tile(item, L.split, tile, s);
   const int n0 = tile * NF * 16;
-  f32x4 sum[(Q + kPackedWaves - 1) / kPackedWaves];
+  f32x4 sum[(Q + KW - 1) / KW];
 #pragma unroll
-  for (int i = 0; i * kPackedWaves < Q; ++i) {
-    const int q = wave + kPackedWaves * i;
+  for (int i = 0; i * KW < Q; ++i) {
+    const int q = wave + KW * i;
     if (q < Q) {
       f32x4 v = red[q * 64 + lane];
 #pragma unroll
-      for (int w = 1; w < kPackedWaves; ++w) v += red[(w * Q + q) * 64 + lane];
+      for (int w = 1; w < KW; ++w) v += red[(w * Q + q) * 64 + lane];
       sum[i] = v;
     }
   }
   lds_sync();  // every wavefront has read the tiles; LDS is free for the next item
   if (L.split == 1) {
 #pragma unroll
-    for (int i = 0; i * kPackedWaves < Q; ++i) {
-      const int q = wave + kPackedWaves * i;
+    for (int i = 0; i * KW < Q; ++i) {
+      const int q = wave + KW * i;
       if (q < Q) packed_store_frag<DT, MT>(L, M, n0, q, lane, sum[i]);
     }
     return;
@@ -313,8 +363,8 @@ __device__ __forceinline__ void packed_finish(const PLinear& L, int M, int item,
   const uint32_t tile_bytes = static_cast<uint32_t>(L.split) * Q * kFragBytes;
   const auto prs = make_rsrc(L.partial + static_cast<int64_t>(tile) * L.split * Q * 256, tile_bytes);
 #pragma unroll
-  for (int i = 0; i * kPackedWaves < Q; ++i) {
-    const int q = wave + kPackedWaves * i;
+  for (int i = 0; i * KW < Q; ++i) {
+    const int q = wave + KW * i;
     if (q < Q)
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum[i]), prs,
                                              static_cast<uint32_t>((s * Q + q) * kFragBytes + lane * 16), 0, kCoherent);
@@ -331,8 +381,8 @@ __device__ __forceinline__ void packed_finish(const PLinear& L, int M, int item,
   lds_sync();
   if (*last_flag == 0) return;
 #pragma unroll
-  for (int i = 0; i * kPackedWaves < Q; ++i) {
-    const int q = wave + kPackedWaves * i;
+  for (int i = 0; i * KW < Q; ++i) {
+    const int q = wave + KW * i;
     if (q < Q) {
       f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
       for (int s0 = 0; s0 < L.split; s0 += 8) {
@@ -360,8 +410,8 @@ __device__ __forceinline__ void packed_finish_rows(const PLinear& L, int M, int 
                                                    f32x4 (&acc)[NF][MT], int* last_flag) {
   constexpr int QW = NF * MT;               // fragments of one wavefront
   constexpr int Q = kPackedWaves * QW;      // fragments of the tile
-  const int tile = item / L.split;
-  const int s = item - tile * L.split;
+  int tile, s;
+  item_tile(item, L.split, tile, s);
   const int n0 = (tile * 4 + wave) * NF * 16;
   if (L.split == 1) {
 #pragma unroll
@@ -428,17 +478,20 @@ __device__ __forceinline__ void barrier_arrive(const PackedArgs& a, int64_t epoc
 __device__ __forceinline__ void barrier_wait(const PackedArgs& a, int64_t epoch, int seq, int lane) {
   const int64_t target = ((epoch + 1) << 16) + seq;
   if (threadIdx.x < 64) {
-    // Each lane polls G/64 flags with device-coherent loads, all issued before any is examined.
+    // Each lane polls G/64 flags with device-coherent loads, issued in batches of eight (one
+    // batch covers 512 workgroups) before any of the batch is examined.
     const auto frs = make_rsrc(a.counters + kPackedBarrierBase, static_cast<uint32_t>(a.G) * 8u);
     for (int i = 0;; ++i) {
       int64_t low = INT64_MAX;
+      for (int j0 = 0; j0 * 64 < a.G; j0 += 8) {
 #pragma unroll
-      for (int j = 0; j < kPkMaxWorkgroups / 64; ++j) {
-        if (j * 64 < a.G) {
-          const u32x2 v = __builtin_bit_cast(
-              u32x2, __builtin_amdgcn_raw_buffer_load_b64(frs, static_cast<uint32_t>((j * 64 + lane) * 8), 0, kCoherent));
-          const int64_t f = static_cast<int64_t>((static_cast<uint64_t>(v.y) << 32) | v.x);
-          low = j * 64 + lane < a.G ? min(low, f) : low;
+        for (int j = j0; j < j0 + 8; ++j) {
+          if (j * 64 < a.G) {
+            const u32x2 v = __builtin_bit_cast(
+                u32x2, __builtin_amdgcn_raw_buffer_load_b64(frs, static_cast<uint32_t>((j * 64 + lane) * 8), 0, kCoherent));
+            const int64_t f = static_cast<int64_t>((static_cast<uint64_t>(v.y) << 32) | v.x);
+            low = j * 64 + lane < a.G ? min(low, f) : low;
+          }
         }
       }
       if (__all(low >= target)) break;
@@ -455,9 +508,11 @@ __device__ __forceinline__ void barrier_wait(const PackedArgs& a, int64_t epoch,
 typedef __attribute__((address_space(3))) void PkLdsVoid;
 
 // Cache warming during a barrier: requests up to kWarmFragments more of the next linear's weight
-// fragments this wavefront will stream (after the D stages already in registers) into a scratch
-// KiB of LDS, so that they are on their way from HBM into the caches while the workgroup waits;
-// the pipeline then finds them in L2 / the Infinity Cache.
+// fragments this wavefront will stream (after the D stages already in registers) into a sink KiB
+// of LDS that nothing reads (kept apart from the X tiles: the wavefronts' sink writes may land
+// after another wavefront has written its next X tile), so that they are on their way from HBM
+// into the caches while the workgroup waits; the pipeline then finds them in L2 / the Infinity
+// Cache.
 constexpr int kWarmFragments = 32;
 
 template <int NF, int D, int KW>
@@ -496,25 +551,42 @@ constexpr int packed_regs() {
 template <int MT, int NF, int D, int KW>
 constexpr bool packed_two_per_cu() {
   if constexpr (KW == 1) return packed_regs<MT, NF, D, KW>() <= 100;
+  if constexpr (KW > 4) return false;
   return packed_regs<MT, NF, D, KW>() <= 128 && (MT <= 6 || packed_regs<MT, NF, D, KW>() <= 104);
 }
+// Minimum wavefronts per SIMD the kernel is compiled for (the register budget: 512 per lane
+// divided by it): two or one 4-wavefront workgroups per CU (KW = 1, 4), one 8- or 16-wavefront
+// workgroup per CU (KW = 8: 2 per SIMD; KW = 16: 4 per SIMD, 128 registers).
 template <int MT, int NF, int D, int KW>
-constexpr int packed_min_blocks() {
+constexpr int packed_waves_per_simd() {
+  if constexpr (KW > 4) return KW / 4;
   return packed_two_per_cu<MT, NF, D, KW>() ? 2 : 1;
 }
 
+// LDS bytes before the warm-up sink: KW = 1: two shared X tile sets (double-buffered by K step);
+// KW = 4: the four wavefronts' fp32 tiles (reduction), then a private X transpose tile set per
+// wavefront; KW > 4: the reduction tiles overlaying the private X tile sets.
+template <int MT, int NF, int KW>
+constexpr size_t packed_lds_body() {
+  constexpr size_t red = static_cast<size_t>(KW) * NF * MT * kFragBytes;
+  constexpr size_t xts = static_cast<size_t>(KW) * MT * kXTileBytes;
+  if constexpr (KW == 1) return static_cast<size_t>(2) * MT * kXTileBytes;
+  if constexpr (KW == 4) return red + xts;
+  return red > xts ? red : xts;
+}
+
 template <int DT, int MT, int NF, int D, int KW>
-__global__ __launch_bounds__(64 * kPackedWaves, (packed_min_blocks<MT, NF, D, KW>())) void packed_gemm_kernel(PackedArgs a) {
+__global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT, NF, D, KW>())) void packed_gemm_kernel(PackedArgs a) {
   constexpr int XN = x_per_wave<MT, KW>();
   __shared__ int last_flag;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // LDS: KW = 4: the four wavefronts' fp32 tiles (reduction), then a private X transpose tile set
-  // per wavefront; KW = 1: two shared X tile sets (double-buffered by K step).
   f32x4* red = packed_lds;
-  char* xt = KW == 4 ? reinterpret_cast<char*>(packed_lds) + static_cast<size_t>(kPackedWaves) * NF * MT * kFragBytes +
-                           static_cast<size_t>(wave) * MT * kXTileBytes
-                     : reinterpret_cast<char*>(packed_lds);
+  char* xt = reinterpret_cast<char*>(packed_lds) +
+             (KW == 1 ? 0
+                      : (KW == 4 ? static_cast<size_t>(4) * NF * MT * kFragBytes : 0) +
+                            static_cast<size_t>(wave) * MT * kXTileBytes);
+  PkLdsVoid* sink = (PkLdsVoid*)(reinterpret_cast<char*>(packed_lds) + packed_lds_body<MT, NF, KW>());
   const int xt_write = (lane >> 2) * 80 + (lane & 3) * 16;
   const int xt_read = (lane & 15) * 80 + (lane >> 4) * 16;
   const int64_t epoch = a.sync ? sgpr64(collect(reinterpret_cast<const int64_t*>(a.counters + kPkEpochSlot))) : 0;
@@ -560,7 +632,7 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_min_blocks<MT, NF, D, KW
 #pragma unroll
           for (int j = 0; j < D; ++j) {
             u32x4 xop[MT];
-            if constexpr (KW == 4) {
+            if constexpr (KW != 1) {
 #pragma unroll
               for (int t = 0; t < MT; ++t) *reinterpret_cast<u32x4*>(xt + t * kXTileBytes + xt_write) = xb[j][t];
 #pragma unroll
@@ -586,8 +658,8 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_min_blocks<MT, NF, D, KW
             __builtin_amdgcn_sched_barrier(0);
           }
         }
-        if constexpr (KW == 4)
-          packed_finish<DT, MT, NF>(L, a.M, cp.item, wave, lane, acc, red, &last_flag);
+        if constexpr (KW != 1)
+          packed_finish<DT, MT, NF, KW>(L, a.M, cp.item, wave, lane, acc, red, &last_flag);
         else
           packed_finish_rows<DT, MT, NF>(L, a.M, cp.item, wave, lane, acc, &last_flag);
         cp.item += a.G;
@@ -616,7 +688,7 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_min_blocks<MT, NF, D, KW
           __builtin_amdgcn_sched_barrier(0);
         }
         w_ready = true;
-        warm_weights<NF, D, KW>(Ln, a.G, wave, lane, nx, wrn, on.wo, (PkLdsVoid*)red);
+        warm_weights<NF, D, KW>(Ln, a.G, wave, lane, nx, wrn, on.wo, sink);
       }
       barrier_wait(a, epoch, L.seq, lane);
     }
@@ -630,14 +702,18 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_min_blocks<MT, NF, D, KW
 template <int MT, int NF, int D, int KW>
 constexpr bool packed_compiled() {
   if (MT < 1 || MT > 8 || (NF != 1 && NF != 2 && NF != 4) || (D != 2 && D != 4 && D != 6 && D != 8)) return false;
-  if ((KW != 1 && KW != 4) || NF * MT > 20) return false;
+  if ((KW != 1 && KW != 4 && KW != 8 && KW != 16) || NF * MT > 20) return false;
+  if constexpr (KW > 4) {
+    // One workgroup per CU; the pipeline within the per-wavefront budget (measured without scratch).
+    return packed_lds_body<MT, NF, KW>() + kFragBytes <= 160 * 1024 &&
+           packed_regs<MT, NF, D, KW>() <= (KW == 8 ? 144 : 60);
+  }
   return packed_two_per_cu<MT, NF, D, KW>() || (MT <= 4 && packed_regs<MT, NF, D, KW>() <= 320);
 }
 
 template <int MT, int NF, int KW>
 constexpr size_t packed_lds_bytes() {
-  return KW == 4 ? static_cast<size_t>(kPackedWaves) * (NF * MT * kFragBytes + MT * kXTileBytes)
-                 : static_cast<size_t>(2) * MT * kXTileBytes;
+  return packed_lds_body<MT, NF, KW>() + kFragBytes;  // + the warm-up sink
 }
 
 // Launches with G = min(a.G, resident workgroups), where a.G arrives as the most items of any
@@ -658,11 +734,8 @@ hipError_t packed_launch(PackedArgs& a, int cus, hipStream_t stream, bool dry) {
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
         if (e != hipSuccess) return e;
       }
-      int n = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(kern), 64 * kPackedWaves, lds) !=
-              hipSuccess ||
-          n < 1)
-        return hipErrorInvalidConfiguration;
+      const int n = resident_per_cu(reinterpret_cast<const void*>(kern), 64 * packed_waves<KW>(), lds);
+      if (n < 1) return hipErrorInvalidConfiguration;
       per_cu = n;
     }
     const int resident = min(cus * per_cu, kPkMaxWorkgroups);
@@ -672,7 +745,7 @@ hipError_t packed_launch(PackedArgs& a, int cus, hipStream_t stream, bool dry) {
     }
     a.G = a.sync ? resident : min(a.G, resident);
     if (a.G < 1) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL(kern, dim3(a.G), dim3(64 * kPackedWaves), lds, stream, a);
+    hipLaunchKernelGGL(kern, dim3(a.G), dim3(64 * packed_waves<KW>()), lds, stream, a);
     if (a.sync) hipLaunchKernelGGL(packed_epoch_kernel<>, dim3(1), dim3(64), 0, stream, a.counters);
     return hipGetLastError();
   }
@@ -711,9 +784,13 @@ hipError_t packed_dispatch_kw(PackedArgs& a, int nf, int d, int cus, hipStream_t
 }
 
 // One translation unit per (dtype, workgroup layout) so that they build in parallel.
-hipError_t packed_dispatch_bf16_k4(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
 hipError_t packed_dispatch_bf16_k1(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
-hipError_t packed_dispatch_f16_k4(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_bf16_k4(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_bf16_k8(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_bf16_k16(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
 hipError_t packed_dispatch_f16_k1(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_f16_k4(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_f16_k8(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_f16_k16(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
 
 }  // namespace plm

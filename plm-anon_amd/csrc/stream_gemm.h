@@ -945,11 +945,8 @@ hipError_t stream_launch(StreamArgs& a, int cus, hipStream_t stream, bool dry) {
     static size_t cached_lds = 0;
     static int cached_per_cu = 0;
     if (cached_lds != lds) {
-      int per_cu = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kern),
-                                                       64 * kStreamWaves, lds) != hipSuccess ||
-          per_cu < 1)
-        return hipErrorInvalidConfiguration;
+      const int per_cu = resident_per_cu(reinterpret_cast<const void*>(kern), 64 * kStreamWaves, lds);
+      if (per_cu < 1) return hipErrorInvalidConfiguration;
       cached_lds = lds;
       cached_per_cu = per_cu;
     }

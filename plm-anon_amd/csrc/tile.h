@@ -16,6 +16,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 #include <stdint.h>
 
 #include "plm_amd.h"
@@ -91,6 +93,26 @@ constexpr int kPackedArriveBase = 49152;
 constexpr int kPackedBarrierBase = 61440;
 
 inline bool aligned16_ptr(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Workgroups of `kern` (with `threads` threads and `dynamic_lds` bytes of dynamic LDS) that one CU
+// holds at once: the runtime's occupancy figure, capped by the LDS count with each workgroup's
+// LDS (static and dynamic) rounded up to the 512-byte allocation granule. A launch whose
+// workgroups wait on each other relies on this count being exact or low, and the runtime's
+// figure has been seen to ignore the granule. Returns 0 on error.
+inline int resident_per_cu(const void* kern, int threads, size_t dynamic_lds) {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, dynamic_lds) != hipSuccess || n < 1) return 0;
+  hipFuncAttributes attr{};
+  if (hipFuncGetAttributes(&attr, kern) != hipSuccess) return 0;
+  int dev = 0, capacity = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&capacity, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess ||
+      capacity <= 0)
+    capacity = 160 * 1024;
+  const size_t per_group = (dynamic_lds + attr.sharedSizeBytes + 511) / 512 * 512;
+  if (per_group > 0) n = std::min<int>(n, static_cast<int>(static_cast<size_t>(capacity) / per_group));
+  return n;
+}
 
 // Cross-workgroup hand-off (split-K partials, per-workgroup row states) without cache-wide
 // maintenance. The MI355X has one L2 per XCD and they are not coherent with each other for

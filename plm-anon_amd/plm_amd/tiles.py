@@ -2,10 +2,10 @@
 
 A tile is ``{"wave_frags", "k_waves", "split_k", "unroll"}`` (``struct plm_tile`` in
 ``include/plm_amd.h``). For the packed-weight GEMM behind ``fast_gemm`` (plm_gemm_packed), each
-of a workgroup's four wavefronts streams ``16*wave_frags`` weight rows, and either
-``k_waves`` = 4: the four split the K range of one ``16*wave_frags``-row tile (summed in LDS), or
-``k_waves`` = 1: the four take adjacent rows of a ``64*wave_frags``-row tile over the whole K range
-and share one copy of X through LDS. ``split_k`` workgroups split K further (fp32 partials summed
+wavefront of a workgroup streams ``16*wave_frags`` weight rows, and either
+``k_waves`` = 4, 8 or 16: that many wavefronts split the K range of one ``16*wave_frags``-row tile
+(summed in LDS), or ``k_waves`` = 1: four wavefronts take adjacent rows of a ``64*wave_frags``-row
+tile over the whole K range and share one copy of X through LDS. ``split_k`` workgroups split K further (fp32 partials summed
 in split order); ``unroll`` (2, 4, 6 or 8) K steps of loads are in flight per wavefront. Items
 (tile x split) = ``ceil(ceil(N/16) / tile_frags) * split_k`` over a persistent grid.
 
@@ -18,16 +18,27 @@ from __future__ import annotations
 import math
 
 CU_COUNT = 256          # MI355X compute units
-K_WAVES = 4             # wavefronts per workgroup
-LAYOUTS = (4, 1)        # k_waves: K split across the wavefronts, or rows split across them
+K_WAVES = 4             # wavefronts per workgroup of the row-split layout
+LAYOUTS = (4, 8, 16, 1)  # k_waves: K split across 4, 8 or 16 wavefronts, or rows split across 4
+LDS_LIMIT = 160 * 1024
+FRAG = 1024             # bytes of one packed fragment
+X_TILE = 16 * 80        # LDS transpose tile of one X fragment
 WAVE_FRAGS = (1, 2, 4)
 DEPTHS = (2, 4, 6, 8)
 SPLITS = (1, 2, 3, 4, 6, 8, 12, 16)
 
 
 def _regs(mt: int, nf: int, d: int, kw: int) -> int:
-    xn = mt if kw == K_WAVES else (mt + 3) // 4
+    xn = (mt + 3) // 4 if kw == 1 else mt
     return (d * (nf + xn) + nf * mt + (mt if kw == 1 else 0)) * 4
+
+
+def lds_body(mt: int, nf: int, kw: int) -> int:
+    """LDS bytes before the warm-up sink (mirrors ``packed_lds_body``)."""
+    red, xts = kw * nf * mt * FRAG, kw * mt * X_TILE
+    if kw == 1:
+        return 2 * mt * X_TILE
+    return red + xts if kw == 4 else max(red, xts)
 
 
 def two_per_cu(M: int, cfg: dict) -> bool:
@@ -36,6 +47,8 @@ def two_per_cu(M: int, cfg: dict) -> bool:
     r = _regs(mt, nf, d, kw)
     if kw == 1:
         return r <= 100
+    if kw > 4:
+        return False
     return r <= 128 and (mt <= 6 or r <= 104)
 
 
@@ -44,9 +57,11 @@ def compiled(M: int, cfg: dict) -> bool:
     ``packed_compiled`` in csrc/packed_gemm.h: at most 20 accumulator fragments, and two
     workgroups per CU, or one with the pipeline within 320 registers for M <= 64)."""
     mt, nf, d, kw = math.ceil(M / 16), cfg["wave_frags"], cfg["unroll"], cfg["k_waves"]
-    if not (1 <= mt <= 8 and nf in WAVE_FRAGS and d in DEPTHS and kw in LAYOUTS):
+    if not (1 <= mt <= 8 and nf in WAVE_FRAGS and d in DEPTHS and kw in LAYOUTS) or nf * mt > 20:
         return False
-    return nf * mt <= 20 and (two_per_cu(M, cfg) or (mt <= 4 and _regs(mt, nf, d, kw) <= 320))
+    if kw > 4:
+        return lds_body(mt, nf, kw) + FRAG <= LDS_LIMIT and _regs(mt, nf, d, kw) <= (144 if kw == 8 else 60)
+    return two_per_cu(M, cfg) or (mt <= 4 and _regs(mt, nf, d, kw) <= 320)
 
 
 def tile_frags(cfg: dict) -> int:
@@ -59,8 +74,8 @@ def items(N: int, cfg: dict) -> int:
 
 
 def steps_per_wave(K: int, cfg: dict) -> int:
-    """32-wide K steps each wavefront streams per item (k_waves = 4: the shortest quarter)."""
-    return math.ceil(K / 32) // cfg["split_k"] // (K_WAVES if cfg["k_waves"] == K_WAVES else 1)
+    """32-wide K steps each wavefront streams per item (K-split layouts: the shortest share)."""
+    return math.ceil(K / 32) // cfg["split_k"] // (1 if cfg["k_waves"] == 1 else cfg["k_waves"])
 
 
 def candidates(M: int, N: int, K: int, supported=None) -> list[dict]:
@@ -109,7 +124,7 @@ def packed_chain_split(N: int, K: int, cfg: dict, workgroups: int) -> int:
     (reduction, stores; with split > 1 the partial round trip)."""
     tiles_ = math.ceil(math.ceil(N / 16) / tile_frags(cfg))
     ks = math.ceil(K / 32)
-    kw = K_WAVES if cfg["k_waves"] == K_WAVES else 1
+    kw = 1 if cfg["k_waves"] == 1 else cfg["k_waves"]
     best, best_cost = 1, None
     for split in SPLITS:
         if split > 1 and ks // split // kw < 2:

@@ -139,7 +139,7 @@ def test_tile_support_matches_register_budget():
     for M in (1, 7, 16, 17, 42, 56, 64, 65, 110, 128):
         for nf in (1, 2, 3, 4):
             for u in (1, 2, 4, 8):
-                for kw in (1, 4, 8):
+                for kw in (1, 4, 8, 16, 5):
                     cfg = {"wave_frags": nf, "k_waves": kw, "split_k": 1, "unroll": u}
                     assert tiles.compiled(M, cfg) == fast_gemm.tile_supported(M, 2048, cfg), (M, cfg)
 

@@ -66,7 +66,9 @@ def test_three_links(device, splits, packed):
                                  {"wave_frags": 4, "k_waves": 4, "split_k": 1, "unroll": 8},
                                  {"wave_frags": 1, "k_waves": 4, "split_k": 1, "unroll": 4},
                                  {"wave_frags": 2, "k_waves": 1, "split_k": 1, "unroll": 2},
-                                 {"wave_frags": 1, "k_waves": 1, "split_k": 1, "unroll": 8}],
+                                 {"wave_frags": 1, "k_waves": 1, "split_k": 1, "unroll": 8},
+                                 {"wave_frags": 2, "k_waves": 8, "split_k": 1, "unroll": 2},
+                                 {"wave_frags": 1, "k_waves": 16, "split_k": 1, "unroll": 2}],
                          ids=lambda c: f"nf{c['wave_frags']}d{c['unroll']}kw{c['k_waves']}")
 def test_packed_chain_tiles(device, cfg):
     # Deep and shallow pipelines, and widths whose K is not a multiple of 32 in the middle link.

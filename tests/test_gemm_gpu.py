@@ -134,7 +134,9 @@ def test_round_widths_edge_cases(device, M):
     for cfg in (tiles.heuristic_tile(M, N, K, supported=supported),
                 {"wave_frags": 1, "k_waves": 4, "split_k": 3, "unroll": 2},
                 {"wave_frags": 1, "k_waves": 1, "split_k": 1, "unroll": 2},
-                {"wave_frags": 2, "k_waves": 1, "split_k": 3, "unroll": 4}):
+                {"wave_frags": 2, "k_waves": 1, "split_k": 3, "unroll": 4},
+                {"wave_frags": 2, "k_waves": 8, "split_k": 1, "unroll": 2},
+                {"wave_frags": 1, "k_waves": 16, "split_k": 2, "unroll": 2}):
         if supported(cfg):
             check(_run(x, w, cfg, device), x, w)
 
@@ -187,7 +189,9 @@ def test_small_integers_are_exact(device):
     for cfg in ({"wave_frags": 2, "k_waves": 4, "split_k": 1, "unroll": 2},
                 {"wave_frags": 1, "k_waves": 4, "split_k": 4, "unroll": 2},
                 {"wave_frags": 1, "k_waves": 1, "split_k": 1, "unroll": 8},
-                {"wave_frags": 2, "k_waves": 1, "split_k": 4, "unroll": 2}):
+                {"wave_frags": 2, "k_waves": 1, "split_k": 4, "unroll": 2},
+                {"wave_frags": 2, "k_waves": 8, "split_k": 3, "unroll": 4},
+                {"wave_frags": 1, "k_waves": 16, "split_k": 1, "unroll": 2}):
         y = _run(x, w, cfg, device).cpu().double().numpy()
         assert (y == exact).all()
 
