@@ -208,7 +208,7 @@ def capture_graph(fn):
 
 
 # Tile of the packed chained round: 32-row tiles, two-stage pipeline (the fastest measured).
-CHAIN_CFG = {"wave_frags": 2, "k_waves": 4, "split_k": 1, "unroll": 2}
+CHAIN_CFG = {"wave_frags": 2, "k_waves": 8, "split_k": 1, "unroll": 2}
 
 
 def round_chain(rnd):

@@ -97,23 +97,32 @@ def candidates(M: int, N: int, K: int, supported=None) -> list[dict]:
     return out
 
 
+def _first_compiled(M: int, nf: int, layouts, supported) -> dict | None:
+    for kw in layouts:
+        for d in DEPTHS:
+            cfg = {"wave_frags": nf, "k_waves": kw, "split_k": 1, "unroll": d}
+            if compiled(M, cfg) and (supported is None or supported(cfg)):
+                return cfg
+    return None
+
+
 def heuristic_tile(M: int, N: int, K: int, supported=None) -> dict:
     """A reasonable tile without measurement (what the MI355X measurements of the round shapes
     favour): 32 rows per wavefront with a two-stage pipeline; rows split across the wavefronts
     (128-row tiles) when that alone gives every compute unit a tile (the LM head: one round of
-    tiles instead of three and a fraction), else K split across them, and K splitting until about
-    three quarters of the compute units have an item, keeping at least two K steps per wavefront."""
+    tiles instead of three and a fraction), else K split across 8 wavefronts (4 where 8 is not
+    compiled), and K splitting until about three quarters of the compute units have an item,
+    keeping at least two K steps per wavefront."""
     for nf in (2, 4, 1):
-        kw = 1 if math.ceil(N / 16) // (K_WAVES * nf) >= CU_COUNT else K_WAVES
-        for d in (2, 4, 6, 8):
-            cfg = {"wave_frags": nf, "k_waves": kw, "split_k": 1, "unroll": d}
-            if not compiled(M, cfg) or (supported is not None and not supported(cfg)):
-                continue
-            split = 1
-            while (items(N, dict(cfg, split_k=split)) < CU_COUNT * 3 // 4 and
-                   steps_per_wave(K, dict(cfg, split_k=2 * split)) >= 2 and split < 16):
-                split *= 2
-            return dict(cfg, split_k=split)
+        layouts = (1,) if math.ceil(N / 16) // (K_WAVES * nf) >= CU_COUNT else (8, 4)
+        cfg = _first_compiled(M, nf, layouts, supported)
+        if cfg is None:
+            continue
+        split = 1
+        while (items(N, dict(cfg, split_k=split)) < CU_COUNT * 3 // 4 and
+               steps_per_wave(K, dict(cfg, split_k=2 * split)) >= 2 and split < 16):
+            split *= 2
+        return dict(cfg, split_k=split)
     raise ValueError(f"no compiled tile fits (M={M}, N={N}, K={K})")
 
 
