@@ -207,8 +207,21 @@ int plm_lm_head_verify(int32_t dtype, const void* x, int64_t ldx, const void* w,
                        int64_t K, const int64_t* pending, float p, int32_t round_mode, uint8_t* accept,
                        int64_t* argmax, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream);
 
-/* Workspace bytes plm_lm_head_verify needs (counter area first, as for plm_gemm). */
+/* Workspace bytes plm_lm_head_verify and plm_lm_head_verify_packed need (counter area first, as for
+ * plm_gemm). */
 size_t plm_lm_head_verify_workspace_bytes(int64_t R, int64_t V, int64_t K, const plm_tile* tile);
+
+/*
+ * plm_lm_head_verify over a packed W (plm_pack_weight; the same decision rule and outputs) on the
+ * packed GEMM's row-split pipeline: `tile` has k_waves = 1, split_k = 1, wave_frags 2 or 4 and
+ * unroll 2, 4 or 8. The logits it decides on are bit for bit those plm_gemm_packed_f32out returns
+ * with any such tile. Requirements: 1 <= R <= 64, K % 8 == 0, K <= 2^24, ldx % 8 == 0, x and
+ * packed_w 16-byte aligned.
+ */
+int plm_lm_head_verify_packed(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, int64_t R, int64_t V,
+                              int64_t K, const int64_t* pending, float p, int32_t round_mode, uint8_t* accept,
+                              int64_t* argmax, const plm_tile* tile, void* workspace, size_t workspace_bytes,
+                              void* stream);
 
 /* Human-readable name of a status code. */
 const char* plm_status_string(int32_t status);

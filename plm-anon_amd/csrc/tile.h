@@ -79,8 +79,9 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
 // Ints of the counter area, so that every entry point can share one workspace:
 //   0, 1      streaming chain: launch epoch, workgroups exited
 //   2         error flag (PLM_WORKSPACE_ERROR_INDEX), any chain
-//   8         verify: workgroups finished
+//   8         verify: workgroups finished (packed verify: groups of workgroups finished)
 //   10, 11    packed chain: launch epoch (int64)
+//   [16, 48)  packed verify: workgroups finished, per group of kVerifyGroupSize
 //   [64, 32768)      streaming kernel: split-K arrival counters
 //   [32768, 49152)   streaming chain: tile-done flags
 //   [49152, 61440)   packed kernel: split-K arrival counters
@@ -88,6 +89,8 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
 constexpr size_t kCounterBytes = PLM_WORKSPACE_COUNTER_BYTES;
 constexpr int64_t kMaxCounters = static_cast<int64_t>(kCounterBytes / sizeof(int));
 constexpr int kVerifyCounter = 8;
+constexpr int kVerifyGroupBase = 16;
+constexpr int kVerifyGroupSize = 32;
 constexpr int kStreamDoneEnd = 32768 + 16384;
 constexpr int kPackedArriveBase = 49152;
 constexpr int kPackedBarrierBase = 61440;

@@ -24,6 +24,7 @@
 #include <climits>
 #include <cmath>
 
+#include "packed_gemm.h"
 #include "plm_amd.h"
 #include "tile.h"
 
@@ -43,6 +44,9 @@ struct VerifyArgs {
   float* own;        // [R]
   float* state;      // [G][R][3]: row max, sum of exp, sum of exp above own
   int* state_idx;    // [G][R]: argmax
+  int* group_counter;  // packed verify: [G / kVerifyGroupSize], zero between launches
+  float* gstate;       // packed verify: [groups][R][3], the merged state of each group
+  int* gstate_idx;     // packed verify: [groups][R]
 };
 
 // Online-softmax state of one row: maximum, sum of exp(l - max), sum of exp(l - max) over l > l_own,
@@ -306,15 +310,391 @@ hipError_t verify_dispatch(const VerifyArgs& a, const plm_tile& t, int cu, hipSt
   return hipErrorInvalidConfiguration;
 }
 
+// ---------------------------------------------------------------------------------------------
+// The same step over packed weights (plm_pack_weight), on the packed GEMM's row-split pipeline
+// (csrc/packed_gemm.h, KW = 1): a workgroup's four wavefronts each own 16*NF vocabulary rows of a
+// 64*NF-row tile over the whole K range, share one copy of X through LDS, and accumulate every
+// logit in one MFMA chain over the K steps in ascending order. No cross-wavefront reduction is
+// needed, so each wavefront folds its own logits into per-row states right after its K steps.
+//
+// The proposal logit of row r is recomputed by one wavefront with exactly that MFMA chain (the
+// packed fragment row holding pending[r] as A, row r's X fragment as B, K steps ascending), which
+// makes it bit-identical to the main pass's value for that column; plm_gemm_packed_f32out with a
+// row-split tile (k_waves = 1, split_k = 1) returns the same logits.
+
+// One wavefront per row: own[r] = logit[r, pending[r]] (NaN for an id outside [0, V)).
+template <int DT, int D>
+__global__ __launch_bounds__(64) void verify_packed_own_kernel(VerifyArgs a) {
+  const int lane = threadIdx.x;
+  const int r = blockIdx.x;
+  const int64_t pid64 = a.pending[r];
+  if (pid64 < 0 || pid64 >= a.V) {
+    if (lane == 0) a.own[r] = NAN;
+    return;
+  }
+  const int pid = static_cast<int>(pid64);
+  const int Ks = (a.K + 31) >> 5;
+  const int k_last = a.K - 32 * (Ks - 1);
+  // The packed fragment row (16 vocabulary rows) holding pid, and row r's X fragment in the MFMA
+  // operand order: lane l = X row 16*(r/16) + l%16, K elements 8*(l/16) .. +8 of each step.
+  const auto wr = make_rsrc(reinterpret_cast<const char*>(a.w) + static_cast<int64_t>(pid >> 4) * Ks * kFragBytes,
+                            static_cast<uint32_t>(Ks) * kFragBytes);
+  const auto xr = make_rsrc(a.x, static_cast<uint32_t>(a.R * a.ldx * 2));
+  const int xrow = 16 * (r >> 4) + (lane & 15);
+  const uint32_t xo = xrow < a.R ? static_cast<uint32_t>(xrow * a.ldx * 2 + (lane >> 4) * 16) : kOutOfRange;
+  const uint32_t xo_last = 8 * (lane >> 4) < k_last ? xo : kOutOfRange;
+  const uint32_t wo = static_cast<uint32_t>(lane * 16);
+  u32x4 wb[D], xb[D];
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    const bool live = j < Ks;
+    wb[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                          wr, wo, static_cast<int>(live ? j * kFragBytes : kNoLoad), 0));
+    xb[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                          xr, j == Ks - 1 ? xo_last : xo, static_cast<int>(live ? j * 64 : kNoLoad), 0));
+  }
+  for (int s0 = 0; s0 < Ks; s0 += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      acc = mfma_16x16x32<DT>(wb[j], xb[j], acc);
+      const int n = s0 + D + j;
+      const bool live = n < Ks;
+      wb[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            wr, wo, static_cast<int>(live ? n * kFragBytes : kNoLoad), 0));
+      xb[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            xr, n == Ks - 1 ? xo_last : xo, static_cast<int>(live ? n * 64 : kNoLoad), 0));
+    }
+  }
+  // Element (vocabulary row pid%16, column r%16) of the 16x16 result: lane r%16 + 16*((pid%16)/4),
+  // component pid%4.
+  const int v = pid & 15;
+  if (lane == (r & 15) + 16 * (v >> 2)) a.own[r] = round_through(acc[v & 3], a.round_mode);
+}
+
+// The final merges run once per launch, on its critical path, so their code is kept short (rolled
+// loops: code executed once is fetched cold) and their loads are issued in one batch.
+//
+// gather_states: the workgroup's threads load member (first + i), i < count <= 32, of every row
+// (device-coherent: other workgroups wrote them) into grid[i][m] in LDS; absent entries are left
+// unread.
+__device__ __forceinline__ void gather_states(const float* st, const int* st_idx, int first, int count, int R,
+                                              f32x4* grid) {
+  const auto fr = make_rsrc(st, static_cast<uint32_t>(first + kVerifyGroupSize) * R * 3 * sizeof(float));
+  const auto ir = make_rsrc(st_idx, static_cast<uint32_t>(first + kVerifyGroupSize) * R * sizeof(int));
+  constexpr int kPer = kVerifyGroupSize * 64 / (64 * kPackedWaves);  // entries per thread
+  f32x4 v[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int i = static_cast<int>(threadIdx.x) + 64 * kPackedWaves * k;
+    const int mem = i >> 6, m = i & 63;
+    const bool ok = mem < count && m < R;
+    const uint32_t slot = static_cast<uint32_t>((first + mem) * R + m);
+#pragma unroll
+    for (int c = 0; c < 3; ++c)
+      v[k][c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(fr, ok ? (slot * 3 + c) * 4 : kOutOfRange, 0, kCoherent));
+    v[k][3] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ir, ok ? slot * 4 : kOutOfRange, 0, kCoherent));
+  }
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) grid[static_cast<int>(threadIdx.x) + 64 * kPackedWaves * k] = v[k];
+  __syncthreads();
+}
+
+// Row m's state merged over members 0..count-1 of grid (lane i holds member i; a 32-lane
+// butterfly in a fixed order), valid in lanes 0..31.
+__device__ __forceinline__ RowState merge_members(const f32x4* grid, int count, int m, int lane) {
+  RowState s = empty_state();
+  if (lane < count) {
+    const f32x4 g = grid[lane * 64 + m];
+    const float idx_bits = g[3];  // (a bit cast applied to the vector element itself read element 0)
+    s = RowState{g[0], g[1], g[2], __builtin_bit_cast(int, idx_bits)};
+  }
+#pragma unroll 1
+  for (int off = kVerifyGroupSize / 2; off >= 1; off >>= 1) s = merge(s, shfl_xor_state(s, off));
+  return s;
+}
+
+// Folds a wavefront's logits into its row states: column n holds vocabulary rows
+// n0 + 16f + i of acc[f][t][i] for row 16t + lane%16; the four lanes of a row (lane%16 equal)
+// combine through two butterflies. Tile maximum with lowest-index ties, then the two exponential
+// sums against it, merged into the running state.
+template <int MODE>
+__device__ __forceinline__ float round_logit(float v) {
+  if constexpr (MODE == PLM_ROUND_BF16) return static_cast<float>(static_cast<__bf16>(v));
+  if constexpr (MODE == PLM_ROUND_F16) return static_cast<float>(static_cast<_Float16>(v));
+  return v;
+}
+
+template <int MT, int NF, int MODE>
+__device__ __forceinline__ void fold_columns(const f32x4 (&acc)[NF][MT], int n0, int V, const float (&own_l)[MT],
+                                             RowState (&rs)[MT]) {
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    float lv[NF][4];
+    float mx = -INFINITY;
+    int ai = INT_MAX;
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int n = n0 + 16 * f + i;
+        const bool valid = n < V;
+        const float l = valid ? round_logit<MODE>(acc[f][t][i]) : -INFINITY;
+        lv[f][i] = l;
+        if (valid && (l > mx || (l == mx && n < ai))) {
+          mx = l;
+          ai = n;
+        }
+      }
+#pragma unroll
+    for (int off = 16; off <= 32; off <<= 1) {
+      const float omx = __shfl_xor(mx, off, 64);
+      const int oai = __shfl_xor(ai, off, 64);
+      if (omx > mx || (omx == mx && oai < ai)) {
+        mx = omx;
+        ai = oai;
+      }
+    }
+    float e = 0.f, ab = 0.f;
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float l = lv[f][i];
+        const float ex = l == -INFINITY ? 0.f : expf(l - mx);
+        e += ex;
+        ab += l > own_l[t] ? ex : 0.f;
+      }
+#pragma unroll
+    for (int off = 16; off <= 32; off <<= 1) {
+      e += __shfl_xor(e, off, 64);
+      ab += __shfl_xor(ab, off, 64);
+    }
+    if (mx != -INFINITY) rs[t] = merge(rs[t], RowState{mx, e, ab, ai});
+  }
+}
+
+template <int MT, int NF, int D>
+constexpr bool verify_packed_compiled() {
+  return MT >= 1 && MT <= 4 && (NF == 2 || NF == 4) && (D == 2 || D == 4 || D == 8) && packed_compiled<MT, NF, D, 1>();
+}
+
+template <int DT, int MT, int NF, int D>
+__global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D, 1>())) void verify_packed_main_kernel(
+    VerifyArgs a) {
+  constexpr int KW = 1;
+  constexpr int XN = x_per_wave<MT, KW>();
+  __shared__ float st_mx[kPackedWaves][64], st_se[kPackedWaves][64], st_ab[kPackedWaves][64];
+  __shared__ int st_ai[kPackedWaves][64];
+  __shared__ f32x4 grid[kVerifyGroupSize * 64];  // final merges: [member][row]
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  char* xt = reinterpret_cast<char*>(packed_lds);
+  const int xt_write = (lane >> 2) * 80 + (lane & 3) * 16;
+  const int xt_read = (lane & 15) * 80 + (lane >> 4) * 16;
+
+  PLinear L{};
+  L.x = a.x;
+  L.wp = a.w;
+  L.ldx = a.ldx;
+  L.N = a.V;
+  L.Ks = (a.K + 31) >> 5;
+  L.k_last = a.K - 32 * (L.Ks - 1);
+  L.split = 1;
+  L.tiles = (((a.V + 15) >> 4) + tile_frags<NF, KW>() - 1) / tile_frags<NF, KW>();
+  L.items = L.tiles;
+  POffsets<MT, NF, XN> o;
+  packed_offsets<MT, NF, KW>(L, a.R, lane, wave, o);
+  const auto wr = make_rsrc(L.wp, static_cast<uint32_t>((L.N + 15) >> 4) * L.Ks * kFragBytes);
+  const auto xr = make_rsrc(L.x, static_cast<uint32_t>(a.R * L.ldx * 2));
+
+  // Row states of the rows this lane's accumulators hold: row 16t + lane%16.
+  RowState rs[MT];
+  float own_l[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    rs[t] = empty_state();
+    const int m = 16 * t + (lane & 15);
+    own_l[t] = m < a.R ? a.own[m] : 0.f;
+  }
+
+  u32x4 wb[D][NF], xb[D][XN];
+  PCursor ld{static_cast<int>(blockIdx.x), 0, 0, 0, 0};
+  pc_enter<NF, D, KW>(L, wave, ld);
+  PCursor cp = ld;
+  if (ld.item < L.items) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      issue_w<NF>(wr, ld, L.items, o.wo, wb[j]);
+      issue_x<MT, NF, XN>(xr, ld, L.items, L.Ks, o, xb[j]);
+      pc_advance<NF, D, KW>(L, a.G, wave, ld);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    for (;;) {
+      f32x4 acc[NF][MT];
+#pragma unroll
+      for (int f = 0; f < NF; ++f)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) acc[f][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int steps = cp.pend - cp.st;  // a multiple of D
+      for (int i = 0; i < steps; i += D) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+          u32x4 xop[MT];
+          char* xs = xt + (j & 1) * MT * kXTileBytes;
+#pragma unroll
+          for (int q = 0; q < XN; ++q)
+            if (wave + 4 * q < MT) *reinterpret_cast<u32x4*>(xs + (wave + 4 * q) * kXTileBytes + xt_write) = xb[j][q];
+          lds_sync();
+#pragma unroll
+          for (int t = 0; t < MT; ++t) xop[t] = *reinterpret_cast<const u32x4*>(xs + t * kXTileBytes + xt_read);
+#pragma unroll
+          for (int f = 0; f < NF; ++f)
+#pragma unroll
+            for (int t = 0; t < MT; ++t) acc[f][t] = mfma_16x16x32<DT>(wb[j][f], xop[t], acc[f][t]);
+          issue_w<NF>(wr, ld, L.items, o.wo, wb[j]);
+          issue_x<MT, NF, XN>(xr, ld, L.items, L.Ks, o, xb[j]);
+          pc_advance<NF, D, KW>(L, a.G, wave, ld);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      // Fold this wavefront's 16*NF columns into the row states (rounding mode resolved once per
+      // item, not per element).
+      const int n0 = (cp.item * kPackedWaves + wave) * NF * 16 + 4 * (lane >> 4);
+      if (a.round_mode == PLM_ROUND_BF16)
+        fold_columns<MT, NF, PLM_ROUND_BF16>(acc, n0, a.V, own_l, rs);
+      else if (a.round_mode == PLM_ROUND_F16)
+        fold_columns<MT, NF, PLM_ROUND_F16>(acc, n0, a.V, own_l, rs);
+      else
+        fold_columns<MT, NF, PLM_ROUND_F32>(acc, n0, a.V, own_l, rs);
+      cp.item += a.G;
+      if (cp.item >= L.items) break;
+      pc_enter<NF, D, KW>(L, wave, cp);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+
+  // The workgroup's state of each row: its four wavefronts merged in wavefront order.
+  if (lane < 16) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int m = 16 * t + lane;
+      st_mx[wave][m] = rs[t].mx;
+      st_se[wave][m] = rs[t].se;
+      st_ab[wave][m] = rs[t].ab;
+      st_ai[wave][m] = rs[t].ai;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < a.R) {
+    const int m = threadIdx.x;
+    RowState s0 = RowState{st_mx[0][m], st_se[0][m], st_ab[0][m], st_ai[0][m]};
+#pragma unroll
+    for (int w = 1; w < kPackedWaves; ++w) s0 = merge(s0, RowState{st_mx[w][m], st_se[w][m], st_ab[w][m], st_ai[w][m]});
+    const int64_t slot = static_cast<int64_t>(blockIdx.x) * a.R + m;
+    publish(a.state + slot * 3 + 0, s0.mx);
+    publish(a.state + slot * 3 + 1, s0.se);
+    publish(a.state + slot * 3 + 2, s0.ab);
+    publish(a.state_idx + slot, s0.ai);
+  }
+  // Two-level merge: the last workgroup of each group of kVerifyGroupSize merges the group's
+  // states, the last group to finish merges the group states. Each level is one batch of
+  // device-coherent loads per lane (lane l holds member l of the group) and a butterfly.
+  const int group = blockIdx.x / kVerifyGroupSize;
+  const int gsize = min(kVerifyGroupSize, a.G - group * kVerifyGroupSize);
+  if (!arrive_last(a.group_counter + group, gsize)) return;
+  gather_states(a.state, a.state_idx, group * kVerifyGroupSize, gsize, a.R, grid);
+#pragma unroll 1
+  for (int m = wave; m < a.R; m += kPackedWaves) {
+    const RowState t = merge_members(grid, gsize, m, lane);
+    if (lane == 0) {
+      const int64_t slot = static_cast<int64_t>(group) * a.R + m;
+      publish(a.gstate + slot * 3 + 0, t.mx);
+      publish(a.gstate + slot * 3 + 1, t.se);
+      publish(a.gstate + slot * 3 + 2, t.ab);
+      publish(a.gstate_idx + slot, t.ai);
+    }
+  }
+  const int groups = (a.G + kVerifyGroupSize - 1) / kVerifyGroupSize;
+  if (!arrive_last(a.counter, groups)) return;
+  gather_states(a.gstate, a.gstate_idx, 0, groups, a.R, grid);
+#pragma unroll 1
+  for (int m = wave; m < a.R; m += kPackedWaves) {
+    const RowState t = merge_members(grid, groups, m, lane);
+    if (lane == 0) {
+      const float own = a.own[m];
+      const bool in_nucleus = (t.ab / t.se) < a.p;
+      const bool is_max = (own >= t.mx) && (a.p > 0.f);
+      const bool valid_id = own == own;  // NaN marks a pending id outside [0, V)
+      a.accept[m] = (valid_id && (in_nucleus || is_max)) ? 1 : 0;
+      a.argmax[m] = t.ai;
+    }
+  }
+}
+
+template <int DT, int MT, int NF, int D>
+hipError_t launch_verify_packed(VerifyArgs a, int cu_count, hipStream_t stream, bool dry) {
+  if constexpr (!verify_packed_compiled<MT, NF, D>()) {
+    return hipErrorInvalidConfiguration;
+  } else {
+    if (dry) return hipSuccess;
+    auto main_kern = verify_packed_main_kernel<DT, MT, NF, D>;
+    constexpr size_t lds = packed_lds_body<MT, NF, 1>();
+    static int per_cu = 0;
+    if (per_cu == 0) {
+      per_cu = resident_per_cu(reinterpret_cast<const void*>(main_kern), 64 * kPackedWaves, lds);
+      if (per_cu < 1) return hipErrorInvalidConfiguration;
+    }
+    const int tiles = ((a.V + 15) / 16 + kPackedWaves * NF - 1) / (kPackedWaves * NF);
+    a.G = min(tiles, min(kMaxVerifyGroups, cu_count * per_cu));
+    hipLaunchKernelGGL((verify_packed_own_kernel<DT, 16>), dim3(a.R), dim3(64), 0, stream, a);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(main_kern, dim3(a.G), dim3(64 * kPackedWaves), lds, stream, a);
+    return hipGetLastError();
+  }
+}
+
+template <int DT, int MT, int NF>
+hipError_t verify_packed_pick_d(const VerifyArgs& a, int d, int cu, hipStream_t s, bool dry) {
+  if (d == 2) return launch_verify_packed<DT, MT, NF, 2>(a, cu, s, dry);
+  if (d == 4) return launch_verify_packed<DT, MT, NF, 4>(a, cu, s, dry);
+  if (d == 8) return launch_verify_packed<DT, MT, NF, 8>(a, cu, s, dry);
+  return hipErrorInvalidConfiguration;
+}
+
+template <int DT>
+hipError_t verify_packed_dispatch(const VerifyArgs& a, const plm_tile& t, int cu, hipStream_t s, bool dry) {
+  if (t.k_waves != 1 || t.split_k != 1) return hipErrorInvalidConfiguration;
+  const int mt = (a.R + 15) / 16;
+#define PLM_VERIFY_PACKED(MT_)                                                           \
+  if (mt == MT_) {                                                                       \
+    if (t.wave_frags == 2) return verify_packed_pick_d<DT, MT_, 2>(a, t.unroll, cu, s, dry); \
+    if (t.wave_frags == 4) return verify_packed_pick_d<DT, MT_, 4>(a, t.unroll, cu, s, dry); \
+  }
+  PLM_VERIFY_PACKED(1)
+  PLM_VERIFY_PACKED(2)
+  PLM_VERIFY_PACKED(3)
+  PLM_VERIFY_PACKED(4)
+#undef PLM_VERIFY_PACKED
+  return hipErrorInvalidConfiguration;
+}
+
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
-// Workspace layout: counter area (int kVerifyCounter used) | own[R] | state[kMaxVerifyGroups][R][3] |
-// state_idx[kMaxVerifyGroups][R]
-void verify_layout(int64_t R, size_t& own_off, size_t& state_off, size_t& idx_off, size_t& total) {
+// Workspace layout: counter area (ints kVerifyCounter and [kVerifyGroupBase, +groups) used) |
+// own[R] | state[kMaxVerifyGroups][R][3] | state_idx[kMaxVerifyGroups][R] | gstate[groups][R][3] |
+// gstate_idx[groups][R], groups = kMaxVerifyGroups / kVerifyGroupSize.
+constexpr int kMaxVerifyGroupSets = kMaxVerifyGroups / kVerifyGroupSize;
+static_assert(kVerifyGroupBase + kMaxVerifyGroupSets <= 64, "group counters fit before the streaming counters");
+void verify_layout(int64_t R, size_t& own_off, size_t& state_off, size_t& idx_off, size_t& gstate_off,
+                   size_t& gidx_off, size_t& total) {
   own_off = kCounterBytes;
   state_off = own_off + align256(static_cast<size_t>(R) * sizeof(float));
   idx_off = state_off + align256(static_cast<size_t>(kMaxVerifyGroups) * R * 3 * sizeof(float));
-  total = idx_off + align256(static_cast<size_t>(kMaxVerifyGroups) * R * sizeof(int));
+  gstate_off = idx_off + align256(static_cast<size_t>(kMaxVerifyGroups) * R * sizeof(int));
+  gidx_off = gstate_off + align256(static_cast<size_t>(kMaxVerifyGroupSets) * R * 3 * sizeof(float));
+  total = gidx_off + align256(static_cast<size_t>(kMaxVerifyGroupSets) * R * sizeof(int));
 }
 
 int device_cu_count() {
@@ -339,8 +719,8 @@ size_t plm_lm_head_verify_workspace_bytes(int64_t R, int64_t V, int64_t K, const
   (void)K;
   (void)tile;
   if (R < 1) return 0;
-  size_t own_off, state_off, idx_off, total;
-  plm::verify_layout(R, own_off, state_off, idx_off, total);
+  size_t own_off, state_off, idx_off, gstate_off, gidx_off, total;
+  plm::verify_layout(R, own_off, state_off, idx_off, gstate_off, gidx_off, total);
   return total;
 }
 
@@ -356,8 +736,8 @@ int plm_lm_head_verify(int32_t dtype, const void* x, int64_t ldx, const void* w,
   if (ldx < K || ldw < K || tile->split_k != 1 || tile->k_waves < 1) return PLM_ERR_ARGUMENT;
   if (R * ldx * 2 >= (int64_t(1) << 31) || 16 * tile->wave_frags * ldw * 2 >= (int64_t(1) << 31)) return PLM_ERR_ARGUMENT;
   if (ldx % 8 != 0 || ldw % 8 != 0 || !plm::aligned16_ptr(x) || !plm::aligned16_ptr(w)) return PLM_ERR_ALIGNMENT;
-  size_t own_off, state_off, idx_off, total;
-  plm::verify_layout(R, own_off, state_off, idx_off, total);
+  size_t own_off, state_off, idx_off, gstate_off, gidx_off, total;
+  plm::verify_layout(R, own_off, state_off, idx_off, gstate_off, gidx_off, total);
   if (workspace == nullptr || workspace_bytes < total || !plm::aligned16_ptr(workspace)) return PLM_ERR_WORKSPACE;
 
   plm::VerifyArgs a{};
@@ -378,6 +758,9 @@ int plm_lm_head_verify(int32_t dtype, const void* x, int64_t ldx, const void* w,
   a.own = reinterpret_cast<float*>(ws + own_off);
   a.state = reinterpret_cast<float*>(ws + state_off);
   a.state_idx = reinterpret_cast<int*>(ws + idx_off);
+  a.group_counter = reinterpret_cast<int*>(ws) + plm::kVerifyGroupBase;
+  a.gstate = reinterpret_cast<float*>(ws + gstate_off);
+  a.gstate_idx = reinterpret_cast<int*>(ws + gidx_off);
 
   const int cu = plm::device_cu_count();
   if (cu <= 0) return PLM_ERR_LAUNCH;
@@ -387,6 +770,59 @@ int plm_lm_head_verify(int32_t dtype, const void* x, int64_t ldx, const void* w,
   if (err != hipSuccess) return PLM_ERR_TILE;
   err = dtype == PLM_BF16 ? plm::verify_dispatch<plm::DT_BF16>(a, *tile, cu, s, false)
                           : plm::verify_dispatch<plm::DT_F16>(a, *tile, cu, s, false);
+  return err == hipSuccess ? PLM_OK : PLM_ERR_LAUNCH;
+}
+
+int plm_lm_head_verify_packed(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, int64_t R, int64_t V,
+                              int64_t K, const int64_t* pending, float p, int32_t round_mode, uint8_t* accept,
+                              int64_t* argmax, const plm_tile* tile, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  if (x == nullptr || packed_w == nullptr || pending == nullptr || accept == nullptr || argmax == nullptr ||
+      tile == nullptr)
+    return PLM_ERR_ARGUMENT;
+  if (dtype != PLM_BF16 && dtype != PLM_F16) return PLM_ERR_ARGUMENT;
+  if (round_mode < PLM_ROUND_F32 || round_mode > PLM_ROUND_F16) return PLM_ERR_ARGUMENT;
+  if (R < 1 || R > 64 || V < 1 || V > (int64_t(1) << 30) || K < 8 || K % 8 != 0 || K > (int64_t(1) << 24))
+    return PLM_ERR_ARGUMENT;
+  if (ldx < K || R * ldx * 2 >= (int64_t(1) << 31)) return PLM_ERR_ARGUMENT;
+  // 32-bit buffer offsets over the packed weight (with the last tile's padding rows).
+  const int64_t ks = (K + 31) / 32;
+  if (((V + 15) / 16 + 4 * tile->wave_frags) * ks * plm::kFragBytes >= (int64_t(1) << 31)) return PLM_ERR_ARGUMENT;
+  if (ldx % 8 != 0 || !plm::aligned16_ptr(x) || !plm::aligned16_ptr(packed_w)) return PLM_ERR_ALIGNMENT;
+  size_t own_off, state_off, idx_off, gstate_off, gidx_off, total;
+  plm::verify_layout(R, own_off, state_off, idx_off, gstate_off, gidx_off, total);
+  if (workspace == nullptr || workspace_bytes < total || !plm::aligned16_ptr(workspace)) return PLM_ERR_WORKSPACE;
+
+  plm::VerifyArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.w = static_cast<const uint16_t*>(packed_w);
+  a.ldx = ldx;
+  a.ldw = K;
+  a.R = static_cast<int>(R);
+  a.V = static_cast<int>(V);
+  a.K = static_cast<int>(K);
+  a.pending = pending;
+  a.p = p;
+  a.round_mode = round_mode;
+  a.accept = accept;
+  a.argmax = argmax;
+  char* ws = static_cast<char*>(workspace);
+  a.counter = reinterpret_cast<int*>(ws) + plm::kVerifyCounter;
+  a.own = reinterpret_cast<float*>(ws + own_off);
+  a.state = reinterpret_cast<float*>(ws + state_off);
+  a.state_idx = reinterpret_cast<int*>(ws + idx_off);
+  a.group_counter = reinterpret_cast<int*>(ws) + plm::kVerifyGroupBase;
+  a.gstate = reinterpret_cast<float*>(ws + gstate_off);
+  a.gstate_idx = reinterpret_cast<int*>(ws + gidx_off);
+
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t err = dtype == PLM_BF16 ? plm::verify_packed_dispatch<plm::DT_BF16>(a, *tile, 1, s, true)
+                                     : plm::verify_packed_dispatch<plm::DT_F16>(a, *tile, 1, s, true);
+  if (err != hipSuccess) return PLM_ERR_TILE;
+  const int cu = plm::device_cu_count();
+  if (cu <= 0) return PLM_ERR_LAUNCH;
+  err = dtype == PLM_BF16 ? plm::verify_packed_dispatch<plm::DT_BF16>(a, *tile, cu, s, false)
+                          : plm::verify_packed_dispatch<plm::DT_F16>(a, *tile, cu, s, false);
   return err == hipSuccess ? PLM_OK : PLM_ERR_LAUNCH;
 }
 

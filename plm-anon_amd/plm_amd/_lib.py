@@ -42,6 +42,7 @@ EXPORTS = (
     "plm_gemm_packed_resident_workgroups",
     "plm_lm_head_verify",
     "plm_lm_head_verify_workspace_bytes",
+    "plm_lm_head_verify_packed",
     "plm_status_string",
 )
 
@@ -108,6 +109,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.plm_lm_head_verify.argtypes = [c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, c_p, ctypes.c_float, c_i32,
                                        c_p, c_p, tile_p, c_p, c_sz, c_p]
     lib.plm_lm_head_verify.restype = ctypes.c_int
+    lib.plm_lm_head_verify_packed.argtypes = [c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_p, ctypes.c_float, c_i32,
+                                              c_p, c_p, tile_p, c_p, c_sz, c_p]
+    lib.plm_lm_head_verify_packed.restype = ctypes.c_int
     lib.plm_lm_head_verify_workspace_bytes.argtypes = [c_i64, c_i64, c_i64, tile_p]
     lib.plm_lm_head_verify_workspace_bytes.restype = c_sz
     lib.plm_status_string.argtypes = [c_i32]

@@ -66,6 +66,19 @@ def test_argument_validation_happens_before_launch():
                                   1 << 30, None) == -1
     assert lib.plm_lm_head_verify(0, fake, 2048, fake, 2048, 65, 50257, 2048, fake, 0.94, 0, fake, fake, vt, fake,
                                   1 << 30, None) == -1
+    # Packed verify: the same checks, K limits, and only row-split tiles without split-K.
+    pt = _lib.Tile(2, 1, 1, 2)
+    assert lib.plm_lm_head_verify_packed(0, fake, 2048, fake, 56, 50257, 2048, fake, 0.94, 9, fake, fake, pt, fake,
+                                         1 << 30, None) == -1
+    assert lib.plm_lm_head_verify_packed(0, fake, 2048, fake, 65, 50257, 2048, fake, 0.94, 0, fake, fake, pt, fake,
+                                         1 << 30, None) == -1
+    assert lib.plm_lm_head_verify_packed(0, fake, 2048, fake, 56, 50257, 2044, fake, 0.94, 0, fake, fake, pt, fake,
+                                         1 << 30, None) == -1
+    assert lib.plm_lm_head_verify_packed(0, fake, 2048, fake, 56, 50257, 2048, fake, 0.94, 0, fake, fake, pt, fake,
+                                         16, None) == -4
+    for bad in (_lib.Tile(2, 4, 1, 2), _lib.Tile(2, 1, 2, 2), _lib.Tile(1, 1, 1, 2), _lib.Tile(2, 1, 1, 6)):
+        assert lib.plm_lm_head_verify_packed(0, fake, 2048, fake, 56, 50257, 2048, fake, 0.94, 0, fake, fake, bad,
+                                             fake, 1 << 30, None) == -3
 
 
 def test_packed_argument_validation_happens_before_launch():

@@ -17,7 +17,7 @@ from conftest import golden_names, load_golden
 from oracle import plm_oracle as po
 from plm_amd import _lib, fast_gemm, workloads
 from plm_amd.fast_gemm import hip_linear_f32
-from plm_amd.verify import LOGITS_CONFIG, lm_head_verify
+from plm_amd.verify import LOGITS_CONFIG, ROWMAJOR_LOGITS_CONFIG, lm_head_verify
 
 pytestmark = pytest.mark.gpu
 
@@ -39,12 +39,13 @@ def _own_logits_from_workspace(R: int, device) -> torch.Tensor:
     return ws[base:base + 4 * R].view(torch.float32).cpu()
 
 
-def run_case(x, w, pending, p, mode, device, cfg=None, check_cpu=True):
-    acc, am = lm_head_verify(x, w, pending, p, mode, cfg)
+def run_case(x, w, pending, p, mode, device, cfg=None, check_cpu=True, packed=True):
+    acc, am = lm_head_verify(x, w, pending, p, mode, cfg, packed=packed)
     acc, am = acc.cpu(), am.cpu()
     # Read before the GEMM below reuses the workspace for its split-K partials.
     own = _own_logits_from_workspace(x.shape[0], device)
-    logits = _rounded(hip_linear_f32(x, w, LOGITS_CONFIG).cpu(), mode)
+    logits_cfg = LOGITS_CONFIG if packed else ROWMAJOR_LOGITS_CONFIG
+    logits = _rounded(hip_linear_f32(x, w, logits_cfg).cpu(), mode)
     # The own-logit pass reproduces the main pass's value for each proposal bit for bit.
     valid = (pending.cpu() >= 0) & (pending.cpu() < w.shape[0])
     rows = torch.arange(x.shape[0])[valid]
@@ -57,7 +58,7 @@ def run_case(x, w, pending, p, mode, device, cfg=None, check_cpu=True):
     assert torch.equal(acc, ref_acc), (acc != ref_acc).nonzero()
     if check_cpu:
         cpu = oracle.linear_fp32(x.cpu(), w.cpu())
-        torch.testing.assert_close(hip_linear_f32(x, w, LOGITS_CONFIG).cpu(), cpu, rtol=1e-3, atol=1e-4)
+        torch.testing.assert_close(hip_linear_f32(x, w, logits_cfg).cpu(), cpu, rtol=1e-3, atol=1e-4)
     return acc, am, logits
 
 
@@ -69,10 +70,11 @@ def _config5(device, dtype=torch.bfloat16, R=56, V=workloads.GPT2_VOCAB, K=2048)
     return x, w, pending
 
 
+@pytest.mark.parametrize("packed", [True, False], ids=["packed", "rowmajor"])
 @pytest.mark.parametrize("mode", ["fp32", "bf16"])
-def test_config5_fused_verify(device, mode):
+def test_config5_fused_verify(device, mode, packed):
     x, w, pending = _config5(device)
-    acc, am, logits = run_case(x, w, pending, P, mode, device)
+    acc, am, logits = run_case(x, w, pending, P, mode, device, packed=packed)
     # Against the oracle on CPU-computed logits, away from rounding-sensitive rows.
     cpu_logits = _rounded(oracle.linear_fp32(x.cpu(), w.cpu()), mode)
     ref_acc, ref_am = oracle.verify(cpu_logits, pending.cpu(), P)
@@ -92,18 +94,30 @@ def test_fp16_model_dtype(device):
     run_case(x, w, pending, P, "fp16", device)
 
 
+@pytest.mark.parametrize("packed", [True, False], ids=["packed", "rowmajor"])
 @pytest.mark.parametrize("R", [1, 7, 14, 28, 42, 64])
-def test_round_widths(device, R):
+def test_round_widths(device, R, packed):
     x, w, pending = _config5(device, R=R, V=5003)
-    run_case(x, w, pending, P, "fp32", device)
+    run_case(x, w, pending, P, "fp32", device, packed=packed)
+
+
+@pytest.mark.parametrize("cfg", [{"wave_frags": 4, "k_waves": 1, "split_k": 1, "unroll": 2},
+                                 {"wave_frags": 4, "k_waves": 1, "split_k": 1, "unroll": 8},
+                                 {"wave_frags": 2, "k_waves": 1, "split_k": 1, "unroll": 4}],
+                         ids=lambda c: f"nf{c['wave_frags']}d{c['unroll']}")
+def test_other_tiles(device, cfg):
+    # K not a multiple of 32 and a vocabulary that ends inside a tile.
+    x, w, pending = _config5(device, R=56, V=12345, K=1000)
+    run_case(x, w, pending, 0.5, "fp32", device, cfg)
 
 
 @pytest.mark.parametrize("cfg", [{"wave_frags": 4, "k_waves": 4, "split_k": 1, "unroll": 2},
                                  {"wave_frags": 4, "k_waves": 4, "split_k": 1, "unroll": 4},
-                                 {"wave_frags": 2, "k_waves": 4, "split_k": 1, "unroll": 2}])
-def test_other_tiles(device, cfg):
+                                 {"wave_frags": 2, "k_waves": 4, "split_k": 1, "unroll": 2}],
+                         ids=lambda c: f"nf{c['wave_frags']}d{c['unroll']}")
+def test_other_tiles_rowmajor(device, cfg):
     x, w, pending = _config5(device, R=56, V=12345, K=1024)
-    run_case(x, w, pending, 0.5, "fp32", device, cfg)
+    run_case(x, w, pending, 0.5, "fp32", device, cfg, packed=False)
 
 
 def test_proposals_at_the_argmax_and_exact_mode(device):
@@ -171,8 +185,9 @@ def test_graph_capture(device):
         torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("packed", [True, False], ids=["packed", "rowmajor"])
 @pytest.mark.parametrize("name", golden_names("verify_"))
-def test_golden_fixture(device, name):
+def test_golden_fixture(device, name, packed):
     """The committed fp64 fixture: accept bits and argmax ids on every row the fixture marks as
     clear of rounding-sensitive boundaries."""
     import numpy as np
@@ -180,7 +195,7 @@ def test_golden_fixture(device, name):
     z = load_golden(name)
     x, w = z["x"].to(device), z["w"].to(device)
     pending = torch.from_numpy(z["pending"]).to(device)
-    acc, am = lm_head_verify(x, w, pending, float(z["p"]), "fp32")
+    acc, am = lm_head_verify(x, w, pending, float(z["p"]), "fp32", packed=packed)
     acc, am = acc.cpu().numpy(), am.cpu().numpy()
     sa, sm = z["safe_accept"], z["safe_argmax"]
     assert np.array_equal(acc[sa], z["accept"][sa])
