@@ -400,17 +400,31 @@ __device__ __forceinline__ void gather_states(const float* st, const int* st_idx
   __syncthreads();
 }
 
-// Row m's state merged over members 0..count-1 of grid (lane i holds member i; a 32-lane
-// butterfly in a fixed order), valid in lanes 0..31.
-__device__ __forceinline__ RowState merge_members(const f32x4* grid, int count, int m, int lane) {
+// Every row's state merged over members 0..count-1 of grid: lane = row; wavefront w merges
+// members [8w, 8w+8) in order, then wavefront 0 merges the four partial states in wavefront order
+// (through the part_* LDS arrays). The result is valid in wavefront 0, lanes < R.
+__device__ __forceinline__ RowState merge_rows(const f32x4* grid, int count, int wave, int lane,
+                                               float (*part_mx)[64], float (*part_se)[64], float (*part_ab)[64],
+                                               int (*part_ai)[64]) {
+  constexpr int kPerWave = kVerifyGroupSize / kPackedWaves;
   RowState s = empty_state();
-  if (lane < count) {
-    const f32x4 g = grid[lane * 64 + m];
-    const float idx_bits = g[3];  // (a bit cast applied to the vector element itself read element 0)
-    s = RowState{g[0], g[1], g[2], __builtin_bit_cast(int, idx_bits)};
-  }
+  const int end = min(count, (wave + 1) * kPerWave);
 #pragma unroll 1
-  for (int off = kVerifyGroupSize / 2; off >= 1; off >>= 1) s = merge(s, shfl_xor_state(s, off));
+  for (int i = wave * kPerWave; i < end; ++i) {
+    const f32x4 g = grid[i * 64 + lane];
+    const float idx_bits = g[3];  // (a bit cast applied to the vector element itself read element 0)
+    s = merge(s, RowState{g[0], g[1], g[2], __builtin_bit_cast(int, idx_bits)});
+  }
+  part_mx[wave][lane] = s.mx;
+  part_se[wave][lane] = s.se;
+  part_ab[wave][lane] = s.ab;
+  part_ai[wave][lane] = s.ai;
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll 1
+    for (int w = 1; w < kPackedWaves; ++w)
+      s = merge(s, RowState{part_mx[w][lane], part_se[w][lane], part_ab[w][lane], part_ai[w][lane]});
+  }
   return s;
 }
 
@@ -599,16 +613,15 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D
   }
   // Two-level merge: the last workgroup of each group of kVerifyGroupSize merges the group's
   // states, the last group to finish merges the group states. Each level is one batch of
-  // device-coherent loads per lane (lane l holds member l of the group) and a butterfly.
+  // device-coherent loads into LDS and a fixed-order merge with one lane per row.
   const int group = blockIdx.x / kVerifyGroupSize;
   const int gsize = min(kVerifyGroupSize, a.G - group * kVerifyGroupSize);
   if (!arrive_last(a.group_counter + group, gsize)) return;
   gather_states(a.state, a.state_idx, group * kVerifyGroupSize, gsize, a.R, grid);
-#pragma unroll 1
-  for (int m = wave; m < a.R; m += kPackedWaves) {
-    const RowState t = merge_members(grid, gsize, m, lane);
-    if (lane == 0) {
-      const int64_t slot = static_cast<int64_t>(group) * a.R + m;
+  {
+    const RowState t = merge_rows(grid, gsize, wave, lane, st_mx, st_se, st_ab, st_ai);
+    if (wave == 0 && lane < a.R) {
+      const int64_t slot = static_cast<int64_t>(group) * a.R + lane;
       publish(a.gstate + slot * 3 + 0, t.mx);
       publish(a.gstate + slot * 3 + 1, t.se);
       publish(a.gstate + slot * 3 + 2, t.ab);
@@ -618,17 +631,15 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D
   const int groups = (a.G + kVerifyGroupSize - 1) / kVerifyGroupSize;
   if (!arrive_last(a.counter, groups)) return;
   gather_states(a.gstate, a.gstate_idx, 0, groups, a.R, grid);
-#pragma unroll 1
-  for (int m = wave; m < a.R; m += kPackedWaves) {
-    const RowState t = merge_members(grid, groups, m, lane);
-    if (lane == 0) {
-      const float own = a.own[m];
-      const bool in_nucleus = (t.ab / t.se) < a.p;
-      const bool is_max = (own >= t.mx) && (a.p > 0.f);
-      const bool valid_id = own == own;  // NaN marks a pending id outside [0, V)
-      a.accept[m] = (valid_id && (in_nucleus || is_max)) ? 1 : 0;
-      a.argmax[m] = t.ai;
-    }
+  const RowState t = merge_rows(grid, groups, wave, lane, st_mx, st_se, st_ab, st_ai);
+  if (wave == 0 && lane < a.R) {
+    const int m = lane;
+    const float own = a.own[m];
+    const bool in_nucleus = (t.ab / t.se) < a.p;
+    const bool is_max = (own >= t.mx) && (a.p > 0.f);
+    const bool valid_id = own == own;  // NaN marks a pending id outside [0, V)
+    a.accept[m] = (valid_id && (in_nucleus || is_max)) ? 1 : 0;
+    a.argmax[m] = t.ai;
   }
 }
 

@@ -62,13 +62,15 @@ def lm_head_verify(x: torch.Tensor, w: torch.Tensor, pending: torch.Tensor, p: f
     x = x if (x.stride(1) == 1 and x.stride(0) % 8 == 0) else x.contiguous()
     w = w if (w.stride(1) == 1 and w.stride(0) % 8 == 0) else w.contiguous()
     pending = pending.contiguous()
-    accept_u8 = torch.empty(R, dtype=torch.uint8, device=x.device)
+    # The kernel writes one byte 0/1 per row: a bool tensor's storage directly.
+    direct = accept is not None and accept.dtype == torch.bool and accept.is_contiguous() and accept.shape == (R,)
+    accept_out = accept if direct else torch.empty(R, dtype=torch.bool, device=x.device)
     if argmax is None:
         argmax = torch.empty(R, dtype=torch.int64, device=x.device)
     lib = _lib.lib()
     need = int(lib.plm_lm_head_verify_workspace_bytes(R, V, K, tile))
     ws = workspace(x.device, need)
-    common = (pending.data_ptr(), float(p), ROUND_MODES[round_to], accept_u8.data_ptr(), argmax.data_ptr(), tile,
+    common = (pending.data_ptr(), float(p), ROUND_MODES[round_to], accept_out.data_ptr(), argmax.data_ptr(), tile,
               ws.data_ptr(), ws.numel(), _lib.stream_handle(x.device))
     if packed:
         status = lib.plm_lm_head_verify_packed(_lib.DTYPE_CODES[x.dtype], x.data_ptr(), x.stride(0),
@@ -78,8 +80,7 @@ def lm_head_verify(x: torch.Tensor, w: torch.Tensor, pending: torch.Tensor, p: f
         status = lib.plm_lm_head_verify(_lib.DTYPE_CODES[x.dtype], x.data_ptr(), x.stride(0), w.data_ptr(),
                                         w.stride(0), R, V, K, *common)
         _lib.check(status, f"plm_lm_head_verify(R={R}, V={V}, K={K}, cfg={cfg})")
-    out = accept_u8.bool()
-    if accept is not None:
-        accept.copy_(out)
-        out = accept
-    return out, argmax
+    if accept is not None and not direct:
+        accept.copy_(accept_out)
+        return accept, argmax
+    return accept_out, argmax
