@@ -153,19 +153,36 @@ int packed_entry(int32_t dtype, const void* x, int64_t ldx, const void* wp, void
                             static_cast<hipStream_t>(stream));
 }
 
-// Derived fields of a packed chain; returns the workspace bytes or a negative status. Split
-// arrival counters and partials are reused after every grid barrier (all of the previous
-// linears are complete there); barrier counters are one per consumed linear.
+// How the linears of a chain wait for the ones they read: 0 (none reads another), 2 (every linear
+// after the first reads the one before it, and none has more tiles than a parity set of tile
+// flags holds: per-wavefront waits on the producer's tile-done flags), or 1 (otherwise: a grid
+// barrier after every linear that is read).
+int packed_chain_mode(const plm_chain_gemm* g, int32_t count, const plm_tile& t) {
+  bool any = false, pure = count > 1;
+  for (int32_t i = 0; i < count; ++i) {
+    any = any || g[i].dep >= 0;
+    if (i > 0 && g[i].dep != i - 1) pure = false;
+    if (packed_tiles(g[i].N, t) > kPkTileFlags) pure = false;
+  }
+  return pure ? 2 : (any ? 1 : 0);
+}
+
+// Derived fields of a packed chain; returns the workspace bytes or a negative status. Consumed
+// linears are numbered 1, 2, ... (done_base): the progress-flag value (grid-barrier mode) or the
+// tile-flag value and parity set (tile-flag mode). Grid-barrier mode reuses the split arrival
+// counters and partials after every barrier (all earlier linears are finished there); tile-flag
+// mode has no point where every workgroup is past a linear, so each linear gets its own.
 int64_t packed_prepare(plm_chain_gemm* g, int32_t count, int64_t M, const plm_tile& t) {
   for (int32_t i = 0; i < count; ++i) g[i].consumed = 0;
   for (int32_t i = 0; i < count; ++i) {
     if (g[i].dep < -1 || g[i].dep >= i) return PLM_ERR_ARGUMENT;
     if (g[i].dep >= 0) g[g[i].dep].consumed = 1;
+    if (g[i].N < 1 || g[i].split_k < 1 || g[i].split_k > 64) return PLM_ERR_ARGUMENT;
   }
+  const int mode = packed_chain_mode(g, count, t);
   const int64_t mt = (M + 15) / 16;
   int64_t arrive = kPackedArriveBase, seq = 0, partial = 0, most_partial = 0;
   for (int32_t i = 0; i < count; ++i) {
-    if (g[i].N < 1 || g[i].split_k < 1 || g[i].split_k > 64) return PLM_ERR_ARGUMENT;
     plm_tile ti = t;
     ti.split_k = g[i].split_k;
     const int64_t tiles = packed_tiles(g[i].N, ti);
@@ -183,10 +200,12 @@ int64_t packed_prepare(plm_chain_gemm* g, int32_t count, int64_t M, const plm_ti
       if (arrive > kPackedBarrierBase) return PLM_ERR_ARGUMENT;
     }
     if (g[i].consumed) {
-      g[i].done_base = static_cast<int32_t>(++seq);  // progress-flag value once this Y is written
+      g[i].done_base = static_cast<int32_t>(++seq);
       if (seq >= (1 << 16)) return PLM_ERR_ARGUMENT;
-      arrive = kPackedArriveBase;  // everything before the barrier is finished
-      partial = 0;
+      if (mode == 1) {
+        arrive = kPackedArriveBase;  // everything before the barrier is finished
+        partial = 0;
+      }
     }
   }
   return static_cast<int64_t>(kCounterBytes) + most_partial * 4;
@@ -316,7 +335,7 @@ int plm_gemm_chain_packed(int32_t dtype, const plm_chain_gemm* host_gemms, const
   a.count = count;
   a.M = static_cast<int>(M);
   a.G = static_cast<int>(most_items);
-  a.sync = sync ? 1 : 0;
+  a.sync = sync ? plm::packed_chain_mode(host_gemms, count, *tile) : 0;
   const int64_t needed = (sync || any_split) ? need : 0;
   return plm::packed_launch_args(dtype, a, *tile, workspace, workspace_bytes, needed,
                                  static_cast<hipStream_t>(stream));

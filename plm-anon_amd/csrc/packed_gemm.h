@@ -59,6 +59,12 @@ constexpr int kXTileBytes = 16 * 80;       // LDS transpose tile of one X fragme
 constexpr int kPkErrorSlot = 2;      // 1 once a bounded wait gave up
 constexpr int kPkEpochSlot = 10;     // int64 at ints 10-11: packed chained launches completed
 constexpr int kPkMaxWorkgroups = 2048;  // progress flags: int64 per workgroup at kPackedBarrierBase
+// Tile-flag mode uses the same 2048 int64 as two parity sets of tile-done flags: consumed linear
+// number q (1, 2, ...) raises flag (q & 1) * kPkTileFlags + tile to ((epoch + 1) << 16) + q once
+// the tile's Y is written. In a chain where every linear reads the one before it, a set is only
+// rewritten (by linear q + 2) after every tile of linear q that a later linear reads is done,
+// and values only grow, so no flag needs clearing.
+constexpr int kPkTileFlags = 1024;
 
 struct PackedArgs {
   const plm_chain_gemm* chain;  // device array of `count` linears, or nullptr: use `single`
@@ -66,7 +72,9 @@ struct PackedArgs {
   int count;
   int M;
   int G;           // workgroups in the grid
-  int sync;        // some linear reads an earlier one's output (progress flags, epoch)
+  int sync;        // 0: no linear reads another's output; 1: grid barriers after such linears
+                   // (progress flags); 2: tile flags (every linear after the first reads the one
+                   // before it: each wavefront waits only for the producer tiles it reads)
   int spin_limit;  // polls before a wait gives up
   int* counters;
   float* partial;
@@ -92,8 +100,10 @@ struct PLinear {
   int N, Ks, k_last, split, tiles, items;  // tiles of 16*NF (KW = 4) or 64*NF (KW = 1) rows
   int out_f32, consumed;
   int* arrive;     // split arrival counters, one per tile
-  int seq;         // consumed linears up to and including this one (progress flag value)
+  int seq;         // consumed linears up to and including this one
   float* partial;  // split partials
+  int64_t* flag;   // sync == 2 and consumed: this linear's tile-done flags (else nullptr)
+  int64_t flag_value;  // the value they get: ((epoch + 1) << 16) + seq
 };
 
 // Wavefronts per workgroup: KW for the K-split layouts, four for the row-split one.
@@ -117,7 +127,7 @@ __device__ __forceinline__ T const_load(const T* p) {
 
 // A linear's descriptor: a chain's from its table, a single linear's from the kernel arguments.
 template <int NF, int KW>
-__device__ __forceinline__ PLinear load_linear(const PackedArgs& a, int gi) {
+__device__ __forceinline__ PLinear load_linear(const PackedArgs& a, int gi, int64_t epoch = 0) {
   plm_chain_gemm g = a.single;
   if (a.chain != nullptr) {
     const plm_chain_gemm* c = a.chain + gi;
@@ -153,7 +163,23 @@ __device__ __forceinline__ PLinear load_linear(const PackedArgs& a, int gi) {
   L.arrive = a.counters + sgpr(g.arrive_base);
   L.seq = sgpr(g.done_base);
   L.partial = a.partial + sgpr64(g.partial_offset);
+  L.flag = (a.sync == 2 && L.consumed)
+               ? reinterpret_cast<int64_t*>(a.counters + kPackedBarrierBase) + (L.seq & 1) * kPkTileFlags
+               : nullptr;
+  L.flag_value = ((epoch + 1) << 16) + L.seq;
   return L;
+}
+
+// sync == 2: raises the tile-done flag of `tile` once every wavefront's stores of it have
+// completed (device-coherent Y stores: visible to every workgroup once complete). An atomic
+// maximum: a tile of linear q that no later linear reads may finish after linear q + 2 has
+// raised the same flag, and must not lower it.
+__device__ __forceinline__ void publish_tile(const PLinear& L, int tile) {
+  if (L.flag == nullptr) return;
+  __builtin_amdgcn_s_waitcnt(0);
+  asm volatile("s_barrier" ::: "memory");
+  if (threadIdx.x == 0)
+    __hip_atomic_fetch_max(L.flag + tile, L.flag_value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // K-step range [b, e) of split s: wavefront w's share of it (K-split layouts: 1/KW) or all of it
@@ -356,6 +382,7 @@ __device__ __forceinline__ void packed_finish(const PLinear& L, int M, int item,
       const int q = wave + KW * i;
       if (q < Q) packed_store_frag<DT, MT>(L, M, n0, q, lane, sum[i]);
     }
+    publish_tile(L, tile);
     return;
   }
   // Split partial: one KiB block per fragment (an fp32 fragment is 64 lanes x 16 bytes), written
@@ -400,6 +427,7 @@ __device__ __forceinline__ void packed_finish(const PLinear& L, int M, int item,
       packed_store_frag<DT, MT>(L, M, n0, q, lane, v);
     }
   }
+  publish_tile(L, tile);
 }
 
 // End of an item for a row-split workgroup (KW = 1): each wavefront owns its NF fragments of the
@@ -418,6 +446,7 @@ __device__ __forceinline__ void packed_finish_rows(const PLinear& L, int M, int 
     for (int f = 0; f < NF; ++f)
 #pragma unroll
       for (int t = 0; t < MT; ++t) packed_store_frag<DT, MT>(L, M, n0, f * MT + t, lane, acc[f][t]);
+    publish_tile(L, tile);
     return;
   }
   const uint32_t tile_bytes = static_cast<uint32_t>(L.split) * Q * kFragBytes;
@@ -461,6 +490,7 @@ __device__ __forceinline__ void packed_finish_rows(const PLinear& L, int M, int 
     }
     packed_store_frag<DT, MT>(L, M, n0, qw, lane, v);
   }
+  publish_tile(L, tile);
 }
 
 extern __shared__ __attribute__((aligned(16))) f32x4 packed_lds[];
@@ -530,6 +560,48 @@ __device__ __forceinline__ void warm_weights(const PLinear& Ln, int G, int wave,
   (void)lane;
 }
 
+// sync == 2: waits until every tile of the producer linear P that this wavefront's items of L
+// read has raised its flag (bounded; error flag on timeout). The range covers every 128-byte
+// line the X loads touch, not only the columns they use: a line holding a column of an
+// unfinished neighbour tile would otherwise enter this XCD's L2 with that column's old value and
+// be served later to a wavefront that waited for the neighbour.
+template <int NF, int KW>
+__device__ __forceinline__ void wait_producer_tiles(const PackedArgs& a, const PLinear& L, const PLinear& P, int wave,
+                                                    int lane) {
+  int lo = L.Ks, hi = 0;
+  for (int item = blockIdx.x; item < L.items; item += a.G) {
+    int tile, s, b, e;
+    item_tile(item, L.split, tile, s);
+    packed_range<KW>(L.Ks, s, L.split, wave, b, e);
+    if (b < e) {
+      lo = min(lo, b);
+      hi = max(hi, e);
+    }
+  }
+  if (lo >= hi) return;
+  constexpr int kCols = 16 * tile_frags<NF, KW>();  // Y columns of one producer tile
+  constexpr int kLineCols = 64;                      // bf16 columns of a 128-byte line
+  const int t0 = max(32 * lo - (kLineCols - 1), 0) / kCols;
+  const int t1 = min((32 * hi - 1 + (kLineCols - 1)) / kCols, P.tiles - 1);
+  const auto frs = make_rsrc(P.flag, static_cast<uint32_t>(P.tiles) * 8u);
+  for (int i = 0;; ++i) {
+    bool done = true;
+    for (int b = t0; b <= t1; b += 64) {
+      const int t = b + lane;
+      const u32x2 v = __builtin_bit_cast(
+          u32x2, __builtin_amdgcn_raw_buffer_load_b64(frs, t <= t1 ? static_cast<uint32_t>(t) * 8u : kOutOfRange, 0, kCoherent));
+      const int64_t f = static_cast<int64_t>((static_cast<uint64_t>(v.y) << 32) | v.x);
+      done = done && (t > t1 || f >= P.flag_value);
+    }
+    if (__all(done)) break;
+    if (i >= a.spin_limit) {
+      if (lane == 0) publish(a.counters + kPkErrorSlot, 1);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
 // Advances the packed-chain epoch after a chained launch (the next launch's flags then exceed
 // every flag of this one).
 template <int kUnused = 0>  // a template, so that every translation unit may instantiate it
@@ -596,7 +668,7 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
   // grid barrier): then only X is still to be loaded for them.
   bool w_ready = false;
   for (int gi = 0; gi < a.count; ++gi) {
-    const PLinear L = load_linear<NF, KW>(a, gi);
+    const PLinear L = load_linear<NF, KW>(a, gi, epoch);
     POffsets<MT, NF, XN> o;
     packed_offsets<MT, NF, KW>(L, a.M, lane, wave, o);
     const auto wr = make_rsrc(L.wp, static_cast<uint32_t>((L.N + 15) >> 4) * L.Ks * kFragBytes);
@@ -605,7 +677,25 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
     pc_enter<NF, D, KW>(L, wave, ld);
     PCursor cp = ld;
     if (ld.item < L.items) {
-      if (!w_ready) {
+      if (a.sync == 2 && gi > 0) {
+        // The first weight stages and more of the weights into the caches, which do not depend
+        // on the producer; then the wait for the producer tiles this wavefront reads; then X.
+        PCursor lw = ld;
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+          issue_w<NF>(wr, lw, L.items, o.wo, wb[j]);
+          pc_advance<NF, D, KW>(L, a.G, wave, lw);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        warm_weights<NF, D, KW>(L, a.G, wave, lane, lw, wr, o.wo, sink);
+        wait_producer_tiles<NF, KW>(a, L, load_linear<NF, KW>(a, gi - 1, epoch), wave, lane);
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+          issue_x<MT, NF, XN>(xr, ld, L.items, L.Ks, o, xb[j]);
+          pc_advance<NF, D, KW>(L, a.G, wave, ld);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else if (!w_ready) {
 #pragma unroll
         for (int j = 0; j < D; ++j) {
           issue_w<NF>(wr, ld, L.items, o.wo, wb[j]);
@@ -668,7 +758,7 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
       }
     }
     w_ready = false;
-    if (L.consumed && gi + 1 < a.count) {
+    if (a.sync == 1 && L.consumed && gi + 1 < a.count) {
       // Arrive, request the next linear's first weight stages into registers and more of its
       // weights into the caches (weights never depend on the barrier), then wait for every
       // workgroup's part of this Y.

@@ -116,8 +116,9 @@ def test_packed_sizes_and_chain_prepare():
     tiles_ = math.ceil(2048 / 16 / 2)
     assert lib.plm_gemm_packed_workspace_bytes(56, 2048, 8192, _lib.Tile(2, 4, 4, 2)) == \
         _lib.COUNTER_BYTES + tiles_ * 4 * 2 * 4 * 1024
-    # Chain: progress-flag values count the consumed linears; partials and arrival counters are
-    # reused after each of them.
+    # Chains number the consumed linears. Where every linear reads the one before it (tile-done
+    # flags, no grid barrier), every linear has its own partials and arrival counters.
+    per_linear = 64 * 2 * 2 * 4 * 1024   # tiles x split x fragments x MT x 1 KiB
     arr = (_lib.ChainGemm * 3)()
     for i, g in enumerate(arr):
         g.x, g.w, g.y, g.ldx, g.ldw, g.ldy = 1 << 20, 1 << 21, (1 << 22) + i * (1 << 20), 2048, 2048, 2048
@@ -125,8 +126,19 @@ def test_packed_sizes_and_chain_prepare():
     need = lib.plm_gemm_chain_packed_prepare(arr, 3, 56, _lib.Tile(2, 4, 1, 2))
     assert [g.consumed for g in arr] == [1, 1, 0]
     assert [g.done_base for g in arr] == [1, 2, 0]
-    assert len({g.arrive_base for g in arr}) == 1 and all(g.partial_offset == 0 for g in arr)
-    assert need == _lib.COUNTER_BYTES + 64 * 2 * 2 * 4 * 1024
+    assert [g.arrive_base for g in arr] == [49152, 49152 + 64, 49152 + 128]
+    assert [g.partial_offset for g in arr] == [0, per_linear // 4, 2 * per_linear // 4]
+    assert need == _lib.COUNTER_BYTES + 3 * per_linear
+    # Otherwise (here two linears read the first) a grid barrier follows every consumed linear,
+    # and partials and arrival counters are reused after it.
+    for i, g in enumerate(arr):
+        g.dep = [-1, 0, 0][i]
+    need = lib.plm_gemm_chain_packed_prepare(arr, 3, 56, _lib.Tile(2, 4, 1, 2))
+    assert [g.consumed for g in arr] == [1, 0, 0]
+    assert [g.done_base for g in arr] == [1, 0, 0]
+    assert [g.arrive_base for g in arr] == [49152, 49152, 49152 + 64]
+    assert [g.partial_offset for g in arr] == [0, 0, per_linear // 4]
+    assert need == _lib.COUNTER_BYTES + 2 * per_linear
 
 
 def test_workspace_sizes():
