@@ -46,10 +46,11 @@ def parse_args():
     ap.add_argument("--no-sweep", action="store_true", help="skip the partial-round M sweep")
     ap.add_argument("--no-verify", action="store_true", help="skip the fused LM-head verify timing")
     ap.add_argument("--only-round", action="store_true", help="time the round only (for profiling runs)")
-    ap.add_argument("--profile", choices=("eager", "copy"),
+    ap.add_argument("--profile", choices=("eager", "copy", "verify"),
                     help="no JSON: 'eager' launches the round and the fused verify step --steps times without a "
                          "graph (for rocprofv3 counter runs); 'copy' runs a 1 GiB device copy, the reference "
-                         "kernel that scales the HBM byte counters")
+                         "kernel that scales the HBM byte counters; 'verify' runs the fused verify step and the "
+                         "LM-head GEMM --steps times each over six LM-head copies (for kernel traces)")
     return ap.parse_args()
 
 
@@ -249,6 +250,9 @@ def main():
         torch.cuda.synchronize()
         print(f"[bench] copied 1 GiB x {max(1, args.steps)}", file=sys.stderr)
         return
+    if args.profile == "verify":
+        profile_verify(args, device)
+        return
     tables = gemm_tables.read_table(args.hidden)
     gemms = [g for _ in range(args.layers) for g in gpt_block(args.hidden, args.mlp)]
     gemms.append(type(gemms[0])("lm_head", GPT2_VOCAB, args.hidden))
@@ -366,6 +370,29 @@ def main():
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_baseline(args.hidden, args.mlp, args.M, args.cpu_seconds)
     print(json.dumps(result), flush=True)
+
+
+def profile_verify(args, device):
+    """The fused verify step and the LM-head GEMM (its tuned tile), eager, rotating over six
+    LM-head copies (1.2 GB: no call finds its weight in the Infinity Cache)."""
+    import torch
+
+    from plm_amd import gemm_tables
+    from plm_amd.fast_gemm import hip_linear
+    from plm_amd.verify import lm_head_verify
+    from plm_amd.workloads import GPT2_VOCAB, TOP_P, proposals
+
+    gen = torch.Generator(device=device).manual_seed(5000)
+    x = torch.randn(args.M, args.hidden, generator=gen, device=device).bfloat16()
+    copies = [(0.02 * torch.randn(GPT2_VOCAB, args.hidden, generator=gen, device=device)).bfloat16() for _ in range(6)]
+    pending = proposals(args.M).to(device)
+    cfg = gemm_tables.read_table(args.hidden)[(args.M, GPT2_VOCAB, args.hidden)]
+    for i in range(max(1, args.steps)):
+        lm_head_verify(x, copies[i % 6], pending, TOP_P)
+    for i in range(max(1, args.steps)):
+        hip_linear(x, copies[i % 6], cfg)
+    torch.cuda.synchronize()
+    print(f"[bench] verify x {max(1, args.steps)}, LM-head GEMM {cfg} x {max(1, args.steps)}", file=sys.stderr)
 
 
 def time_verify(w_lm, hidden, device, steps):
