@@ -419,9 +419,28 @@ def time_verify(w_lm, hidden, device, steps):
             lm_head_verify(x, w, pending, TOP_P, accept=acc, argmax=am)
     ms = time_graph(graph, max(5, steps // 2), 2) / len(copies)
     nbytes = 2 * (w_lm.shape[0] * hidden + 56 * hidden) + 56 * (8 + 8 + 1)
+    del graph
+    # The round's whole LM-head end (k = 7): proposals into the verify rows, the fused verify, and the
+    # epilogue's state update (plm/decoder.py:351-365), as one graph per round.
+    from plm_amd.verify import RoundVerify
+
+    k = 7
+    rv = RoundVerify(k, "nucleus", TOP_P, "bf16", device)
+    verify_tokens = proposals(k).to(device)
+    state = [pending[: k - 1].clone(), torch.zeros(1, dtype=torch.int64, device=device),
+             torch.full((1 << 17,), -1, dtype=torch.int64, device=device),
+             torch.zeros((), dtype=torch.int64, device=device), torch.zeros((), dtype=torch.int64, device=device)]
+    for w in copies:
+        rv(x, w, verify_tokens, *state)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for w in copies:
+            rv(x, w, verify_tokens, *state)
+    ms_round = time_graph(graph, max(5, steps // 2), 2) / len(copies)
     del graph, copies
     return {"us": round(ms * 1000.0, 2), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
-            "bytes": nbytes, "accepted": int(acc.sum().item())}
+            "bytes": nbytes, "accepted": int(acc.sum().item()), "round_us": round(ms_round * 1000.0, 2)}
 
 
 if __name__ == "__main__":

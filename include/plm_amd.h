@@ -28,6 +28,11 @@ enum plm_dtype { PLM_BF16 = 0, PLM_F16 = 1 };
  * accumulator, plm/decoder.py:73 upcasts it again). */
 enum plm_round_mode { PLM_ROUND_F32 = 0, PLM_ROUND_BF16 = 1, PLM_ROUND_F16 = 2 };
 
+/* Acceptance rule of the verify step (RoundDecoder's accept_rule, plm/decoder.py:88-89, 353):
+ * PLM_RULE_NUCLEUS is nucleus_acceptance (plm/decoder.py:71-75) with threshold = top-p;
+ * PLM_RULE_FLOOR is floor_acceptance (plm/decoder.py:78-82) with threshold = epsilon. */
+enum plm_accept_rule { PLM_RULE_NUCLEUS = 0, PLM_RULE_FLOOR = 1 };
+
 /* Every workspace starts with this many bytes of integer arrival counters, which must be zero
  * before the first call and which every kernel leaves zero; the rest of a workspace is scratch
  * that needs no initialisation. One workspace may therefore serve every entry point in turn on
@@ -196,15 +201,19 @@ int plm_gemm_tile_supported(int32_t dtype, int64_t M, int64_t K, const plm_tile*
 /*
  * Fused LM-head verify step: logits[R,V] = X[R,K] · W[V,K]^T are formed tile by tile and never
  * written to memory. For every row r:
- *   accept[r] = nucleus membership of pending[r] at top-p `p`, as nucleus_acceptance
- *               (plm/decoder.py:71-75): mass strictly above the proposal's own probability < p,
- *               or the proposal is the row maximum and p > 0; p <= 0 accepts nothing.
+ *   accept[r] = the acceptance rule's decision for pending[r] (enum plm_accept_rule):
+ *               PLM_RULE_NUCLEUS, as nucleus_acceptance (plm/decoder.py:71-75): mass strictly
+ *               above the proposal's own probability < p, or the proposal is the row maximum and
+ *               p > 0; p <= 0 accepts nothing (exact matching, plm/decoder.py:115).
+ *               PLM_RULE_FLOOR, as floor_acceptance (plm/decoder.py:78-82): logit[pending[r]] -
+ *               logsumexp(logits[r]) > log(p), with p = epsilon.
+ *               An id outside [0, V) is never accepted.
  *   argmax[r] = index of the row maximum, lowest index on ties (plm/decoder.py:362).
  * `round_mode` (enum plm_round_mode) fixes the logits the decision reads. Requirements as
- * plm_gemm, plus 0 <= pending[r] < V. `tile` uses split_k == 1.
+ * plm_gemm. `tile` uses split_k == 1.
  */
 int plm_lm_head_verify(int32_t dtype, const void* x, int64_t ldx, const void* w, int64_t ldw, int64_t R, int64_t V,
-                       int64_t K, const int64_t* pending, float p, int32_t round_mode, uint8_t* accept,
+                       int64_t K, const int64_t* pending, int32_t rule, float p, int32_t round_mode, uint8_t* accept,
                        int64_t* argmax, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace bytes plm_lm_head_verify and plm_lm_head_verify_packed need (counter area first, as for
@@ -219,9 +228,31 @@ size_t plm_lm_head_verify_workspace_bytes(int64_t R, int64_t V, int64_t K, const
  * packed_w 16-byte aligned.
  */
 int plm_lm_head_verify_packed(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, int64_t R, int64_t V,
-                              int64_t K, const int64_t* pending, float p, int32_t round_mode, uint8_t* accept,
+                              int64_t K, const int64_t* pending, int32_t rule, float p, int32_t round_mode, uint8_t* accept,
                               int64_t* argmax, const plm_tile* tile, void* workspace, size_t workspace_bytes,
                               void* stream);
+
+/*
+ * One round's bookkeeping after the verify step, on the device: RoundDecoder._epilogue
+ * (plm/decoder.py:351-365) from the verify kernel's outputs. With k proposals per round
+ * (round width k + k*k):
+ *   widened[k-1]     the acceptance rule's decision for verify rows 0..k-2 (accept[] of the verify
+ *                    step over those rows with the proposals as pending ids)
+ *   hypotheses[k*k]  argmax of the proposal rows k..k+k*k-1 (argmax[] of the verify step)
+ *   verify[k]        the verify rows' decoded tokens
+ *   accepted[i]   = verify[i] == pending[i] || widened[i]; num_correct = leading accepted count
+ *   out[base + i] = pending[i] for i < num_correct and verify[num_correct] at i == num_correct
+ *                   (slots outside [0, out_len) are not written)
+ *   round_sequence[min(step, sequence_len - 1)] = num_correct; step += 1 (both may be NULL)
+ *   pending       = hypotheses[num_correct*k + 1 .. num_correct*k + k-1]   (updated in place)
+ *   anchor[0] = verify[num_correct]; base += num_correct + 1; offset += num_correct + 1
+ * `accepted` (k-1 bytes) and `num_correct` (one int64) are optional outputs (NULL: not written).
+ * All pointers are device pointers; 1 <= k <= 64. One wavefront, no workspace.
+ */
+int plm_round_epilogue(int64_t k, const uint8_t* widened, const int64_t* hypotheses, const int64_t* verify,
+                       int64_t* pending, int64_t* anchor, int64_t* out, int64_t out_len, int64_t* base,
+                       int64_t* offset, int64_t* round_sequence, int64_t sequence_len, int64_t* sequence_step,
+                       uint8_t* accepted, int64_t* num_correct, void* stream);
 
 /* Human-readable name of a status code. */
 const char* plm_status_string(int32_t status);

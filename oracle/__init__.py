@@ -16,6 +16,9 @@ Every function cites the reference lines it restates. Pinning (each is checked i
 * ``argmax``                — pinned (ties resolve to the lowest index, brute force).
 * ``verify``                — composition of the two above; pinned through them.
 * ``epilogue``              — pinned (hand-worked rounds: all accepted, none, first rejection).
+* ``epilogue_state``        — the same bookkeeping with the reference's state writes, from the
+                              rule's decisions; ``epilogue`` runs through it, so the hand-worked
+                              rounds pin it, plus slot / sequence-capacity cases of its own.
 
 The reference ships no tests or golden vectors for this path (it has none at all), so the fixtures
 under ``tests/golden/`` are generated from this oracle on seeded inputs.
@@ -24,6 +27,7 @@ under ``tests/golden/`` are generated from this oracle on seeded inputs.
 from .plm_oracle import (  # noqa: F401
     argmax,
     epilogue,
+    epilogue_state,
     floor_acceptance,
     linear,
     linear_fp32,

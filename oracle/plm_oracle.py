@@ -119,20 +119,50 @@ def argmax_fp64(logits: torch.Tensor) -> np.ndarray:
 
 # --------------------------------------------------------------------------- the round epilogue
 
+def epilogue_state(widened: torch.Tensor, hypotheses: torch.Tensor, verify_tokens: torch.Tensor,
+                   pending: torch.Tensor, anchor: torch.Tensor, out: torch.Tensor, base_t: torch.Tensor,
+                   offset_t: torch.Tensor, round_sequence: torch.Tensor, sequence_step: torch.Tensor,
+                   k: int, sequence_capacity: int) -> dict:
+    """``RoundDecoder._epilogue`` (plm/decoder.py:351-365) from the rule's decisions, state writes
+    included, on CPU copies: ``widened[k-1]`` is the rule over verify rows 0..k-2, ``hypotheses[k*k]``
+    the argmax of the proposal rows. Returns the updated state and ``accepted``/``num_correct``."""
+    pending, anchor, out = pending.cpu().clone(), anchor.cpu().clone(), out.cpu().clone()
+    base_t, offset_t = base_t.cpu().clone(), offset_t.cpu().clone()
+    round_sequence, sequence_step = round_sequence.cpu().clone(), sequence_step.cpu().clone()
+    verify_tokens, hypotheses = verify_tokens.cpu(), hypotheses.cpu()
+    kidx = torch.arange(k)
+    accepted = (verify_tokens[:-1] == pending) | widened.cpu().bool()
+    num_correct = accepted.to(torch.int64).cumprod(0).sum()
+    confirmed_head = torch.cat([pending, verify_tokens[-1:]])
+    picked = verify_tokens.index_select(0, num_correct.clamp(max=k - 1).view(1))
+    slots = base_t + kidx
+    out[slots] = torch.where(kidx < num_correct, confirmed_head,
+                             torch.where(kidx == num_correct, picked.expand(k), out[slots]))
+    round_sequence.index_copy_(0, sequence_step.clamp(max=sequence_capacity - 1), num_correct.view(1))
+    sequence_step.add_(1)
+    pending.copy_(hypotheses.view(k, k).index_select(0, num_correct.view(1))[0][1:k])
+    anchor.copy_(picked)
+    base_t.add_(num_correct + 1)
+    offset_t.add_(num_correct + 1)
+    return {"accepted": accepted, "num_correct": int(num_correct), "pending": pending, "anchor": anchor,
+            "out": out, "base_t": base_t, "offset_t": offset_t, "round_sequence": round_sequence,
+            "sequence_step": sequence_step}
+
+
 def epilogue(logits: torch.Tensor, verify_tokens: torch.Tensor, pending: torch.Tensor, k: int, rule: str,
              threshold: float) -> dict:
-    """One round's bookkeeping after the LM head (plm/decoder.py:351-365), without the state writes.
+    """One round's bookkeeping after the LM head (plm/decoder.py:351-365) from the round's logits.
 
     ``logits`` is ``[k + k*k, V]`` (verify rows first, then ``k`` proposal blocks of ``k``),
     ``verify_tokens[k]`` the verify rows' own decodes, ``pending[k-1]`` last round's proposals.
-    Returns ``accepted[k-1]``, ``num_correct``, the ``num_correct + 1`` committed tokens and the next
-    round's ``pending[k-1]``."""
+    Returns ``accepted[k-1]``, ``num_correct``, the ``num_correct + 1`` committed tokens (the slots
+    the round writes, from a fresh state at position 0) and the next round's ``pending[k-1]``."""
     widened = floor_acceptance if rule == "floor" else nucleus_acceptance
-    accepted = (verify_tokens[:-1].cpu() == pending.cpu()) | widened(logits[: k - 1], pending, threshold)
-    num_correct = int(accepted.to(torch.int64).cumprod(0).sum())
-    confirmed_head = torch.cat([pending.cpu(), verify_tokens[-1:].cpu()])
-    picked = verify_tokens.cpu()[min(num_correct, k - 1)]
-    committed = torch.cat([confirmed_head[:num_correct], picked.view(1)])
-    hypotheses = argmax(logits[k:]).view(k, k)
-    return {"accepted": accepted, "num_correct": num_correct, "committed": committed,
-            "next_pending": hypotheses[num_correct][1:k]}
+    decisions = widened(logits[: k - 1], pending, threshold)
+    state = epilogue_state(decisions, argmax(logits[k:]), verify_tokens, pending,
+                           torch.zeros(1, dtype=torch.int64), torch.full((k,), -1, dtype=torch.int64),
+                           torch.zeros((), dtype=torch.int64), torch.zeros((), dtype=torch.int64),
+                           torch.zeros(1, dtype=torch.int64), torch.zeros(1, dtype=torch.int64), k, 1)
+    n = state["num_correct"]
+    return {"accepted": state["accepted"], "num_correct": n, "committed": state["out"][: n + 1],
+            "next_pending": state["pending"]}

@@ -9,6 +9,8 @@
 //   accept = (sum_{j: l_j > l_own} e_j) / (sum_j e_j) < p  |  (l_own >= mx & p > 0)
 // exp is monotone, so "probs > own" and "l > l_own" select the same set except where exp/divide
 // rounding makes two distinct logits produce equal probabilities.
+// The floor rule (plm/decoder.py:78-82), accept = l_own - logsumexp(l) > log(eps), reads the same
+// row state: logsumexp(l) = mx + log(sum_j e_j).
 //
 // Two launches:
 //   1. own_logit_kernel: one workgroup per row r recomputes the single logit l[r, pending[r]] with
@@ -36,7 +38,8 @@ struct VerifyArgs {
   int64_t ldx, ldw;
   int R, V, K, G;
   const int64_t* pending;
-  float p;
+  float p;           // top-p for PLM_RULE_NUCLEUS, epsilon for PLM_RULE_FLOOR
+  int rule;
   int round_mode;
   uint8_t* accept;
   int64_t* argmax;
@@ -58,6 +61,16 @@ struct RowState {
 };
 
 __device__ __forceinline__ RowState empty_state() { return RowState{-INFINITY, 0.f, 0.f, INT_MAX}; }
+
+// The acceptance decision for a proposal with logit `own` (NaN: not a vocabulary id, never
+// accepted) in a row with merged state t.
+__device__ __forceinline__ bool accept_proposal(const VerifyArgs& a, float own, const RowState& t) {
+  if (!(own == own)) return false;
+  if (a.rule == PLM_RULE_FLOOR) return (own - (t.mx + logf(t.se))) > logf(a.p);
+  const bool in_nucleus = (t.ab / t.se) < a.p;
+  const bool is_max = (own >= t.mx) && (a.p > 0.f);
+  return in_nucleus || is_max;
+}
 
 #pragma clang fp contract(off)
 __device__ __forceinline__ RowState merge(RowState a, RowState b) {
@@ -218,11 +231,7 @@ __global__ __launch_bounds__(64 * KW) void verify_main_kernel(VerifyArgs a) {
     }
     s = wave_merge(s);
     if (lane == 0) {
-      const float own = a.own[m];
-      const bool in_nucleus = (s.ab / s.se) < a.p;
-      const bool is_max = (own >= s.mx) && (a.p > 0.f);
-      const bool valid_id = own == own;  // NaN marks a pending id outside [0, V)
-      a.accept[m] = (valid_id && (in_nucleus || is_max)) ? 1 : 0;
+      a.accept[m] = accept_proposal(a, a.own[m], s) ? 1 : 0;
       a.argmax[m] = s.ai;
     }
   }
@@ -634,11 +643,7 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D
   const RowState t = merge_rows(grid, groups, wave, lane, st_mx, st_se, st_ab, st_ai);
   if (wave == 0 && lane < a.R) {
     const int m = lane;
-    const float own = a.own[m];
-    const bool in_nucleus = (t.ab / t.se) < a.p;
-    const bool is_max = (own >= t.mx) && (a.p > 0.f);
-    const bool valid_id = own == own;  // NaN marks a pending id outside [0, V)
-    a.accept[m] = (valid_id && (in_nucleus || is_max)) ? 1 : 0;
+    a.accept[m] = accept_proposal(a, a.own[m], t) ? 1 : 0;
     a.argmax[m] = t.ai;
   }
 }
@@ -736,12 +741,13 @@ size_t plm_lm_head_verify_workspace_bytes(int64_t R, int64_t V, int64_t K, const
 }
 
 int plm_lm_head_verify(int32_t dtype, const void* x, int64_t ldx, const void* w, int64_t ldw, int64_t R, int64_t V,
-                       int64_t K, const int64_t* pending, float p, int32_t round_mode, uint8_t* accept,
+                       int64_t K, const int64_t* pending, int32_t rule, float p, int32_t round_mode, uint8_t* accept,
                        int64_t* argmax, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream) {
   if (x == nullptr || w == nullptr || pending == nullptr || accept == nullptr || argmax == nullptr || tile == nullptr)
     return PLM_ERR_ARGUMENT;
   if (dtype != PLM_BF16 && dtype != PLM_F16) return PLM_ERR_ARGUMENT;
   if (round_mode < PLM_ROUND_F32 || round_mode > PLM_ROUND_F16) return PLM_ERR_ARGUMENT;
+  if (rule != PLM_RULE_NUCLEUS && rule != PLM_RULE_FLOOR) return PLM_ERR_ARGUMENT;
   if (R < 1 || R > 64 || V < 1 || V > (int64_t(1) << 30) || K < 8 || K % 8 != 0 || K > (int64_t(1) << 30))
     return PLM_ERR_ARGUMENT;
   if (ldx < K || ldw < K || tile->split_k != 1 || tile->k_waves < 1) return PLM_ERR_ARGUMENT;
@@ -761,6 +767,7 @@ int plm_lm_head_verify(int32_t dtype, const void* x, int64_t ldx, const void* w,
   a.K = static_cast<int>(K);
   a.pending = pending;
   a.p = p;
+  a.rule = rule;
   a.round_mode = round_mode;
   a.accept = accept;
   a.argmax = argmax;
@@ -785,7 +792,7 @@ int plm_lm_head_verify(int32_t dtype, const void* x, int64_t ldx, const void* w,
 }
 
 int plm_lm_head_verify_packed(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, int64_t R, int64_t V,
-                              int64_t K, const int64_t* pending, float p, int32_t round_mode, uint8_t* accept,
+                              int64_t K, const int64_t* pending, int32_t rule, float p, int32_t round_mode, uint8_t* accept,
                               int64_t* argmax, const plm_tile* tile, void* workspace, size_t workspace_bytes,
                               void* stream) {
   if (x == nullptr || packed_w == nullptr || pending == nullptr || accept == nullptr || argmax == nullptr ||
@@ -793,6 +800,7 @@ int plm_lm_head_verify_packed(int32_t dtype, const void* x, int64_t ldx, const v
     return PLM_ERR_ARGUMENT;
   if (dtype != PLM_BF16 && dtype != PLM_F16) return PLM_ERR_ARGUMENT;
   if (round_mode < PLM_ROUND_F32 || round_mode > PLM_ROUND_F16) return PLM_ERR_ARGUMENT;
+  if (rule != PLM_RULE_NUCLEUS && rule != PLM_RULE_FLOOR) return PLM_ERR_ARGUMENT;
   if (R < 1 || R > 64 || V < 1 || V > (int64_t(1) << 30) || K < 8 || K % 8 != 0 || K > (int64_t(1) << 24))
     return PLM_ERR_ARGUMENT;
   if (ldx < K || R * ldx * 2 >= (int64_t(1) << 31)) return PLM_ERR_ARGUMENT;
@@ -814,6 +822,7 @@ int plm_lm_head_verify_packed(int32_t dtype, const void* x, int64_t ldx, const v
   a.K = static_cast<int>(K);
   a.pending = pending;
   a.p = p;
+  a.rule = rule;
   a.round_mode = round_mode;
   a.accept = accept;
   a.argmax = argmax;

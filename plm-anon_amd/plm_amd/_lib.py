@@ -16,6 +16,7 @@ LIBRARY = Path(__file__).resolve().parent / "libplm_amd.so"
 
 PLM_BF16, PLM_F16 = 0, 1
 PLM_ROUND_F32, PLM_ROUND_BF16, PLM_ROUND_F16 = 0, 1, 2
+PLM_RULE_NUCLEUS, PLM_RULE_FLOOR = 0, 1
 DTYPE_CODES = {torch.bfloat16: PLM_BF16, torch.float16: PLM_F16}
 # PLM_WORKSPACE_COUNTER_BYTES: the zero-between-calls counter area at the start of every workspace.
 COUNTER_BYTES = 1 << 18
@@ -43,6 +44,7 @@ EXPORTS = (
     "plm_lm_head_verify",
     "plm_lm_head_verify_workspace_bytes",
     "plm_lm_head_verify_packed",
+    "plm_round_epilogue",
     "plm_status_string",
 )
 
@@ -106,14 +108,17 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.plm_gemm_chain_packed.restype = ctypes.c_int
     lib.plm_gemm_packed_resident_workgroups.argtypes = [c_i32, c_i64, tile_p]
     lib.plm_gemm_packed_resident_workgroups.restype = ctypes.c_int
-    lib.plm_lm_head_verify.argtypes = [c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, c_p, ctypes.c_float, c_i32,
-                                       c_p, c_p, tile_p, c_p, c_sz, c_p]
+    lib.plm_lm_head_verify.argtypes = [c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, c_p, c_i32, ctypes.c_float,
+                                       c_i32, c_p, c_p, tile_p, c_p, c_sz, c_p]
     lib.plm_lm_head_verify.restype = ctypes.c_int
-    lib.plm_lm_head_verify_packed.argtypes = [c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_p, ctypes.c_float, c_i32,
-                                              c_p, c_p, tile_p, c_p, c_sz, c_p]
+    lib.plm_lm_head_verify_packed.argtypes = [c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_p, c_i32, ctypes.c_float,
+                                              c_i32, c_p, c_p, tile_p, c_p, c_sz, c_p]
     lib.plm_lm_head_verify_packed.restype = ctypes.c_int
     lib.plm_lm_head_verify_workspace_bytes.argtypes = [c_i64, c_i64, c_i64, tile_p]
     lib.plm_lm_head_verify_workspace_bytes.restype = c_sz
+    lib.plm_round_epilogue.argtypes = [c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_p, c_p, c_p, c_i64, c_p, c_p, c_p,
+                                       c_p]
+    lib.plm_round_epilogue.restype = ctypes.c_int
     lib.plm_status_string.argtypes = [c_i32]
     lib.plm_status_string.restype = ctypes.c_char_p
 

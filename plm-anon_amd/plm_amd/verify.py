@@ -1,9 +1,10 @@
 """Fused LM-head verify step on the HIP kernel: the LM-head GEMM with the round's acceptance
 epilogue folded in, so the ``[R, V]`` logits are never written to memory.
 
-Per row ``r`` it returns the nucleus decision for ``pending[r]`` (``nucleus_acceptance``,
-plm/decoder.py:71-75) and the row argmax with lowest-index ties (``logits.argmax(-1)``,
-plm/decoder.py:362). ``round_to`` fixes which logits the decision reads: ``"fp32"`` is the fp32
+Per row ``r`` it returns the acceptance rule's decision for ``pending[r]`` (``nucleus_acceptance``,
+plm/decoder.py:71-75, or ``floor_acceptance``, 78-82) and the row argmax with lowest-index ties
+(``logits.argmax(-1)``, plm/decoder.py:362). ``round_epilogue`` is the rest of the round's
+bookkeeping (``RoundDecoder._epilogue``, plm/decoder.py:351-365) on the device. ``round_to`` fixes which logits the decision reads: ``"fp32"`` is the fp32
 accumulator; ``"bf16"``/``"fp16"`` round it to the model dtype first, which is what the reference's
 decoder sees (the GEMM output cast at plm/fast_gemm.py:46, upcast again at plm/decoder.py:73).
 """
@@ -16,6 +17,7 @@ from . import _lib
 from .fast_gemm import HALF_DTYPES, Config, packed_weight, workspace
 
 ROUND_MODES = {"fp32": _lib.PLM_ROUND_F32, "bf16": _lib.PLM_ROUND_BF16, "fp16": _lib.PLM_ROUND_F16}
+RULES = {"nucleus": _lib.PLM_RULE_NUCLEUS, "floor": _lib.PLM_RULE_FLOOR}
 
 # Verify tile over packed weights (plm_lm_head_verify_packed): the row-split layout, 128-row tiles.
 VERIFY_CONFIG: Config = {"wave_frags": 2, "k_waves": 1, "split_k": 1, "unroll": 2}
@@ -38,11 +40,14 @@ def verify_workspace_bytes(R: int, V: int, K: int, cfg: Config = VERIFY_CONFIG) 
 
 def lm_head_verify(x: torch.Tensor, w: torch.Tensor, pending: torch.Tensor, p: float, round_to: str = "fp32",
                    cfg: Config | None = None, accept: torch.Tensor | None = None,
-                   argmax: torch.Tensor | None = None, packed: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
+                   argmax: torch.Tensor | None = None, packed: bool = True,
+                   rule: str = "nucleus") -> tuple[torch.Tensor, torch.Tensor]:
     """``(accept[R] bool, argmax[R] int64)`` for ``logits = x[R,K] @ w[V,K]^T``.
 
     ``pending[R]`` (int64, on the GPU) are the proposed ids; an id outside ``[0, V)`` is never
-    accepted. ``p <= 0`` accepts nothing (exact matching, plm/decoder.py:115). With ``packed``
+    accepted. ``rule`` is the decoder's ``accept_rule``: ``"nucleus"`` reads ``p`` as top-p
+    (``p <= 0`` accepts nothing: exact matching, plm/decoder.py:115), ``"floor"`` as epsilon.
+    With ``packed``
     (the default) W is read through its packed copy (``fast_gemm.packed_weight``, made once per
     weight) on the packed GEMM's pipeline; ``packed=False`` reads W row-major."""
     if x.dim() != 2 or w.dim() != 2 or x.shape[1] != w.shape[1]:
@@ -51,6 +56,8 @@ def lm_head_verify(x: torch.Tensor, w: torch.Tensor, pending: torch.Tensor, p: f
         raise TypeError(f"lm_head_verify needs matching bf16/fp16 operands, got {x.dtype} and {w.dtype}")
     if round_to not in ROUND_MODES:
         raise ValueError(f"round_to must be one of {sorted(ROUND_MODES)}")
+    if rule not in RULES:
+        raise ValueError(f"rule must be one of {sorted(RULES)}")
     R, K = x.shape
     V = w.shape[0]
     if pending.shape != (R,) or pending.dtype != torch.int64 or pending.device != x.device:
@@ -70,7 +77,7 @@ def lm_head_verify(x: torch.Tensor, w: torch.Tensor, pending: torch.Tensor, p: f
     lib = _lib.lib()
     need = int(lib.plm_lm_head_verify_workspace_bytes(R, V, K, tile))
     ws = workspace(x.device, need)
-    common = (pending.data_ptr(), float(p), ROUND_MODES[round_to], accept_out.data_ptr(), argmax.data_ptr(), tile,
+    common = (pending.data_ptr(), RULES[rule], float(p), ROUND_MODES[round_to], accept_out.data_ptr(), argmax.data_ptr(), tile,
               ws.data_ptr(), ws.numel(), _lib.stream_handle(x.device))
     if packed:
         status = lib.plm_lm_head_verify_packed(_lib.DTYPE_CODES[x.dtype], x.data_ptr(), x.stride(0),
@@ -84,3 +91,79 @@ def lm_head_verify(x: torch.Tensor, w: torch.Tensor, pending: torch.Tensor, p: f
         accept.copy_(accept_out)
         return accept, argmax
     return accept_out, argmax
+
+
+def round_epilogue(k: int, widened: torch.Tensor, hypotheses: torch.Tensor, verify: torch.Tensor,
+                   pending: torch.Tensor, anchor: torch.Tensor, out: torch.Tensor, base_t: torch.Tensor,
+                   offset_t: torch.Tensor, round_sequence: torch.Tensor | None = None,
+                   sequence_step: torch.Tensor | None = None, accepted: torch.Tensor | None = None,
+                   num_correct: torch.Tensor | None = None) -> None:
+    """``RoundDecoder._epilogue`` (plm/decoder.py:351-365) after the fused verify, in one launch.
+
+    ``widened[k-1]`` (bool/uint8) is ``lm_head_verify``'s ``accept`` for verify rows ``0..k-2``
+    with ``pending`` as the proposed ids; ``hypotheses[k*k]`` its ``argmax`` for the proposal rows
+    ``k..k+k*k-1``; ``verify[k]`` the verify rows' decoded tokens. Updates ``pending``, ``anchor``,
+    ``out``, ``base_t``, ``offset_t`` and (if given) ``round_sequence``/``sequence_step`` in place, as
+    the reference does; ``accepted[k-1]`` and ``num_correct`` (0-dim or [1] int64) are optional
+    outputs. Every tensor is a contiguous int64 (``widened``/``accepted``: one byte per entry)
+    tensor on the GPU."""
+    if not 1 <= k <= 64:
+        raise ValueError(f"k must be in [1, 64], got {k}")
+    dev = verify.device
+    if not verify.is_cuda:
+        raise RuntimeError("round_epilogue runs on the GPU only; got a CPU tensor")
+
+    def need(t: torch.Tensor | None, name: str, n: int, dtypes: tuple) -> int:
+        if t is None:
+            return 0
+        if t.device != dev or t.dtype not in dtypes or not t.is_contiguous() or t.numel() < n:
+            raise ValueError(f"{name} must be a contiguous {dtypes[0]} tensor of >= {n} entries on {dev}")
+        return t.data_ptr()
+
+    i64, u8 = (torch.int64,), (torch.bool, torch.uint8)
+    if (round_sequence is None) != (sequence_step is None):
+        raise ValueError("round_sequence and sequence_step go together")
+    args = (need(widened, "widened", k - 1, u8) if k > 1 else 0, need(hypotheses, "hypotheses", k * k, i64),
+            need(verify, "verify", k, i64), need(pending, "pending", k - 1, i64) if k > 1 else 0,
+            need(anchor, "anchor", 1, i64), need(out, "out", 0, i64), out.numel(), need(base_t, "base_t", 1, i64),
+            need(offset_t, "offset_t", 1, i64), need(round_sequence, "round_sequence", 1, i64),
+            0 if round_sequence is None else round_sequence.numel(), need(sequence_step, "sequence_step", 1, i64),
+            need(accepted, "accepted", k - 1, u8), need(num_correct, "num_correct", 1, i64))
+    status = _lib.lib().plm_round_epilogue(k, *args, _lib.stream_handle(dev))
+    _lib.check(status, f"plm_round_epilogue(k={k})")
+
+
+class RoundVerify:
+    """The LM-head end of one round on the device (plm/decoder.py:351-365): one fused verify pass over
+    the round's ``k + k*k`` rows (the rule's decisions for verify rows ``0..k-2`` against the pending
+    proposals, the argmax of every row) and ``round_epilogue``. Rows go to the verify kernel in
+    chunks of at most 64 (a round of ``k <= 7`` is one pass over W). Buffers are allocated once, so
+    calls can be captured in a HIP graph."""
+
+    def __init__(self, k: int, rule: str = "nucleus", threshold: float = -1.0, round_to: str = "fp32",
+                 device: torch.device | str = "cuda", cfg: Config | None = None):
+        if rule not in RULES or round_to not in ROUND_MODES:
+            raise ValueError(f"rule must be one of {sorted(RULES)} and round_to one of {sorted(ROUND_MODES)}")
+        if not 1 <= k <= 64:
+            raise ValueError(f"k must be in [1, 64], got {k}")
+        self.k, self.width = k, k + k * k
+        self.rule, self.threshold, self.round_to, self.cfg = rule, float(threshold), round_to, cfg
+        self.rows_pending = torch.full((self.width,), -1, dtype=torch.int64, device=device)
+        self.accept = torch.zeros(self.width, dtype=torch.bool, device=device)
+        self.argmax = torch.zeros(self.width, dtype=torch.int64, device=device)
+
+    def __call__(self, hidden: torch.Tensor, w: torch.Tensor, verify_tokens: torch.Tensor, pending: torch.Tensor,
+                 anchor: torch.Tensor, out: torch.Tensor, base_t: torch.Tensor, offset_t: torch.Tensor,
+                 round_sequence: torch.Tensor | None = None, sequence_step: torch.Tensor | None = None,
+                 accepted: torch.Tensor | None = None, num_correct: torch.Tensor | None = None) -> None:
+        k, W = self.k, self.width
+        if hidden.dim() != 2 or hidden.shape[0] != W:
+            raise ValueError(f"hidden must be [{W}, K] for k={k}, got {tuple(hidden.shape)}")
+        if k > 1:
+            self.rows_pending[: k - 1].copy_(pending)
+        for r0 in range(0, W, 64):
+            r1 = min(W, r0 + 64)
+            lm_head_verify(hidden[r0:r1], w, self.rows_pending[r0:r1], self.threshold, self.round_to, self.cfg,
+                           accept=self.accept[r0:r1], argmax=self.argmax[r0:r1], rule=self.rule)
+        round_epilogue(k, self.accept[: max(k - 1, 0)], self.argmax[k:], verify_tokens, pending, anchor, out, base_t,
+                       offset_t, round_sequence, sequence_step, accepted, num_correct)

@@ -62,23 +62,43 @@ def test_argument_validation_happens_before_launch():
     assert lib.plm_gemm(0, fake, 1024, fake, 1024, fake, 4096, 42, 4096, 1024, odd, None, 0, None) == -3
     # Verify: bad round mode, R too large.
     vt = _lib.Tile(2, 4, 1, 4)
-    assert lib.plm_lm_head_verify(0, fake, 2048, fake, 2048, 56, 50257, 2048, fake, 0.94, 9, fake, fake, vt, fake,
+    assert lib.plm_lm_head_verify(0, fake, 2048, fake, 2048, 56, 50257, 2048, fake, 0, 0.94, 9, fake, fake, vt, fake,
                                   1 << 30, None) == -1
-    assert lib.plm_lm_head_verify(0, fake, 2048, fake, 2048, 65, 50257, 2048, fake, 0.94, 0, fake, fake, vt, fake,
+    assert lib.plm_lm_head_verify(0, fake, 2048, fake, 2048, 65, 50257, 2048, fake, 0, 0.94, 0, fake, fake, vt, fake,
+                                  1 << 30, None) == -1
+    # Unknown acceptance rule.
+    assert lib.plm_lm_head_verify(0, fake, 2048, fake, 2048, 56, 50257, 2048, fake, 2, 0.94, 0, fake, fake, vt, fake,
                                   1 << 30, None) == -1
     # Packed verify: the same checks, K limits, and only row-split tiles without split-K.
     pt = _lib.Tile(2, 1, 1, 2)
-    assert lib.plm_lm_head_verify_packed(0, fake, 2048, fake, 56, 50257, 2048, fake, 0.94, 9, fake, fake, pt, fake,
+    assert lib.plm_lm_head_verify_packed(0, fake, 2048, fake, 56, 50257, 2048, fake, 0, 0.94, 9, fake, fake, pt, fake,
                                          1 << 30, None) == -1
-    assert lib.plm_lm_head_verify_packed(0, fake, 2048, fake, 65, 50257, 2048, fake, 0.94, 0, fake, fake, pt, fake,
+    assert lib.plm_lm_head_verify_packed(0, fake, 2048, fake, 65, 50257, 2048, fake, 0, 0.94, 0, fake, fake, pt, fake,
                                          1 << 30, None) == -1
-    assert lib.plm_lm_head_verify_packed(0, fake, 2048, fake, 56, 50257, 2044, fake, 0.94, 0, fake, fake, pt, fake,
+    assert lib.plm_lm_head_verify_packed(0, fake, 2048, fake, 56, 50257, 2044, fake, 0, 0.94, 0, fake, fake, pt, fake,
                                          1 << 30, None) == -1
-    assert lib.plm_lm_head_verify_packed(0, fake, 2048, fake, 56, 50257, 2048, fake, 0.94, 0, fake, fake, pt, fake,
+    assert lib.plm_lm_head_verify_packed(0, fake, 2048, fake, 56, 50257, 2048, fake, 0, 0.94, 0, fake, fake, pt, fake,
                                          16, None) == -4
+    assert lib.plm_lm_head_verify_packed(0, fake, 2048, fake, 56, 50257, 2048, fake, -1, 0.94, 0, fake, fake, pt, fake,
+                                         1 << 30, None) == -1
     for bad in (_lib.Tile(2, 4, 1, 2), _lib.Tile(2, 1, 2, 2), _lib.Tile(1, 1, 1, 2), _lib.Tile(2, 1, 1, 6)):
-        assert lib.plm_lm_head_verify_packed(0, fake, 2048, fake, 56, 50257, 2048, fake, 0.94, 0, fake, fake, bad,
+        assert lib.plm_lm_head_verify_packed(0, fake, 2048, fake, 56, 50257, 2048, fake, 0, 0.94, 0, fake, fake, bad,
                                              fake, 1 << 30, None) == -3
+
+
+def test_epilogue_argument_validation_happens_before_launch():
+    lib = _lib.lib()
+    fake = 1 << 20
+    full = (fake, fake, fake, fake, fake, fake, 100, fake, fake, fake, 10, fake, None, None, None)
+    # k outside [1, 64].
+    assert lib.plm_round_epilogue(0, *full) == -1
+    assert lib.plm_round_epilogue(65, *full) == -1
+    # Proposals without decisions; a round sequence without its step counter; a negative out length.
+    assert lib.plm_round_epilogue(7, None, *full[1:]) == -1
+    assert lib.plm_round_epilogue(7, *full[:11], None, *full[12:]) == -1
+    assert lib.plm_round_epilogue(7, *full[:6], -1, *full[7:]) == -1
+    # An empty round sequence.
+    assert lib.plm_round_epilogue(7, *full[:10], 0, *full[11:]) == -1
 
 
 def test_packed_argument_validation_happens_before_launch():

@@ -210,6 +210,35 @@ def test_epilogue_exact_match_accepts_by_equality_only():
     assert out["committed"].tolist() == [4, 6]
 
 
+def test_epilogue_state_writes_at_the_base_and_clamps_the_sequence():
+    """Hand-worked state update: k = 4, base 10, the third proposal rejected (num_correct = 2)."""
+    k = 4
+    widened = torch.tensor([True, False, False], dtype=torch.bool)
+    pending = torch.tensor([11, 12, 13])
+    verify = torch.tensor([50, 12, 60, 70])       # proposal 1 matches its decode, 0 is widened, 2 neither
+    hyp = torch.arange(100, 116)                  # 4 blocks of 4 hypotheses
+    out = torch.full((20,), -1, dtype=torch.int64)
+    out[14] = 99                                  # slot past the round's reach keeps its value
+    st = oracle.epilogue_state(widened, hyp, verify, pending, torch.tensor([0]), out, torch.tensor(10),
+                               torch.tensor(30), torch.zeros(3, dtype=torch.int64), torch.tensor([5]), k, 3)
+    assert st["accepted"].tolist() == [True, True, False] and st["num_correct"] == 2
+    assert st["out"][10:15].tolist() == [11, 12, 60, -1, 99]
+    assert st["pending"].tolist() == [109, 110, 111]   # block 2 = 108..111, entries 1..3
+    assert st["anchor"].tolist() == [60]
+    assert int(st["base_t"]) == 13 and int(st["offset_t"]) == 33
+    assert st["round_sequence"].tolist() == [0, 0, 2] and st["sequence_step"].tolist() == [6]
+
+
+def test_epilogue_state_single_proposal_round():
+    """k = 1: no proposals, nothing to accept; the verify row's token is committed."""
+    st = oracle.epilogue_state(torch.zeros(0, dtype=torch.bool), torch.tensor([7]), torch.tensor([42]),
+                               torch.zeros(0, dtype=torch.int64), torch.tensor([0]),
+                               torch.full((4,), -1, dtype=torch.int64), torch.tensor(2), torch.tensor(0),
+                               torch.zeros(2, dtype=torch.int64), torch.tensor([0]), 1, 2)
+    assert st["num_correct"] == 0 and st["out"].tolist() == [-1, -1, 42, -1]
+    assert st["pending"].numel() == 0 and int(st["base_t"]) == 3 and st["anchor"].tolist() == [42]
+
+
 # --------------------------------------------------------------------------- planted mistakes
 
 
