@@ -154,15 +154,15 @@ int packed_entry(int32_t dtype, const void* x, int64_t ldx, const void* wp, void
 }
 
 // How the linears of a chain wait for the ones they read: 0 (none reads another), 2 (every linear
-// after the first reads the one before it, and none has more tiles than a parity set of tile
-// flags holds: per-wavefront waits on the producer's tile-done flags), or 1 (otherwise: a grid
-// barrier after every linear that is read).
+// after the first reads the one before it, and none that is read has more tiles than a parity set
+// of tile flags holds: per-wavefront waits on the producer's tile-done flags; the last linear,
+// read by none, raises no flags), or 1 (otherwise: a grid barrier after every linear that is read).
 int packed_chain_mode(const plm_chain_gemm* g, int32_t count, const plm_tile& t) {
   bool any = false, pure = count > 1;
   for (int32_t i = 0; i < count; ++i) {
     any = any || g[i].dep >= 0;
     if (i > 0 && g[i].dep != i - 1) pure = false;
-    if (packed_tiles(g[i].N, t) > kPkTileFlags) pure = false;
+    if (i + 1 < count && packed_tiles(g[i].N, t) > kPkTileFlags) pure = false;
   }
   return pure ? 2 : (any ? 1 : 0);
 }
