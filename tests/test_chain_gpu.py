@@ -1,6 +1,7 @@
 """GPU parity of the chained launches: linears back to back in one persistent grid, over packed
-weights (plm_gemm_chain_packed: grid barriers of per-workgroup progress flags) and over row-major
-weights (plm_gemm_chain: each consumer tile starts once the producer tiles it reads are written).
+weights (plm_gemm_chain_packed: tile-done flags when every linear reads the one before it, else
+grid barriers of per-workgroup progress flags) and over row-major weights (plm_gemm_chain: each
+consumer tile starts once the producer tiles it reads are written).
 
 Checks: every link's output equals the single-linear kernel's on the same operands bit for bit
 (same kernel, same K partition), and the CPU oracle's within the GEMM tolerance; repeated launches
@@ -40,12 +41,21 @@ def _chain(x, ws, splits, deps=None, ys=None):
 
 
 def _check_against_single(links, cfg=CFG, packed=True):
+    """Bit for bit the single-linear kernel; against the oracle within 1e-3 rel / 2e-2 abs, or one
+    output rounding step where the oracle's own fp32 sum lands on the other side of a rounding
+    midpoint (at |y| >= 4 one bf16 step exceeds 2e-2), for at most 0.1 % of a link's elements."""
     for i, ln in enumerate(links):
         linear = hip_linear if packed else hip_linear_rowmajor
         single = linear(ln.x, ln.w, dict(cfg, split_k=ln.split_k))
         assert torch.equal(ln.y, single), f"link {i} differs from the single-linear kernel"
-        torch.testing.assert_close(ln.y.cpu().float(), oracle.linear(ln.x.cpu(), ln.w.cpu()).float(), rtol=RTOL,
-                                   atol=ATOL)
+        got = ln.y.cpu().float()
+        ref = oracle.linear(ln.x.cpu(), ln.w.cpu()).float()
+        diff = (got - ref).abs()
+        in_tol = diff <= ATOL + RTOL * ref.abs()
+        bits = 8 if ln.y.dtype == torch.bfloat16 else 11
+        step = 2.0 ** (torch.floor(torch.log2(ref.abs().clamp_min(2.0 ** -14))) - (bits - 1))
+        assert bool((in_tol | (diff <= step * 1.0001)).all()), f"link {i}: max |got - oracle| {diff.max():.4g}"
+        assert int((~in_tol).sum()) <= max(1, got.numel() // 1000), (i, int((~in_tol).sum()))
 
 
 @pytest.mark.parametrize("packed", [True, False], ids=["packed", "rowmajor"])
@@ -80,6 +90,22 @@ def test_packed_chain_tiles(device, cfg):
     chain = LinearChain(links, cfg, packed=True)
     chain.run()
     _check_against_single(links, cfg)
+    assert chain.error_flag() == 0
+
+
+def test_tile_flag_chain_long_and_wide_links(device):
+    """The tile-flag chain with the round's tile: items of 2 to 32 K steps per wavefront, several
+    items per workgroup (625 and 1250 tiles), a K that ends inside a step, a split link."""
+    M = 56
+    cfg = {"wave_frags": 2, "k_waves": 8, "split_k": 1, "unroll": 2}
+    g = torch.Generator(device=device).manual_seed(40)
+    x = torch.randn(M, 2048, generator=g, device=device).bfloat16()
+    ws = _weights([(8192, 2048), (2048, 8192), (20000, 2048), (1000, 20000), (40000, 1000)], 41, device)
+    links, _ = _chain(x, ws, (1, 1, 1, 2, 1))
+    chain = LinearChain(links, cfg, packed=True)
+    for _ in range(2):
+        chain.run()
+        _check_against_single(links, cfg)
     assert chain.error_flag() == 0
 
 
