@@ -45,6 +45,7 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget (0 disables it)")
     ap.add_argument("--no-sweep", action="store_true", help="skip the partial-round M sweep")
     ap.add_argument("--no-verify", action="store_true", help="skip the fused LM-head verify timing")
+    ap.add_argument("--no-llama", action="store_true", help="skip the reference's Llama-style linear sets")
     ap.add_argument("--only-round", action="store_true", help="time the round only (for profiling runs)")
     ap.add_argument("--profile", choices=("eager", "copy", "verify"),
                     help="no JSON: 'eager' launches the round and the fused verify step --steps times without a "
@@ -57,14 +58,16 @@ def parse_args():
 class Round:
     """The round's weights, activation chain and captured graph at one width M."""
 
-    def __init__(self, M, hidden, mlp, layers, weights, tables, device):
+    def __init__(self, M, hidden, mlp, layers, weights, tables, device, gemms=None):
         import torch
 
         from plm_amd.workloads import GPT2_VOCAB, gpt_block
 
         self.M = M
-        self.gemms = [g for _ in range(layers) for g in gpt_block(hidden, mlp)]
-        self.gemms.append(type(self.gemms[0])("lm_head", GPT2_VOCAB, hidden))
+        if gemms is None:
+            gemms = [g for _ in range(layers) for g in gpt_block(hidden, mlp)]
+            gemms.append(type(gemms[0])("lm_head", GPT2_VOCAB, hidden))
+        self.gemms = list(gemms)
         self.weights = weights
         self.cfgs = [tables[(M, g.N, g.K)] for g in self.gemms]
         g = torch.Generator(device=device).manual_seed(3000 + M)
@@ -389,6 +392,8 @@ def main():
             print(f"[bench] M sweep: {sweep}", file=sys.stderr, flush=True)
         if not args.no_verify:
             result["verify"] = time_verify(weights[-1], args.hidden, device, args.steps)
+        if not args.no_llama:
+            result["llama_rounds"] = time_llama_rounds(args, device)
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_baseline(args.hidden, args.mlp, args.M, args.cpu_seconds)
     print(json.dumps(result), flush=True)
@@ -415,6 +420,54 @@ def profile_verify(args, device):
         hip_linear(x, copies[i % 6], cfg)
     torch.cuda.synchronize()
     print(f"[bench] verify x {max(1, args.steps)}, LM-head GEMM {cfg} x {max(1, args.steps)}", file=sys.stderr)
+
+
+def time_llama_rounds(args, device):
+    """The reference's Llama-style linear sets (hidden 2048 and 3072: GQA QKV, fused gate/up, vocabulary
+    50304) as rounds at width M, both ways: the chained launch of the block linears + LM-head launch
+    (checked bit for bit against per-linear launches first) and the per-GEMM graph with the tuned
+    table's tile per shape."""
+    import torch
+
+    from plm_amd import gemm_tables
+    from plm_amd.fast_gemm import hip_linear
+    from plm_amd.workloads import LLAMA_SETS, llama_round
+
+    out = {}
+    for name, spec in LLAMA_SETS.items():
+        gemms = llama_round(name)
+        tables = gemm_tables.read_table(spec["hidden"])
+        gen = torch.Generator(device=device)
+        weights = []
+        for i, g in enumerate(gemms):
+            gen.manual_seed(7 + 1000 * 6 + i)
+            weights.append((0.02 * torch.randn(g.N, g.K, generator=gen, device=device)).bfloat16())
+        rnd = Round(args.M, spec["hidden"], None, spec["layers"], weights, tables, device, gemms=gemms)
+        chained = ChainedRound(rnd)
+        chained.run()
+        torch.cuda.synchronize()
+        chain_outs = [o.clone() for o in rnd.outs]
+        for i, ln in enumerate(chained.chain.links):
+            hip_linear(ln.x, ln.w, dict(chained.chain.cfg, split_k=ln.split_k), rnd.outs[i])
+        hip_linear(*chained.head)
+        torch.cuda.synchronize()
+        same = all(torch.equal(a, b) for a, b in zip(chain_outs, rnd.outs)) and not chained.chain.error_flag()
+        graph = capture_graph(chained.run)
+        us_chain = time_graph(graph, max(10, args.steps // 2), 3) * 1000.0
+        del graph
+        graph = rnd.capture()
+        us_graph = time_graph(graph, max(10, args.steps // 2), 3) * 1000.0
+        del graph
+        nbytes = rnd.bytes
+        out[name] = {"layers": spec["layers"], "hidden": spec["hidden"], "bytes": nbytes,
+                     "chained_us": round(us_chain, 1), "chained_gbps": round(nbytes / (us_chain * 1e-6) / 1e9, 1),
+                     "per_gemm_us": round(us_graph, 1), "per_gemm_gbps": round(nbytes / (us_graph * 1e-6) / 1e9, 1),
+                     "chain_matches_per_linear": bool(same)}
+        print(f"[bench] Llama-style {name} round: chained {us_chain:.1f} us, per-GEMM {us_graph:.1f} us", file=sys.stderr,
+              flush=True)
+        del rnd, chained, weights, chain_outs
+        torch.cuda.empty_cache()
+    return out
 
 
 def time_verify(w_lm, hidden, device, steps):

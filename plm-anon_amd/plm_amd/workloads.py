@@ -41,6 +41,29 @@ def gpt_block(hidden: int, mlp: int) -> list[Gemm]:
             Gemm("mlp_down", hidden, mlp)]
 
 
+def llama_block(hidden: int, qkv: int, intermediate: int) -> list[Gemm]:
+    """The reference's per-layer linears (plm/gemm_tables.py:22-27): fused QKV with grouped KV heads,
+    attention-out, fused gate/up, down."""
+    return [Gemm("qkv", qkv, hidden), Gemm("o", hidden, hidden), Gemm("gate_up", 2 * intermediate, hidden),
+            Gemm("down", hidden, intermediate)]
+
+
+# The reference's released Llama-style linear sets at hidden 2048 and 3072 (the shapes its tile tables
+# key, plm/gpu_tuning/tiles_hidden{2048,3072}.json; vocabulary padded to 50304, plm/gemm_tables.py:16,
+# 26). The reference reads the layer counts from its checkpoints; these are the build's choice for
+# the 1.3B and 3B classes.
+LLAMA_SETS = {
+    "1.3B": {"hidden": 2048, "qkv": 3072, "intermediate": 5632, "layers": 24, "vocab": 50304},
+    "3B": {"hidden": 3072, "qkv": 4608, "intermediate": 8192, "layers": 28, "vocab": 50304},
+}
+
+
+def llama_round(name: str) -> list[Gemm]:
+    s = LLAMA_SETS[name]
+    gemms = [g for _ in range(s["layers"]) for g in llama_block(s["hidden"], s["qkv"], s["intermediate"])]
+    return gemms + [Gemm("lm_head", s["vocab"], s["hidden"])]
+
+
 def round_linears(hidden: int, mlp: int, layers: int, vocab: int = GPT2_VOCAB) -> list[Gemm]:
     gemms = [g for _ in range(layers) for g in gpt_block(hidden, mlp)]
     return gemms + [Gemm("lm_head", vocab, hidden)]
