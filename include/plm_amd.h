@@ -254,6 +254,23 @@ int plm_round_epilogue(int64_t k, const uint8_t* widened, const int64_t* hypothe
                        int64_t* offset, int64_t* round_sequence, int64_t sequence_len, int64_t* sequence_step,
                        uint8_t* accepted, int64_t* num_correct, void* stream);
 
+/*
+ * The round's whole LM-head end in one verify launch pair: plm_lm_head_verify_packed over the round's
+ * R = k + k*k rows (rows 0..k-2 decide on pending[0..k-2], the other rows propose nothing) with
+ * plm_round_epilogue's bookkeeping run by the last workgroup after its final merge (widened = the
+ * rule's decisions of rows 0..k-2, hypotheses = the argmax of rows k..R-1), so neither the
+ * decisions nor the hypotheses make a round trip through memory. Arguments as those two entry
+ * points; 1 <= k <= 7 (R <= 64); `accept[R]` and `argmax[R]` (every row's decision and argmax) are
+ * optional outputs (NULL: not written), `pending` is read for the decisions and rewritten with
+ * the next round's proposals. Workspace as plm_lm_head_verify_workspace_bytes(R, V, K, tile).
+ */
+int plm_round_verify_packed(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, int64_t k, int64_t V,
+                            int64_t K, int32_t rule, float p, int32_t round_mode, const int64_t* verify,
+                            int64_t* pending, int64_t* anchor, int64_t* out, int64_t out_len, int64_t* base,
+                            int64_t* offset, int64_t* round_sequence, int64_t sequence_len, int64_t* sequence_step,
+                            uint8_t* accept, int64_t* argmax, uint8_t* accepted, int64_t* num_correct,
+                            const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Human-readable name of a status code. */
 const char* plm_status_string(int32_t status);
 

@@ -26,6 +26,7 @@
 #include <climits>
 #include <cmath>
 
+#include "epilogue.h"
 #include "packed_gemm.h"
 #include "plm_amd.h"
 #include "tile.h"
@@ -38,6 +39,7 @@ struct VerifyArgs {
   int64_t ldx, ldw;
   int R, V, K, G;
   const int64_t* pending;
+  int pending_rows;  // rows r >= pending_rows propose no id (never accepted)
   float p;           // top-p for PLM_RULE_NUCLEUS, epsilon for PLM_RULE_FLOOR
   int rule;
   int round_mode;
@@ -50,6 +52,7 @@ struct VerifyArgs {
   int* group_counter;  // packed verify: [G / kVerifyGroupSize], zero between launches
   float* gstate;       // packed verify: [groups][R][3], the merged state of each group
   int* gstate_idx;     // packed verify: [groups][R]
+  RoundEpilogue round;  // packed verify: k > 0 runs the round's epilogue after the last merge
 };
 
 // Online-softmax state of one row: maximum, sum of exp(l - max), sum of exp(l - max) over l > l_own,
@@ -104,7 +107,7 @@ __global__ __launch_bounds__(64 * KW) void own_logit_kernel(VerifyArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = blockIdx.x;
-  const int64_t pid64 = a.pending[r];
+  const int64_t pid64 = r < a.pending_rows ? a.pending[r] : -1;
   if (pid64 < 0 || pid64 >= a.V) {  // not a vocabulary id: no logit, and the row accepts nothing
     if (threadIdx.x == 0) a.own[r] = NAN;
     return;
@@ -336,7 +339,7 @@ template <int DT, int D>
 __global__ __launch_bounds__(64) void verify_packed_own_kernel(VerifyArgs a) {
   const int lane = threadIdx.x;
   const int r = blockIdx.x;
-  const int64_t pid64 = a.pending[r];
+  const int64_t pid64 = r < a.pending_rows ? a.pending[r] : -1;
   if (pid64 < 0 || pid64 >= a.V) {
     if (lane == 0) a.own[r] = NAN;
     return;
@@ -641,10 +644,19 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D
   if (!arrive_last(a.counter, groups)) return;
   gather_states(a.gstate, a.gstate_idx, 0, groups, a.R, grid);
   const RowState t = merge_rows(grid, groups, wave, lane, st_mx, st_se, st_ab, st_ai);
-  if (wave == 0 && lane < a.R) {
-    const int m = lane;
-    a.accept[m] = accept_proposal(a, a.own[m], t) ? 1 : 0;
-    a.argmax[m] = t.ai;
+  if (wave == 0) {
+    const bool acc = lane < a.R && accept_proposal(a, a.own[lane], t);
+    if (lane < a.R) {
+      if (a.accept != nullptr) a.accept[lane] = acc ? 1 : 0;
+      if (a.argmax != nullptr) a.argmax[lane] = t.ai;
+    }
+    if (a.round.k > 0) {
+      // Rows 0..k-1 verify, rows k.. are the proposal blocks: lane i holds row i's decision and
+      // argmax, so hypothesis j is lane k + j's argmax.
+      const int ai = t.ai;
+      const int k = a.round.k;
+      round_epilogue_wave(a.round, lane, acc, [&](int j) { return static_cast<int64_t>(__shfl(ai, k + j)); });
+    }
   }
 }
 
@@ -766,6 +778,7 @@ int plm_lm_head_verify(int32_t dtype, const void* x, int64_t ldx, const void* w,
   a.V = static_cast<int>(V);
   a.K = static_cast<int>(K);
   a.pending = pending;
+  a.pending_rows = static_cast<int>(R);
   a.p = p;
   a.rule = rule;
   a.round_mode = round_mode;
@@ -791,12 +804,16 @@ int plm_lm_head_verify(int32_t dtype, const void* x, int64_t ldx, const void* w,
   return err == hipSuccess ? PLM_OK : PLM_ERR_LAUNCH;
 }
 
-int plm_lm_head_verify_packed(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, int64_t R, int64_t V,
-                              int64_t K, const int64_t* pending, int32_t rule, float p, int32_t round_mode, uint8_t* accept,
-                              int64_t* argmax, const plm_tile* tile, void* workspace, size_t workspace_bytes,
-                              void* stream) {
-  if (x == nullptr || packed_w == nullptr || pending == nullptr || accept == nullptr || argmax == nullptr ||
-      tile == nullptr)
+}  // extern "C"
+
+namespace {
+
+// The packed verify launch behind plm_lm_head_verify_packed and plm_round_verify_packed.
+int packed_verify_entry(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, int64_t R, int64_t V,
+                        int64_t K, const int64_t* pending, int64_t pending_rows, int32_t rule, float p,
+                        int32_t round_mode, uint8_t* accept, int64_t* argmax, const plm::RoundEpilogue& round,
+                        const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream) {
+  if (x == nullptr || packed_w == nullptr || (pending_rows > 0 && pending == nullptr) || tile == nullptr)
     return PLM_ERR_ARGUMENT;
   if (dtype != PLM_BF16 && dtype != PLM_F16) return PLM_ERR_ARGUMENT;
   if (round_mode < PLM_ROUND_F32 || round_mode > PLM_ROUND_F16) return PLM_ERR_ARGUMENT;
@@ -821,11 +838,13 @@ int plm_lm_head_verify_packed(int32_t dtype, const void* x, int64_t ldx, const v
   a.V = static_cast<int>(V);
   a.K = static_cast<int>(K);
   a.pending = pending;
+  a.pending_rows = static_cast<int>(pending_rows);
   a.p = p;
   a.rule = rule;
   a.round_mode = round_mode;
   a.accept = accept;
   a.argmax = argmax;
+  a.round = round;
   char* ws = static_cast<char*>(workspace);
   a.counter = reinterpret_cast<int*>(ws) + plm::kVerifyCounter;
   a.own = reinterpret_cast<float*>(ws + own_off);
@@ -844,6 +863,49 @@ int plm_lm_head_verify_packed(int32_t dtype, const void* x, int64_t ldx, const v
   err = dtype == PLM_BF16 ? plm::verify_packed_dispatch<plm::DT_BF16>(a, *tile, cu, s, false)
                           : plm::verify_packed_dispatch<plm::DT_F16>(a, *tile, cu, s, false);
   return err == hipSuccess ? PLM_OK : PLM_ERR_LAUNCH;
+}
+
+}  // namespace
+
+extern "C" {
+
+int plm_lm_head_verify_packed(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, int64_t R, int64_t V,
+                              int64_t K, const int64_t* pending, int32_t rule, float p, int32_t round_mode, uint8_t* accept,
+                              int64_t* argmax, const plm_tile* tile, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  if (pending == nullptr || accept == nullptr || argmax == nullptr) return PLM_ERR_ARGUMENT;
+  return packed_verify_entry(dtype, x, ldx, packed_w, R, V, K, pending, R, rule, p, round_mode, accept, argmax,
+                             plm::RoundEpilogue{}, tile, workspace, workspace_bytes, stream);
+}
+
+int plm_round_verify_packed(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, int64_t k, int64_t V,
+                            int64_t K, int32_t rule, float p, int32_t round_mode, const int64_t* verify,
+                            int64_t* pending, int64_t* anchor, int64_t* out, int64_t out_len, int64_t* base,
+                            int64_t* offset, int64_t* round_sequence, int64_t sequence_len, int64_t* sequence_step,
+                            uint8_t* accept, int64_t* argmax, uint8_t* accepted, int64_t* num_correct,
+                            const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream) {
+  if (k < 1 || k + k * k > 64 || out_len < 0) return PLM_ERR_ARGUMENT;
+  if (verify == nullptr || anchor == nullptr || out == nullptr || base == nullptr || offset == nullptr)
+    return PLM_ERR_ARGUMENT;
+  if (k > 1 && pending == nullptr) return PLM_ERR_ARGUMENT;
+  if ((round_sequence == nullptr) != (sequence_step == nullptr)) return PLM_ERR_ARGUMENT;
+  if (round_sequence != nullptr && sequence_len < 1) return PLM_ERR_ARGUMENT;
+  plm::RoundEpilogue e{};
+  e.k = static_cast<int>(k);
+  e.verify = verify;
+  e.pending = pending;
+  e.anchor = anchor;
+  e.out = out;
+  e.out_len = out_len;
+  e.base = base;
+  e.offset = offset;
+  e.round_sequence = round_sequence;
+  e.sequence_len = sequence_len;
+  e.sequence_step = sequence_step;
+  e.accepted = accepted;
+  e.num_correct = num_correct;
+  return packed_verify_entry(dtype, x, ldx, packed_w, k + k * k, V, K, pending, k - 1, rule, p, round_mode, accept,
+                             argmax, e, tile, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

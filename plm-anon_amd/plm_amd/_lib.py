@@ -45,6 +45,7 @@ EXPORTS = (
     "plm_lm_head_verify_workspace_bytes",
     "plm_lm_head_verify_packed",
     "plm_round_epilogue",
+    "plm_round_verify_packed",
     "plm_status_string",
 )
 
@@ -119,6 +120,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.plm_round_epilogue.argtypes = [c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_p, c_p, c_p, c_i64, c_p, c_p, c_p,
                                        c_p]
     lib.plm_round_epilogue.restype = ctypes.c_int
+    lib.plm_round_verify_packed.argtypes = [c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i32, ctypes.c_float, c_i32, c_p,
+                                            c_p, c_p, c_p, c_i64, c_p, c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p, tile_p,
+                                            c_p, c_sz, c_p]
+    lib.plm_round_verify_packed.restype = ctypes.c_int
     lib.plm_status_string.argtypes = [c_i32]
     lib.plm_status_string.restype = ctypes.c_char_p
 

@@ -93,6 +93,28 @@ def lm_head_verify(x: torch.Tensor, w: torch.Tensor, pending: torch.Tensor, p: f
     return accept_out, argmax
 
 
+_I64, _U8 = (torch.int64,), (torch.bool, torch.uint8)
+
+
+def _ptr(t: torch.Tensor | None, name: str, n: int, dtypes: tuple, dev: torch.device) -> int:
+    """Device pointer of a contiguous tensor of at least ``n`` entries on ``dev`` (0 for None)."""
+    if t is None:
+        return 0
+    if t.device != dev or t.dtype not in dtypes or not t.is_contiguous() or t.numel() < n:
+        raise ValueError(f"{name} must be a contiguous {dtypes[0]} tensor of >= {n} entries on {dev}")
+    return t.data_ptr()
+
+
+def _state_args(k, verify, pending, anchor, out, base_t, offset_t, round_sequence, sequence_step, dev) -> tuple:
+    """The decoder-state arguments shared by plm_round_epilogue and plm_round_verify_packed, from
+    ``verify`` to ``sequence_step``."""
+    return (_ptr(verify, "verify", k, _I64, dev), _ptr(pending, "pending", k - 1, _I64, dev) if k > 1 else 0,
+            _ptr(anchor, "anchor", 1, _I64, dev), _ptr(out, "out", 0, _I64, dev), out.numel(),
+            _ptr(base_t, "base_t", 1, _I64, dev), _ptr(offset_t, "offset_t", 1, _I64, dev),
+            _ptr(round_sequence, "round_sequence", 1, _I64, dev),
+            0 if round_sequence is None else round_sequence.numel(), _ptr(sequence_step, "sequence_step", 1, _I64, dev))
+
+
 def round_epilogue(k: int, widened: torch.Tensor, hypotheses: torch.Tensor, verify: torch.Tensor,
                    pending: torch.Tensor, anchor: torch.Tensor, out: torch.Tensor, base_t: torch.Tensor,
                    offset_t: torch.Tensor, round_sequence: torch.Tensor | None = None,
@@ -113,22 +135,11 @@ def round_epilogue(k: int, widened: torch.Tensor, hypotheses: torch.Tensor, veri
     if not verify.is_cuda:
         raise RuntimeError("round_epilogue runs on the GPU only; got a CPU tensor")
 
-    def need(t: torch.Tensor | None, name: str, n: int, dtypes: tuple) -> int:
-        if t is None:
-            return 0
-        if t.device != dev or t.dtype not in dtypes or not t.is_contiguous() or t.numel() < n:
-            raise ValueError(f"{name} must be a contiguous {dtypes[0]} tensor of >= {n} entries on {dev}")
-        return t.data_ptr()
-
-    i64, u8 = (torch.int64,), (torch.bool, torch.uint8)
     if (round_sequence is None) != (sequence_step is None):
         raise ValueError("round_sequence and sequence_step go together")
-    args = (need(widened, "widened", k - 1, u8) if k > 1 else 0, need(hypotheses, "hypotheses", k * k, i64),
-            need(verify, "verify", k, i64), need(pending, "pending", k - 1, i64) if k > 1 else 0,
-            need(anchor, "anchor", 1, i64), need(out, "out", 0, i64), out.numel(), need(base_t, "base_t", 1, i64),
-            need(offset_t, "offset_t", 1, i64), need(round_sequence, "round_sequence", 1, i64),
-            0 if round_sequence is None else round_sequence.numel(), need(sequence_step, "sequence_step", 1, i64),
-            need(accepted, "accepted", k - 1, u8), need(num_correct, "num_correct", 1, i64))
+    args = (_ptr(widened, "widened", k - 1, _U8, dev) if k > 1 else 0, _ptr(hypotheses, "hypotheses", k * k, _I64, dev),
+            *_state_args(k, verify, pending, anchor, out, base_t, offset_t, round_sequence, sequence_step, dev),
+            _ptr(accepted, "accepted", k - 1, _U8, dev), _ptr(num_correct, "num_correct", 1, _I64, dev))
     status = _lib.lib().plm_round_epilogue(k, *args, _lib.stream_handle(dev))
     _lib.check(status, f"plm_round_epilogue(k={k})")
 
@@ -136,12 +147,13 @@ def round_epilogue(k: int, widened: torch.Tensor, hypotheses: torch.Tensor, veri
 class RoundVerify:
     """The LM-head end of one round on the device (plm/decoder.py:351-365): one fused verify pass over
     the round's ``k + k*k`` rows (the rule's decisions for verify rows ``0..k-2`` against the pending
-    proposals, the argmax of every row) and ``round_epilogue``. Rows go to the verify kernel in
-    chunks of at most 64 (a round of ``k <= 7`` is one pass over W). Buffers are allocated once, so
-    calls can be captured in a HIP graph."""
+    proposals, the argmax of every row) and the epilogue. With ``fused`` (the default, for rounds of
+    at most 64 rows: k <= 7) both are one launch pair, ``plm_round_verify_packed``, whose last
+    workgroup runs the epilogue; otherwise rows go to the verify kernel in chunks of at most 64 and
+    ``round_epilogue`` follows. Buffers are allocated once, so calls can be captured in a HIP graph."""
 
     def __init__(self, k: int, rule: str = "nucleus", threshold: float = -1.0, round_to: str = "fp32",
-                 device: torch.device | str = "cuda", cfg: Config | None = None):
+                 device: torch.device | str = "cuda", cfg: Config | None = None, fused: bool = True):
         if rule not in RULES or round_to not in ROUND_MODES:
             raise ValueError(f"rule must be one of {sorted(RULES)} and round_to one of {sorted(ROUND_MODES)}")
         if not 1 <= k <= 64:
@@ -151,6 +163,7 @@ class RoundVerify:
         self.rows_pending = torch.full((self.width,), -1, dtype=torch.int64, device=device)
         self.accept = torch.zeros(self.width, dtype=torch.bool, device=device)
         self.argmax = torch.zeros(self.width, dtype=torch.int64, device=device)
+        self.fused = fused and self.width <= 64
 
     def __call__(self, hidden: torch.Tensor, w: torch.Tensor, verify_tokens: torch.Tensor, pending: torch.Tensor,
                  anchor: torch.Tensor, out: torch.Tensor, base_t: torch.Tensor, offset_t: torch.Tensor,
@@ -159,6 +172,10 @@ class RoundVerify:
         k, W = self.k, self.width
         if hidden.dim() != 2 or hidden.shape[0] != W:
             raise ValueError(f"hidden must be [{W}, K] for k={k}, got {tuple(hidden.shape)}")
+        if self.fused:
+            self._fused(hidden, w, verify_tokens, pending, anchor, out, base_t, offset_t, round_sequence,
+                        sequence_step, accepted, num_correct)
+            return
         if k > 1:
             self.rows_pending[: k - 1].copy_(pending)
         for r0 in range(0, W, 64):
@@ -167,3 +184,26 @@ class RoundVerify:
                            accept=self.accept[r0:r1], argmax=self.argmax[r0:r1], rule=self.rule)
         round_epilogue(k, self.accept[: max(k - 1, 0)], self.argmax[k:], verify_tokens, pending, anchor, out, base_t,
                        offset_t, round_sequence, sequence_step, accepted, num_correct)
+
+    def _fused(self, hidden, w, verify_tokens, pending, anchor, out, base_t, offset_t, round_sequence, sequence_step,
+               accepted, num_correct) -> None:
+        k, W = self.k, self.width
+        if hidden.dtype not in HALF_DTYPES or w.dtype != hidden.dtype or hidden.shape[1] != w.shape[1]:
+            raise TypeError(f"RoundVerify needs matching bf16/fp16 operands, got {hidden.dtype} and {w.dtype}")
+        if not (hidden.is_cuda and w.is_cuda):
+            raise RuntimeError("RoundVerify runs on the GPU only; got a CPU tensor")
+        if (round_sequence is None) != (sequence_step is None):
+            raise ValueError("round_sequence and sequence_step go together")
+        dev = hidden.device
+        x = hidden if (hidden.stride(1) == 1 and hidden.stride(0) % 8 == 0) else hidden.contiguous()
+        V, K = w.shape
+        tile = _lib.Tile.from_config(VERIFY_CONFIG if self.cfg is None else self.cfg)
+        lib = _lib.lib()
+        ws = workspace(dev, int(lib.plm_lm_head_verify_workspace_bytes(W, V, K, tile)))
+        status = lib.plm_round_verify_packed(
+            _lib.DTYPE_CODES[x.dtype], x.data_ptr(), x.stride(0), packed_weight(w).data_ptr(), k, V, K,
+            RULES[self.rule], self.threshold, ROUND_MODES[self.round_to],
+            *_state_args(k, verify_tokens, pending, anchor, out, base_t, offset_t, round_sequence, sequence_step, dev),
+            self.accept.data_ptr(), self.argmax.data_ptr(), _ptr(accepted, "accepted", k - 1, _U8, dev),
+            _ptr(num_correct, "num_correct", 1, _I64, dev), tile, ws.data_ptr(), ws.numel(), _lib.stream_handle(dev))
+        _lib.check(status, f"plm_round_verify_packed(k={k}, V={V}, K={K})")

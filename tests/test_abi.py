@@ -101,6 +101,23 @@ def test_epilogue_argument_validation_happens_before_launch():
     assert lib.plm_round_epilogue(7, *full[:10], 0, *full[11:]) == -1
 
 
+def test_round_verify_argument_validation_happens_before_launch():
+    lib = _lib.lib()
+    fake = 1 << 20
+    pt = _lib.Tile(2, 1, 1, 2)
+
+    def call(k, verify=fake, rule=0, seq=fake, seq_len=8):
+        return lib.plm_round_verify_packed(0, fake, 2048, fake, k, 50257, 2048, rule, 0.94, 0, verify, fake, fake, fake,
+                                           100, fake, fake, seq, seq_len, fake, None, None, None, None, pt, fake,
+                                           1 << 30, None)
+
+    assert call(0) == -1 and call(8) == -1          # k + k*k must be within 1..64
+    assert call(7, verify=None) == -1                # no verify tokens
+    assert call(7, rule=3) == -1                     # unknown rule
+    assert call(7, seq=None) == -1                   # a step counter without its sequence
+    assert call(7, seq_len=0) == -1
+
+
 def test_packed_argument_validation_happens_before_launch():
     lib = _lib.lib()
     tile = _lib.Tile(2, 4, 1, 2)

@@ -215,7 +215,8 @@ def _round_inputs(device, k=7, V=workloads.GPT2_VOCAB, K=2048):
     ("nucleus", -1.0, "bf16", [1, 1, 0, 0, 0, 0]),              # exact matching: equality only
     ("floor", 2e-4, "bf16", [1, 1, 0, 1, 1, 1]),
     ("floor", 2e-4, "fp32", [1, 1, 0, 1, 1, 1])])
-def test_round_verify_matches_the_oracle(device, rule, threshold, mode, accepted_bits):
+@pytest.mark.parametrize("fused", [True, False], ids=["fused", "separate"])
+def test_round_verify_matches_the_oracle(device, rule, threshold, mode, accepted_bits, fused):
     k = 7
     x, w, logits, pending, verify = _round_inputs(device, k)
     logits = _rounded(logits, mode)
@@ -223,7 +224,8 @@ def test_round_verify_matches_the_oracle(device, rule, threshold, mode, accepted
         assert (_floor_margin(logits[: k - 1], pending, threshold) > 1e-4).all()
     ref = oracle.epilogue(logits, verify, pending, k, rule, threshold)
     assert ref["accepted"].tolist() == [bool(b) for b in accepted_bits]
-    rv = RoundVerify(k, rule, threshold, mode, device)
+    rv = RoundVerify(k, rule, threshold, mode, device, fused=fused)
+    assert rv.fused == fused
     state = {"pending": pending.to(device), "anchor": torch.zeros(1, dtype=torch.int64, device=device),
              "out": torch.full((32,), -1, dtype=torch.int64, device=device),
              "base_t": torch.zeros((), dtype=torch.int64, device=device),
@@ -278,3 +280,43 @@ def test_round_verify_graph_replays(device):
         rv(x, w, vt, g["pending"].clone(), g["anchor"].clone(), g["out"].clone(), g["base_t"].clone(),
            g["offset_t"].clone())                # eager work between replays, on scratch copies
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("k", [1, 2, 3, 5, 7])
+@pytest.mark.parametrize("rule,threshold", [("nucleus", 0.3), ("floor", 1e-4)])
+def test_fused_round_verify_equals_verify_then_epilogue(device, k, rule, threshold):
+    """plm_round_verify_packed (epilogue in the verify's last workgroup) against lm_head_verify over
+    the round's rows followed by plm_round_epilogue: every state tensor and every row's decision and
+    argmax, bit for bit, over several rounds of random decoder states."""
+    W = k + k * k
+    x, w = _config5(device, R=W, V=20011, K=1024, seed=700 + k)
+    logits = hip_linear_f32(x, w, LOGITS_CONFIG).cpu()
+    g = torch.Generator().manual_seed(800 + k)
+    for rnd in range(4):
+        order = logits[: max(k - 1, 1)].argsort(dim=-1, descending=True, stable=True)
+        ranks = torch.randint(0, 400, (k - 1,), generator=g)
+        pending = order[torch.arange(k - 1), ranks] if k > 1 else torch.zeros(0, dtype=torch.int64)
+        verify = torch.randint(0, 20011, (k,), generator=g)
+        eq = torch.rand(k - 1, generator=g) < 0.3
+        verify[: k - 1] = torch.where(eq, pending, verify[: k - 1])
+        base = int(torch.randint(0, 40, (1,), generator=g))
+        runs = {}
+        for fused in (True, False):
+            st = {"pending": pending.clone().to(device), "anchor": torch.zeros(1, dtype=torch.int64, device=device),
+                  "out": torch.full((64,), -1, dtype=torch.int64, device=device),
+                  "base_t": torch.tensor(base, device=device), "offset_t": torch.tensor(base + 9, device=device),
+                  "round_sequence": torch.zeros(3, dtype=torch.int64, device=device),
+                  "sequence_step": torch.tensor([rnd], device=device)}
+            acc = torch.zeros(max(k - 1, 1), dtype=torch.bool, device=device)
+            nc = torch.full((), -1, dtype=torch.int64, device=device)
+            rv = RoundVerify(k, rule, threshold, "bf16", device, fused=fused)
+            rv(x, w, verify.to(device), st["pending"], st["anchor"], st["out"], st["base_t"], st["offset_t"],
+               st["round_sequence"], st["sequence_step"], acc, nc)
+            torch.cuda.synchronize()
+            runs[fused] = ({n: t.cpu() for n, t in st.items()}, acc.cpu(), int(nc), rv.accept.cpu(), rv.argmax.cpu())
+        (s1, a1, n1, acc1, am1), (s2, a2, n2, acc2, am2) = runs[True], runs[False]
+        for name in s1:
+            assert torch.equal(s1[name], s2[name]), (rnd, name, s1[name], s2[name])
+        assert n1 == n2 and torch.equal(a1[: k - 1], a2[: k - 1])
+        assert torch.equal(am1, am2)
+        assert torch.equal(acc1[: k - 1], acc2[: k - 1])   # rows past k-2 propose nothing in either path
