@@ -211,8 +211,6 @@ def capture_graph(fn):
     return graph
 
 
-# Tile of the packed chained round: 32-row tiles, two-stage pipeline (the fastest measured).
-CHAIN_CFG = {"wave_frags": 2, "k_waves": 8, "split_k": 1, "unroll": 2}
 
 
 class ChainedRound:
@@ -225,9 +223,9 @@ class ChainedRound:
         from plm_amd import _lib
         from plm_amd.chain import Link, LinearChain
         from plm_amd.fast_gemm import _tile
-        from plm_amd.tiles import packed_chain_split
+        from plm_amd.tiles import packed_chain_split, packed_chain_tile
 
-        cfg = dict(CHAIN_CFG)
+        cfg = packed_chain_tile(rnd.M)
         G = _lib.lib().plm_gemm_packed_resident_workgroups(_lib.PLM_BF16, rnd.M, _tile(cfg))
         _lib.check(min(G, 0), "plm_gemm_packed_resident_workgroups")
         n = len(rnd.gemms) - 1
@@ -349,7 +347,7 @@ def main():
                                f"{args.layers} GPT-style blocks + LM head, M={args.M} (k=7)",
                    "M": args.M, "hidden": args.hidden, "mlp": args.mlp, "layers": args.layers,
                    "vocab": GPT2_VOCAB, "gemm_launches": len(gemms), "bytes_per_round": rnd.bytes,
-                   "timing": timing, "chain_tile": CHAIN_CFG},
+                   "timing": timing, "chain_tile": chain.cfg},
         "gbps": round(gbps_value, 1), "pct_of_hbm_peak": round(100.0 * gbps_value / HBM_PEAK_GBPS, 2),
         "chained_round": {"us": round(us_round, 2), "gbps": round(gbps, 1), "launches": 2,
                           "chain_launch_us": round(us_chain, 2)},
@@ -364,7 +362,7 @@ def main():
             # The chained launch is the round's dominant kernel: its HIP-event time per replay (a graph
             # of that launch alone) is its duration.
             kernel = "packed_gemm_kernel<bf16, MT=%d, NF=%d, D=%d, KW=%d> (chained block linears)" % (
-                math.ceil(args.M / 16), CHAIN_CFG["wave_frags"], CHAIN_CFG["unroll"], CHAIN_CFG["k_waves"])
+                math.ceil(args.M / 16), chain.cfg["wave_frags"], chain.cfg["unroll"], chain.cfg["k_waves"])
             achieved = chained.chain_bytes / (us_chain * 1e-6) / 1e9
             result["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                                   "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),

@@ -199,6 +199,15 @@ def chain_tile(M: int) -> dict:
     return dict(CHAIN_TILE)
 
 
+def packed_chain_tile(M: int) -> dict:
+    """Tile of a packed chained round at width M: 32-row tiles of eight wavefronts splitting K, one
+    workgroup per CU. At M > 48 (four X fragments) the two-stage pipeline has that residency; at
+    M <= 48 the two-stage kernel's smaller register count admits two workgroups per CU, which
+    measured slower (1167 against 1025 us for the 1.3B-shape round at M = 42), so the four-stage
+    pipeline is used."""
+    return {"wave_frags": 2, "k_waves": 8, "split_k": 1, "unroll": 2 if M > 48 else 4}
+
+
 def chain_split(N: int, K: int, cfg: dict = CHAIN_TILE, workgroups: int = CU_COUNT) -> int:
     """K split of one linear inside a chain: the smallest power of two that gives about one item
     per resident workgroup, keeping at least two chunks per item."""
