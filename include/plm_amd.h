@@ -271,6 +271,25 @@ int plm_round_verify_packed(int32_t dtype, const void* x, int64_t ldx, const voi
                             uint8_t* accept, int64_t* argmax, uint8_t* accepted, int64_t* num_correct,
                             const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Gated LoRA linear over a packed W (GatedLoraMethod.apply, plm/gated_lora.py:45-57): Y = X W^T for
+ * every row, and for rows m >= gated_from the rank-r correction of the rows that carry the adapter:
+ *   h = round(X[gated_from:] A^T)                 [M - gated_from, shards*rank]  (54)
+ *   Y[m, n] = round(round(X W^T)[m, n] + h[m - gated_from, s*rank .. +rank] . B[n, :])   (55-58)
+ * with A the shards' down-projections stacked ([shards*rank, K], packed by plm_pack_weight), B the
+ * shards' up-projections stacked by output column (lora_b: [N, rank] row-major), and shard s owning
+ * the next shard_sizes[s] output columns (1 <= shards <= 3: a fused q/k/v or gate/up projection;
+ * shards*rank a multiple of 8). Two launches: h into the workspace, then the GEMM (`tile`) with the
+ * correction applied where it stores Y. gated_from >= M is plm_gemm_packed. Workspace:
+ * plm_gemm_packed_lora_workspace_bytes.
+ */
+int plm_gemm_packed_lora(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy,
+                         int64_t M, int64_t N, int64_t K, int64_t gated_from, const void* packed_a, const void* lora_b,
+                         int64_t rank, int32_t shards, const int64_t* shard_sizes, const plm_tile* tile,
+                         void* workspace, size_t workspace_bytes, void* stream);
+size_t plm_gemm_packed_lora_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t gated_from, int64_t rank,
+                                            int32_t shards, const plm_tile* tile);
+
 /* Human-readable name of a status code. */
 const char* plm_status_string(int32_t status);
 

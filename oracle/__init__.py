@@ -16,6 +16,9 @@ Every function cites the reference lines it restates. Pinning (each is checked i
 * ``argmax``                — pinned (ties resolve to the lowest index, brute force).
 * ``verify``                — composition of the two above; pinned through them.
 * ``epilogue``              — pinned (hand-worked rounds: all accepted, none, first rejection).
+* ``gated_lora``            — pinned (fp64 numpy restatement within one output step, no gated row /
+                              zero B reduce to ``linear``, exact small-integer shards, one-hot
+                              shard routing).
 * ``epilogue_state``        — the same bookkeeping with the reference's state writes, from the
                               rule's decisions; ``epilogue`` runs through it, so the hand-worked
                               rounds pin it, plus slot / sequence-capacity cases of its own.
@@ -29,6 +32,8 @@ from .plm_oracle import (  # noqa: F401
     epilogue,
     epilogue_state,
     floor_acceptance,
+    gated_lora,
+    gated_lora_fp64,
     linear,
     linear_fp32,
     linear_fp64,

@@ -34,6 +34,47 @@ def linear_fp64(x: torch.Tensor, w: torch.Tensor) -> np.ndarray:
     return xa @ wa.T
 
 
+# --------------------------------------------------------------------------- gated LoRA
+
+def gated_lora(x: torch.Tensor, w: torch.Tensor, lora_a: torch.Tensor, lora_bs: list[torch.Tensor],
+               first_gated_row: int | None) -> torch.Tensor:
+    """``GatedLoraMethod.apply`` (plm/gated_lora.py:45-57) on CPU copies in the operands' dtype: the base
+    linear over every row; rows from ``first_gated_row`` add ``(x A^T) B_s^T`` into each shard's own
+    output columns (one ``addmm_`` per shard, the hidden product already in the model dtype)."""
+    output = linear(x, w)
+    if first_gated_row is None or first_gated_row >= x.shape[0]:
+        return output
+    hidden = linear(x[first_gated_row:], lora_a)
+    rank = hidden.shape[1] // len(lora_bs)
+    gated = output[first_gated_row:]
+    col = 0
+    for shard, b in enumerate(lora_bs):
+        b = b.cpu()
+        gated[:, col:col + b.shape[0]].addmm_(hidden[:, shard * rank:(shard + 1) * rank], b.t())
+        col += b.shape[0]
+    return output
+
+
+def gated_lora_fp64(x: torch.Tensor, w: torch.Tensor, lora_a: torch.Tensor, lora_bs: list[torch.Tensor],
+                    first_gated_row: int) -> np.ndarray:
+    """Independent numpy version: the base and hidden products exact in fp64 and rounded to the model
+    dtype, the correction added in fp64 and rounded once."""
+    dt = x.dtype
+    rnd = lambda a: torch.from_numpy(a).to(dt).double().numpy()
+    xd, wd, ad = (t.cpu().double().numpy() for t in (x, w, lora_a))
+    out = rnd(xd @ wd.T)
+    g = first_gated_row
+    if g >= xd.shape[0]:
+        return out
+    h = rnd(xd[g:] @ ad.T)
+    rank = h.shape[1] // len(lora_bs)
+    b_cat = np.concatenate([b.cpu().double().numpy() for b in lora_bs], axis=0)
+    shard = np.repeat(np.arange(len(lora_bs)), [b.shape[0] for b in lora_bs])
+    corr = np.stack([h[:, s * rank:(s + 1) * rank] @ b_cat[n] for n, s in enumerate(shard)], axis=1)
+    out[g:] = rnd(out[g:] + corr)
+    return out
+
+
 # --------------------------------------------------------------------------- verify epilogue
 
 def nucleus_acceptance(logits: torch.Tensor, pending: torch.Tensor, nucleus: float) -> torch.Tensor:

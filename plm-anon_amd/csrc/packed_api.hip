@@ -89,6 +89,16 @@ int64_t packed_workspace(int64_t M, int64_t N, const plm_tile& t) {
   return static_cast<int64_t>(kCounterBytes) + packed_tiles(N, t) * t.split_k * tile_fragments(t) * mt * kFragBytes;
 }
 
+// Gated-LoRA launch: the GEMM's own workspace, then the bf16/fp16 h = X[gated_from:] A^T (256-aligned).
+int64_t lora_h_offset(int64_t M, int64_t N, const plm_tile& t) {
+  const int64_t w = std::max<int64_t>(packed_workspace(M, N, t), kCounterBytes);
+  return (w + 255) / 256 * 256;
+}
+
+// The small GEMM that forms h: 16-row tiles of four wavefronts splitting K, two stages (compiled at
+// every width up to 128 rows).
+constexpr plm_tile kLoraDownTile{1, 4, 1, 2};
+
 constexpr int kPackedSpinLimit = 1 << 20;  // polls (each one device round trip) before a wait gives up
 // Counter area of a packed launch: split arrival counters from kPackedArriveBase, progress flags
 // of a chain (an int64 per workgroup) from kPackedBarrierBase.
@@ -123,7 +133,8 @@ int packed_launch_args(int32_t dtype, PackedArgs& a, const plm_tile& t, void* wo
 }
 
 int packed_entry(int32_t dtype, const void* x, int64_t ldx, const void* wp, void* y, int64_t ldy, int64_t M, int64_t N,
-                 int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream, int out_f32) {
+                 int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream, int out_f32,
+                 const PkLora* lora = nullptr) {
   if (!packed_tile_valid(tile)) return PLM_ERR_TILE;
   const plm_tile& t = *tile;
   if (N < 1 || N > (int64_t(1) << 30) || K > (int64_t(1) << 30)) return PLM_ERR_ARGUMENT;
@@ -149,6 +160,7 @@ int packed_entry(int32_t dtype, const void* x, int64_t ldx, const void* wp, void
   a.count = 1;
   a.M = static_cast<int>(M);
   a.G = static_cast<int>(tiles * t.split_k);
+  if (lora != nullptr) a.lora = *lora;
   return packed_launch_args(dtype, a, t, workspace, workspace_bytes, packed_workspace(M, N, t),
                             static_cast<hipStream_t>(stream));
 }
@@ -339,6 +351,54 @@ int plm_gemm_chain_packed(int32_t dtype, const plm_chain_gemm* host_gemms, const
   const int64_t needed = (sync || any_split) ? need : 0;
   return plm::packed_launch_args(dtype, a, *tile, workspace, workspace_bytes, needed,
                                  static_cast<hipStream_t>(stream));
+}
+
+size_t plm_gemm_packed_lora_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t gated_from, int64_t rank,
+                                            int32_t shards, const plm_tile* tile) {
+  (void)K;
+  if (!plm::packed_tile_valid(tile) || M < 1 || N < 1 || rank < 1 || shards < 1) return 0;
+  const int64_t rows = gated_from < M ? M - std::max<int64_t>(gated_from, 0) : 0;
+  return static_cast<size_t>(plm::lora_h_offset(M, N, *tile) + rows * shards * rank * 2);
+}
+
+int plm_gemm_packed_lora(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy, int64_t M,
+                         int64_t N, int64_t K, int64_t gated_from, const void* packed_a, const void* lora_b, int64_t rank,
+                         int32_t shards, const int64_t* shard_sizes, const plm_tile* tile, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  if (gated_from < 0 || rank < 1 || rank > 1024 || shards < 1 || shards > 3 || shard_sizes == nullptr) return PLM_ERR_ARGUMENT;
+  if (gated_from >= M)  // no gated row: the base linear alone (plm/gated_lora.py:47-48)
+    return plm::packed_entry(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, 0);
+  if (packed_a == nullptr || lora_b == nullptr || !plm::packed_tile_valid(tile)) return PLM_ERR_ARGUMENT;
+  const int64_t width = shards * rank;  // h columns
+  if (width % 8 != 0) return PLM_ERR_ARGUMENT;
+  plm::PkLora z{};
+  int64_t end = 0;
+  for (int i = 0; i < 3; ++i) z.shard_end[i] = static_cast<int>(N);
+  for (int32_t i = 0; i < shards; ++i) {
+    if (shard_sizes[i] < 1) return PLM_ERR_ARGUMENT;
+    end += shard_sizes[i];
+    if (i + 1 < shards) z.shard_end[i] = static_cast<int>(end);
+  }
+  if (end != N) return PLM_ERR_ARGUMENT;
+  if ((reinterpret_cast<uintptr_t>(lora_b) & 15) != 0) return PLM_ERR_ALIGNMENT;
+  const int64_t h_off = plm::lora_h_offset(M, N, *tile);
+  const int64_t rows = M - gated_from;
+  if (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < h_off + rows * width * 2 ||
+      (reinterpret_cast<uintptr_t>(workspace) & 15) != 0)
+    return PLM_ERR_WORKSPACE;
+  void* h = static_cast<char*>(workspace) + h_off;
+  // h = X[gated_from:] A^T in the model dtype, as the reference's second GEMM returns it (54).
+  const plm_tile down = plm::kLoraDownTile;
+  const void* xg = static_cast<const char*>(x) + gated_from * ldx * 2;
+  int status = plm::packed_entry(dtype, xg, ldx, packed_a, h, width, rows, width, K, &down, workspace, workspace_bytes,
+                                 stream, 0);
+  if (status != PLM_OK) return status;
+  z.h = static_cast<const uint16_t*>(h);
+  z.b = static_cast<const uint16_t*>(lora_b);
+  z.ldh = static_cast<int>(width);
+  z.rank = static_cast<int>(rank);
+  z.gated_from = static_cast<int>(gated_from);
+  return plm::packed_entry(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, 0, &z);
 }
 
 }  // extern "C"

@@ -51,6 +51,16 @@ __device__ __forceinline__ uint16_t to_bits16(float v) {
   }
 }
 
+// 16-bit storage -> fp32 (exact).
+template <int DT>
+__device__ __forceinline__ float from_bits16(uint16_t h) {
+  if constexpr (DT == DT_BF16) {
+    return __builtin_bit_cast(float, static_cast<uint32_t>(h) << 16);
+  } else {
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+  }
+}
+
 __device__ __forceinline__ float round_through(float v, int mode) {
   if (mode == 1) return static_cast<float>(static_cast<__bf16>(v));
   if (mode == 2) return static_cast<float>(static_cast<_Float16>(v));

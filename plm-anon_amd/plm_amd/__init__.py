@@ -9,5 +9,5 @@
 All compute runs in ``libplm_amd.so`` (hand-written HIP kernels, C ABI in ``include/plm_amd.h``).
 """
 
-from . import fast_gemm, gemm_tables, verify, workloads  # noqa: F401
+from . import fast_gemm, gated_lora, gemm_tables, verify, workloads  # noqa: F401
 from ._lib import LIBRARY, lib  # noqa: F401

@@ -46,6 +46,8 @@ EXPORTS = (
     "plm_lm_head_verify_packed",
     "plm_round_epilogue",
     "plm_round_verify_packed",
+    "plm_gemm_packed_lora",
+    "plm_gemm_packed_lora_workspace_bytes",
     "plm_status_string",
 )
 
@@ -124,6 +126,11 @@ def _declare(lib: ctypes.CDLL) -> None:
                                             c_p, c_p, c_p, c_i64, c_p, c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p, tile_p,
                                             c_p, c_sz, c_p]
     lib.plm_round_verify_packed.restype = ctypes.c_int
+    lib.plm_gemm_packed_lora.argtypes = [c_i32, c_p, c_i64, c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_i64, c_p, c_p, c_i64,
+                                         c_i32, c_p, tile_p, c_p, c_sz, c_p]
+    lib.plm_gemm_packed_lora.restype = ctypes.c_int
+    lib.plm_gemm_packed_lora_workspace_bytes.argtypes = [c_i64, c_i64, c_i64, c_i64, c_i64, c_i32, tile_p]
+    lib.plm_gemm_packed_lora_workspace_bytes.restype = c_sz
     lib.plm_status_string.argtypes = [c_i32]
     lib.plm_status_string.restype = ctypes.c_char_p
 

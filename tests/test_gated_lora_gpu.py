@@ -1,0 +1,114 @@
+"""GPU parity of the gated-LoRA linear (plm_gemm_packed_lora, GatedLoraMethod.apply at
+plm/gated_lora.py:45-57) against the oracle's restatement of the reference's unfused composition.
+
+Shapes are the reference's Llama-style fused projections at the round width M = 56 with the gate at
+k = 7 (verify rows 0..6 plain, rows 7.. adapted): QKV 2048 -> 2048+512+512 (three shards), gate/up
+2048 -> 5632+5632 (two), attention-out (one), and down with a split-K tile. Parity: within 1e-3
+relative / 2e-2 absolute of the oracle, or at most two output rounding steps away (the base product
+and the final sum each round to bf16, and either can land on the other side of a rounding midpoint
+from the oracle's), for at most 0.5 % of the elements; rows before the gate bit for bit the plain
+packed GEMM."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle
+from plm_amd.fast_gemm import hip_linear
+from plm_amd.gated_lora import GatedLoraMethod, gated_linear, rows_from
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-3, 2e-2
+
+
+def _operands(M, shards, K, rank, seed, device, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    N = sum(shards)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    w = (0.02 * torch.randn(N, K, generator=g)).to(dtype)
+    a = (0.05 * torch.randn(len(shards) * rank, K, generator=g)).to(dtype)
+    bs = [(0.5 * torch.randn(n, rank, generator=g)).to(dtype) for n in shards]
+    return x, w, a, bs, (x.to(device), w.to(device), a.to(device), [b.to(device) for b in bs])
+
+
+def _check(got: torch.Tensor, ref: torch.Tensor, dtype=torch.bfloat16):
+    got, ref = got.cpu().float(), ref.float()
+    diff = (got - ref).abs()
+    in_tol = diff <= ATOL + RTOL * ref.abs()
+    bits = 8 if dtype == torch.bfloat16 else 11
+    step = 2.0 ** (torch.floor(torch.log2(ref.abs().clamp_min(2.0 ** -14))) - (bits - 1))
+    assert bool((in_tol | (diff <= 2 * step * 1.0001)).all()), f"max |got - oracle| {diff.max():.4g}"
+    assert int((~in_tol).sum()) <= max(1, got.numel() // 200), int((~in_tol).sum())
+
+
+CASES = {
+    "qkv": ((2048, 512, 512), 2048, 16, {"wave_frags": 2, "k_waves": 8, "split_k": 1, "unroll": 2}),
+    "gate_up": ((5632, 5632), 2048, 16, {"wave_frags": 4, "k_waves": 8, "split_k": 1, "unroll": 2}),
+    "o": ((2048,), 2048, 32, {"wave_frags": 2, "k_waves": 8, "split_k": 4, "unroll": 2}),
+    "down_rowsplit": ((2048,), 5632, 16, {"wave_frags": 2, "k_waves": 1, "split_k": 2, "unroll": 4}),
+}
+
+
+@pytest.mark.parametrize("name", list(CASES))
+@pytest.mark.parametrize("gate", [7, 0, 55])
+def test_gated_linear_matches_the_reference_composition(device, name, gate):
+    shards, K, rank, cfg = CASES[name]
+    x, w, a, bs, (xg, wg, ag, bsg) = _operands(56, shards, K, rank, 10 + len(name) + gate, device)
+    got = gated_linear(xg, wg, ag, bsg, gate, cfg=cfg)
+    ref = oracle.gated_lora(x, w, a, bs, gate)
+    _check(got, ref)
+    # Rows before the gate: the plain linear with the same tile, bit for bit.
+    base = hip_linear(xg, wg, cfg)
+    assert torch.equal(got[:gate], base[:gate])
+    # The correction is real: rows from the gate differ from the base.
+    assert not torch.equal(got[gate:], base[gate:])
+
+
+def test_no_gated_rows_is_the_plain_linear(device):
+    shards, K, rank, cfg = CASES["qkv"]
+    _, _, _, _, (xg, wg, ag, bsg) = _operands(56, shards, K, rank, 3, device)
+    from plm_amd import fast_gemm
+
+    fast_gemm.install({(56, sum(shards), K): cfg})
+    try:
+        assert torch.equal(gated_linear(xg, wg, ag, bsg, 56), hip_linear(xg, wg, cfg))
+        assert torch.equal(gated_linear(xg, wg, ag, bsg, None), hip_linear(xg, wg, cfg))
+    finally:
+        fast_gemm.uninstall()
+
+
+def test_fp16_and_narrow_rounds(device):
+    for M, gate in ((7, 1), (42, 6), (20, 3)):
+        x, w, a, bs, (xg, wg, ag, bsg) = _operands(M, (1024, 256, 256), 1024, 8, M, device, torch.float16)
+        cfg = {"wave_frags": 2, "k_waves": 4, "split_k": 1, "unroll": 4}
+        got = gated_linear(xg, wg, ag, bsg, gate, cfg=cfg)
+        _check(got, oracle.gated_lora(x, w, a, bs, gate), torch.float16)
+
+
+def test_method_wrapper_routes_through_rows_from(device):
+    """GatedLoraMethod.apply: outside rows_from the inner method runs; inside, the gated linear."""
+    shards, K, rank, cfg = CASES["gate_up"]
+    x, w, a, bs, (xg, wg, ag, bsg) = _operands(56, shards, K, rank, 21, device)
+
+    class Inner:
+        def apply(self, layer, x, bias=None):
+            return hip_linear(x, layer.weight, cfg)
+
+    layer = torch.nn.Module()
+    layer.weight = torch.nn.Parameter(wg, requires_grad=False)
+    layer.register_buffer("lora_a", ag)
+    method = GatedLoraMethod(Inner(), bsg)
+    from plm_amd import fast_gemm
+
+    fast_gemm.install({(56, sum(shards), K): cfg})
+    try:
+        plain = method.apply(layer, xg)
+        with rows_from(7):
+            gated = method.apply(layer, xg)
+    finally:
+        fast_gemm.uninstall()
+    assert torch.equal(plain, hip_linear(xg, wg, cfg))
+    _check(gated, oracle.gated_lora(x, w, a, bs, 7))
+    assert torch.equal(gated[:7], plain[:7])

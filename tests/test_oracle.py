@@ -239,6 +239,60 @@ def test_epilogue_state_single_proposal_round():
     assert st["pending"].numel() == 0 and int(st["base_t"]) == 3 and st["anchor"].tolist() == [42]
 
 
+# --------------------------------------------------------------------------- gated LoRA
+
+
+def _lora_operands(M, shards, K, rank, seed, dtype=torch.bfloat16, scale=0.05):
+    g = torch.Generator().manual_seed(seed)
+    N = sum(shards)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    w = (0.02 * torch.randn(N, K, generator=g)).to(dtype)
+    a = (scale * torch.randn(len(shards) * rank, K, generator=g)).to(dtype)
+    bs = [(scale * torch.randn(n, rank, generator=g)).to(dtype) for n in shards]
+    return x, w, a, bs
+
+
+def test_gated_lora_matches_fp64_restatement():
+    x, w, a, bs = _lora_operands(21, (96, 32, 32), 256, 8, 3)
+    got = oracle.gated_lora(x, w, a, bs, 5).float().numpy()
+    ref = po.gated_lora_fp64(x, w, a, bs, 5)
+    step = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -14))) - 7)
+    assert np.all(np.abs(got - ref) <= step * 1.0001)
+    assert np.mean(np.abs(got - ref) > 0) < 0.02
+    assert not np.array_equal(got[5:], oracle.linear(x, w).float().numpy()[5:])   # the correction is there
+
+
+def test_gated_lora_without_gated_rows_or_with_zero_b_is_the_linear():
+    x, w, a, bs = _lora_operands(12, (64,), 128, 4, 4)
+    base = oracle.linear(x, w)
+    assert torch.equal(oracle.gated_lora(x, w, a, bs, None), base)
+    assert torch.equal(oracle.gated_lora(x, w, a, bs, 12), base)
+    assert torch.equal(oracle.gated_lora(x, w, a, [torch.zeros_like(b) for b in bs], 0), base)
+
+
+def test_gated_lora_small_integers_are_exact_per_shard():
+    """Small-integer operands make every product exact: the result is integer arithmetic, and each
+    shard's columns use that shard's slice of the hidden product (a one-hot A per shard)."""
+    g = torch.Generator().manual_seed(5)
+    M, K, rank, shards = 6, 16, 2, (8, 4, 4)
+    x = torch.randint(-2, 3, (M, K), generator=g).to(torch.bfloat16)
+    w = torch.randint(-2, 3, (sum(shards), K), generator=g).to(torch.bfloat16)
+    a = torch.zeros(len(shards) * rank, K)
+    for r in range(a.shape[0]):
+        a[r, r] = 1.0                      # hidden column r = x[:, r]
+    a = a.to(torch.bfloat16)
+    bs = [torch.randint(-2, 3, (n, rank), generator=g).to(torch.bfloat16) for n in shards]
+    got = oracle.gated_lora(x, w, a, bs, 2).to(torch.int64)
+    xi, wi = x.to(torch.int64), w.to(torch.int64)
+    ref = xi @ wi.T
+    col = 0
+    for s_, b in enumerate(bs):
+        h = xi[2:, s_ * rank:(s_ + 1) * rank]
+        ref[2:, col:col + b.shape[0]] += h @ b.to(torch.int64).T
+        col += b.shape[0]
+    assert torch.equal(got, ref)
+
+
 # --------------------------------------------------------------------------- planted mistakes
 
 
