@@ -392,6 +392,7 @@ def main():
             result["verify"] = time_verify(weights[-1], args.hidden, device, args.steps)
         if not args.no_llama:
             result["llama_rounds"] = time_llama_rounds(args, device)
+            result["gated_lora"] = time_gated_lora(args, device)
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_baseline(args.hidden, args.mlp, args.M, args.cpu_seconds)
     print(json.dumps(result), flush=True)
@@ -466,6 +467,56 @@ def time_llama_rounds(args, device):
         del rnd, chained, weights, chain_outs
         torch.cuda.empty_cache()
     return out
+
+
+def time_gated_lora(args, device):
+    """Gated LoRA on the Llama-style 1.3B fused QKV (2048 -> 2048+512+512, rank 16, gate at k = 7):
+    the fused two-launch form (plm_gemm_packed_lora) against the same GEMMs as the reference composes
+    them (base GEMM, hidden GEMM, one addmm per shard; the GEMMs on this build's kernel), graphs
+    rotating enough weight copies that each call streams its weight from HBM."""
+    import torch
+
+    from plm_amd import gemm_tables
+    from plm_amd.fast_gemm import hip_linear
+    from plm_amd.gated_lora import gated_linear
+
+    M, K, shards, rank, gate = args.M, 2048, (2048, 512, 512), 16, 7
+    N = sum(shards)
+    cfg = gemm_tables.read_table(K)[(M, N, K)]
+    gen = torch.Generator(device=device).manual_seed(77)
+    x = torch.randn(M, K, generator=gen, device=device).bfloat16()
+    sets = []
+    for _ in range(20):   # 20 x 12.6 MB > 256 MB
+        w = (0.02 * torch.randn(N, K, generator=gen, device=device)).bfloat16()
+        a = (0.05 * torch.randn(len(shards) * rank, K, generator=gen, device=device)).bfloat16()
+        bs = [(0.5 * torch.randn(n, rank, generator=gen, device=device)).bfloat16() for n in shards]
+        sets.append((w, a, bs))
+    down_cfg = {"wave_frags": 1, "k_waves": 4, "split_k": 1, "unroll": 2}
+
+    def composed(w, a, bs):
+        out = hip_linear(x, w, cfg)
+        hidden = hip_linear(x[gate:], a, down_cfg)
+        col = 0
+        for s_, b in enumerate(bs):
+            out[gate:, col:col + b.shape[0]].addmm_(hidden[:, s_ * rank:(s_ + 1) * rank], b.t().contiguous())
+            col += b.shape[0]
+        return out
+
+    res = {}
+    for name, fn in (("fused_us", lambda w, a, bs: gated_linear(x, w, a, bs, gate, cfg=cfg)), ("composed_us", composed),
+                     ("base_gemm_us", lambda w, a, bs: hip_linear(x, w, cfg))):
+        for st in sets:
+            fn(*st)
+        torch.cuda.synchronize()
+        stream = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for st in sets:
+                fn(*st)
+        res[name] = round(time_graph(graph, max(5, args.steps // 4), 2) * 1000.0 / len(sets), 2)
+        del graph
+    print(f"[bench] gated LoRA qkv: {res}", file=sys.stderr, flush=True)
+    return dict(res, shape=f"M={M} N={N} K={K} rank={rank} shards={list(shards)} gate={gate}")
 
 
 def time_verify(w_lm, hidden, device, steps):

@@ -89,15 +89,17 @@ int64_t packed_workspace(int64_t M, int64_t N, const plm_tile& t) {
   return static_cast<int64_t>(kCounterBytes) + packed_tiles(N, t) * t.split_k * tile_fragments(t) * mt * kFragBytes;
 }
 
-// Gated-LoRA launch: the GEMM's own workspace, then the bf16/fp16 h = X[gated_from:] A^T (256-aligned).
-int64_t lora_h_offset(int64_t M, int64_t N, const plm_tile& t) {
-  const int64_t w = std::max<int64_t>(packed_workspace(M, N, t), kCounterBytes);
+// The small GEMM that forms h: 16-row tiles of eight wavefronts splitting K, four K splits (a few
+// dozen workgroups for a fused projection's shards*rank rows), two stages.
+constexpr plm_tile kLoraDownTile{1, 8, 4, 2};
+
+// Gated-LoRA launch: the larger of the two GEMMs' workspaces (they run one after the other), then
+// the model-dtype h = X[gated_from:] A^T (256-aligned).
+int64_t lora_h_offset(int64_t M, int64_t N, int64_t rows, int64_t width, const plm_tile& t) {
+  const int64_t w = std::max<int64_t>(std::max(packed_workspace(M, N, t), packed_workspace(rows, width, kLoraDownTile)),
+                                      kCounterBytes);
   return (w + 255) / 256 * 256;
 }
-
-// The small GEMM that forms h: 16-row tiles of four wavefronts splitting K, two stages (compiled at
-// every width up to 128 rows).
-constexpr plm_tile kLoraDownTile{1, 4, 1, 2};
 
 constexpr int kPackedSpinLimit = 1 << 20;  // polls (each one device round trip) before a wait gives up
 // Counter area of a packed launch: split arrival counters from kPackedArriveBase, progress flags
@@ -358,19 +360,19 @@ size_t plm_gemm_packed_lora_workspace_bytes(int64_t M, int64_t N, int64_t K, int
   (void)K;
   if (!plm::packed_tile_valid(tile) || M < 1 || N < 1 || rank < 1 || shards < 1) return 0;
   const int64_t rows = gated_from < M ? M - std::max<int64_t>(gated_from, 0) : 0;
-  return static_cast<size_t>(plm::lora_h_offset(M, N, *tile) + rows * shards * rank * 2);
+  return static_cast<size_t>(plm::lora_h_offset(M, N, rows, shards * rank, *tile) + rows * shards * rank * 2);
 }
 
 int plm_gemm_packed_lora(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy, int64_t M,
                          int64_t N, int64_t K, int64_t gated_from, const void* packed_a, const void* lora_b, int64_t rank,
                          int32_t shards, const int64_t* shard_sizes, const plm_tile* tile, void* workspace,
                          size_t workspace_bytes, void* stream) {
-  if (gated_from < 0 || rank < 1 || rank > 1024 || shards < 1 || shards > 3 || shard_sizes == nullptr) return PLM_ERR_ARGUMENT;
+  if (gated_from < 0 || rank < 8 || rank > 1024 || rank % 8 != 0 || shards < 1 || shards > 3 || shard_sizes == nullptr)
+    return PLM_ERR_ARGUMENT;
   if (gated_from >= M)  // no gated row: the base linear alone (plm/gated_lora.py:47-48)
     return plm::packed_entry(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, 0);
   if (packed_a == nullptr || lora_b == nullptr || !plm::packed_tile_valid(tile)) return PLM_ERR_ARGUMENT;
   const int64_t width = shards * rank;  // h columns
-  if (width % 8 != 0) return PLM_ERR_ARGUMENT;
   plm::PkLora z{};
   int64_t end = 0;
   for (int i = 0; i < 3; ++i) z.shard_end[i] = static_cast<int>(N);
@@ -381,8 +383,8 @@ int plm_gemm_packed_lora(int32_t dtype, const void* x, int64_t ldx, const void* 
   }
   if (end != N) return PLM_ERR_ARGUMENT;
   if ((reinterpret_cast<uintptr_t>(lora_b) & 15) != 0) return PLM_ERR_ALIGNMENT;
-  const int64_t h_off = plm::lora_h_offset(M, N, *tile);
   const int64_t rows = M - gated_from;
+  const int64_t h_off = plm::lora_h_offset(M, N, rows, width, *tile);
   if (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < h_off + rows * width * 2 ||
       (reinterpret_cast<uintptr_t>(workspace) & 15) != 0)
     return PLM_ERR_WORKSPACE;

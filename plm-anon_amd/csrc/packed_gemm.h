@@ -323,6 +323,19 @@ __device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t xr, const PCursor
 // The gated correction of Y[m, n..n+3] (m >= gated_from): the base value rounded to the model dtype
 // first, as the reference's base GEMM output is, then the rank-r product added in fp32.
 template <int DT>
+__device__ __forceinline__ float dot8(u32x4 a, u32x4 b, float acc) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    acc += from_bits16<DT>(static_cast<uint16_t>(a[w] & 0xffffu)) * from_bits16<DT>(static_cast<uint16_t>(b[w] & 0xffffu));
+    acc += from_bits16<DT>(static_cast<uint16_t>(a[w] >> 16)) * from_bits16<DT>(static_cast<uint16_t>(b[w] >> 16));
+  }
+  return acc;
+}
+
+// The gated correction of Y[m, n..n+3] (m >= gated_from): the base value rounded to the model dtype
+// first, as the reference's base GEMM output is, then the rank-r product added in fp32. rank is a
+// multiple of 8, so h and B rows are read 16 bytes at a time (independent loads, issued together).
+template <int DT>
 __device__ __forceinline__ f32x4 lora_correct(const PLinear& L, int m, int n, f32x4 v) {
   const PkLora& z = L.lora;
   const uint16_t* hrow = z.h + static_cast<int64_t>(m - z.gated_from) * z.ldh;
@@ -331,11 +344,11 @@ __device__ __forceinline__ f32x4 lora_correct(const PLinear& L, int m, int n, f3
     const int c = n + i;
     if (c >= L.N) continue;
     const int s = (c >= z.shard_end[0]) + (c >= z.shard_end[1]) + (c >= z.shard_end[2]);  // shard of column c
-    const uint16_t* hs = hrow + s * z.rank;
-    const uint16_t* br = z.b + static_cast<int64_t>(c) * z.rank;
+    const u32x4* hs = reinterpret_cast<const u32x4*>(hrow + s * z.rank);
+    const u32x4* br = reinterpret_cast<const u32x4*>(z.b + static_cast<int64_t>(c) * z.rank);
     float acc = 0.f;
-#pragma unroll 1
-    for (int j = 0; j < z.rank; ++j) acc += from_bits16<DT>(hs[j]) * from_bits16<DT>(br[j]);
+#pragma unroll 4
+    for (int j = 0; j < z.rank / 8; ++j) acc = dot8<DT>(hs[j], br[j], acc);
     v[i] = from_bits16<DT>(to_bits16<DT>(v[i])) + acc;
   }
   return v;

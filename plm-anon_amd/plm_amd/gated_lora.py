@@ -72,7 +72,7 @@ def gated_linear(x: torch.Tensor, weight: torch.Tensor, lora_a: torch.Tensor, lo
     rank = lora_a.shape[0] // shards
     eligible = (cfg is not None and bias is None and x.dim() == 2 and x.dtype in HALF_DTYPES and
                 weight.dtype == x.dtype and lora_a.dtype == x.dtype and all(b.dtype == x.dtype for b in lora_bs) and
-                x.is_cuda and 1 <= shards <= 3 and lora_a.shape[0] == shards * rank and (shards * rank) % 8 == 0 and
+                x.is_cuda and 1 <= shards <= 3 and lora_a.shape[0] == shards * rank and rank % 8 == 0 and
                 all(b.shape[1] == rank for b in lora_bs) and sum(b.shape[0] for b in lora_bs) == weight.shape[0])
     if not eligible:
         gemm = dispatch_unquantized_gemm()
