@@ -279,8 +279,8 @@ int plm_round_verify_packed(int32_t dtype, const void* x, int64_t ldx, const voi
  * with A the shards' down-projections stacked ([shards*rank, K], packed by plm_pack_weight), B the
  * shards' up-projections stacked by output column (lora_b: [N, rank] row-major), and shard s owning
  * the next shard_sizes[s] output columns (1 <= shards <= 3: a fused q/k/v or gate/up projection;
- * rank a multiple of 8; lora_b 16-byte aligned). Two launches: h into the workspace, then the GEMM (`tile`) with the
- * correction applied where it stores Y. gated_from >= M is plm_gemm_packed. Workspace:
+ * rank a multiple of 8; lora_b 16-byte aligned). Three launches: h into the workspace, the base GEMM
+ * (`tile`), then the gated rows' correction in place. gated_from >= M is plm_gemm_packed. Workspace:
  * plm_gemm_packed_lora_workspace_bytes.
  */
 int plm_gemm_packed_lora(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy,

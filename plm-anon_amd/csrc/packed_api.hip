@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <vector>
 
+#include "lora.h"
 #include "packed_gemm.h"
 #include "plm_amd.h"
 
@@ -135,8 +136,7 @@ int packed_launch_args(int32_t dtype, PackedArgs& a, const plm_tile& t, void* wo
 }
 
 int packed_entry(int32_t dtype, const void* x, int64_t ldx, const void* wp, void* y, int64_t ldy, int64_t M, int64_t N,
-                 int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream, int out_f32,
-                 const PkLora* lora = nullptr) {
+                 int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream, int out_f32) {
   if (!packed_tile_valid(tile)) return PLM_ERR_TILE;
   const plm_tile& t = *tile;
   if (N < 1 || N > (int64_t(1) << 30) || K > (int64_t(1) << 30)) return PLM_ERR_ARGUMENT;
@@ -162,7 +162,6 @@ int packed_entry(int32_t dtype, const void* x, int64_t ldx, const void* wp, void
   a.count = 1;
   a.M = static_cast<int>(M);
   a.G = static_cast<int>(tiles * t.split_k);
-  if (lora != nullptr) a.lora = *lora;
   return packed_launch_args(dtype, a, t, workspace, workspace_bytes, packed_workspace(M, N, t),
                             static_cast<hipStream_t>(stream));
 }
@@ -373,7 +372,7 @@ int plm_gemm_packed_lora(int32_t dtype, const void* x, int64_t ldx, const void* 
     return plm::packed_entry(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, 0);
   if (packed_a == nullptr || lora_b == nullptr || !plm::packed_tile_valid(tile)) return PLM_ERR_ARGUMENT;
   const int64_t width = shards * rank;  // h columns
-  plm::PkLora z{};
+  plm::LoraArgs z{};
   int64_t end = 0;
   for (int i = 0; i < 3; ++i) z.shard_end[i] = static_cast<int>(N);
   for (int32_t i = 0; i < shards; ++i) {
@@ -395,12 +394,20 @@ int plm_gemm_packed_lora(int32_t dtype, const void* x, int64_t ldx, const void* 
   int status = plm::packed_entry(dtype, xg, ldx, packed_a, h, width, rows, width, K, &down, workspace, workspace_bytes,
                                  stream, 0);
   if (status != PLM_OK) return status;
+  // Y = X W^T for every row (the reference's base output, in the model dtype), then the gated rows'
+  // correction in place.
+  status = plm::packed_entry(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, 0);
+  if (status != PLM_OK) return status;
+  z.y = static_cast<uint16_t*>(y);
+  z.ldy = ldy;
   z.h = static_cast<const uint16_t*>(h);
   z.b = static_cast<const uint16_t*>(lora_b);
   z.ldh = static_cast<int>(width);
   z.rank = static_cast<int>(rank);
   z.gated_from = static_cast<int>(gated_from);
-  return plm::packed_entry(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, 0, &z);
+  z.M = static_cast<int>(M);
+  z.N = static_cast<int>(N);
+  return plm::lora_apply(dtype, z, static_cast<hipStream_t>(stream)) == hipSuccess ? PLM_OK : PLM_ERR_LAUNCH;
 }
 
 }  // extern "C"

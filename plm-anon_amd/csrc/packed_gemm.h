@@ -66,17 +66,6 @@ constexpr int kPkMaxWorkgroups = 2048;  // progress flags: int64 per workgroup a
 // and values only grow, so no flag needs clearing.
 constexpr int kPkTileFlags = 1024;
 
-// Gated low-rank correction of a single linear (plm/gated_lora.py:45-57): rows m >= gated_from of Y
-// become round(round(X W^T)[m, n] + sum_j h[m - gated_from, s*rank + j] * B[n, j]) with s the shard
-// holding column n, h = X[gated_from:] A^T (in the model dtype) and B the shards' up-projections
-// stacked by output column. h == nullptr: no correction.
-struct PkLora {
-  const uint16_t* h;  // [M - gated_from][ldh]
-  const uint16_t* b;  // [N][rank]
-  int ldh, rank, gated_from;
-  int shard_end[3];   // exclusive column ends of the first three shards, ascending (N past the last)
-};
-
 struct PackedArgs {
   const plm_chain_gemm* chain;  // device array of `count` linears, or nullptr: use `single`
   plm_chain_gemm single;
@@ -89,7 +78,6 @@ struct PackedArgs {
   int spin_limit;  // polls before a wait gives up
   int* counters;
   float* partial;
-  PkLora lora;     // single linear only
 };
 
 __device__ __forceinline__ int sgpr(int v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -116,7 +104,6 @@ struct PLinear {
   float* partial;  // split partials
   int64_t* flag;   // sync == 2 and consumed: this linear's tile-done flags (else nullptr)
   int64_t flag_value;  // the value they get: ((epoch + 1) << 16) + seq
-  PkLora lora;     // the single linear's gated correction (h == nullptr: none)
 };
 
 // Wavefronts per workgroup: KW for the K-split layouts, four for the row-split one.
@@ -180,8 +167,6 @@ __device__ __forceinline__ PLinear load_linear(const PackedArgs& a, int gi, int6
                ? reinterpret_cast<int64_t*>(a.counters + kPackedBarrierBase) + (L.seq & 1) * kPkTileFlags
                : nullptr;
   L.flag_value = ((epoch + 1) << 16) + L.seq;
-  L.lora = a.lora;
-  if (a.chain != nullptr) L.lora.h = nullptr;
   return L;
 }
 
@@ -320,40 +305,6 @@ __device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t xr, const PCursor
 
 // Four columns n..n+3 of Y row m (fewer at N's end); written through to the device-coherent level
 // when a later linear of the chain reads this Y.
-// The gated correction of Y[m, n..n+3] (m >= gated_from): the base value rounded to the model dtype
-// first, as the reference's base GEMM output is, then the rank-r product added in fp32.
-template <int DT>
-__device__ __forceinline__ float dot8(u32x4 a, u32x4 b, float acc) {
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    acc += from_bits16<DT>(static_cast<uint16_t>(a[w] & 0xffffu)) * from_bits16<DT>(static_cast<uint16_t>(b[w] & 0xffffu));
-    acc += from_bits16<DT>(static_cast<uint16_t>(a[w] >> 16)) * from_bits16<DT>(static_cast<uint16_t>(b[w] >> 16));
-  }
-  return acc;
-}
-
-// The gated correction of Y[m, n..n+3] (m >= gated_from): the base value rounded to the model dtype
-// first, as the reference's base GEMM output is, then the rank-r product added in fp32. rank is a
-// multiple of 8, so h and B rows are read 16 bytes at a time (independent loads, issued together).
-template <int DT>
-__device__ __forceinline__ f32x4 lora_correct(const PLinear& L, int m, int n, f32x4 v) {
-  const PkLora& z = L.lora;
-  const uint16_t* hrow = z.h + static_cast<int64_t>(m - z.gated_from) * z.ldh;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c = n + i;
-    if (c >= L.N) continue;
-    const int s = (c >= z.shard_end[0]) + (c >= z.shard_end[1]) + (c >= z.shard_end[2]);  // shard of column c
-    const u32x4* hs = reinterpret_cast<const u32x4*>(hrow + s * z.rank);
-    const u32x4* br = reinterpret_cast<const u32x4*>(z.b + static_cast<int64_t>(c) * z.rank);
-    float acc = 0.f;
-#pragma unroll 4
-    for (int j = 0; j < z.rank / 8; ++j) acc = dot8<DT>(hs[j], br[j], acc);
-    v[i] = from_bits16<DT>(to_bits16<DT>(v[i])) + acc;
-  }
-  return v;
-}
-
 template <int DT>
 __device__ __forceinline__ void packed_store4(const PLinear& L, int m, int n, f32x4 v) {
   const int left = L.N - n;
@@ -393,10 +344,7 @@ __device__ __forceinline__ void packed_store_frag(const PLinear& L, int M, int n
   const int f = q / MT, t = q - f * MT;
   const int m = 16 * t + (lane & 15);
   const int n = n0 + 16 * f + 4 * (lane >> 4);
-  if (m < M && n < L.N) {
-    if (L.lora.h != nullptr && m >= L.lora.gated_from) v = lora_correct<DT>(L, m, n, v);
-    packed_store4<DT>(L, m, n, v);
-  }
+  if (m < M && n < L.N) packed_store4<DT>(L, m, n, v);
 }
 
 // End of an item for a K-split workgroup: sums the KW wavefronts' tiles (LDS, wavefront order)

@@ -2,9 +2,8 @@
 
 The reference's ``GatedLoraMethod.apply`` runs the base linear over every row, a second GEMM
 ``h = x[g:] A^T`` and one ``addmm_`` per shard of a fused projection (plm/gated_lora.py:45-57). Here a
-tuned, eligible call is two launches of ``plm_gemm_packed_lora``: ``h`` into the workspace, then the
-base GEMM with the rank-r correction added where it stores each gated row (no extra pass over the
-output). Calls the reference itself would not route to its fast GEMM (a bias, an untuned shape, a
+tuned, eligible call is one ``plm_gemm_packed_lora``: ``h`` into the workspace, the base GEMM, then
+one small kernel that adds every shard's rank-r correction to the gated rows in place. Calls the reference itself would not route to its fast GEMM (a bias, an untuned shape, a
 non-half dtype) take the reference's unfused composition through ``fast_gemm``'s dispatch slot.
 
 ``rows_from(g)`` sets the first gated row for the calls inside it, as the reference's context manager
