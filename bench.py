@@ -478,7 +478,7 @@ def time_gated_lora(args, device):
 
     from plm_amd import gemm_tables
     from plm_amd.fast_gemm import hip_linear
-    from plm_amd.gated_lora import gated_linear
+    from plm_amd.gated_lora import gated_linear, stack_b
 
     M, K, shards, rank, gate = args.M, 2048, (2048, 512, 512), 16, 7
     N = sum(shards)
@@ -490,10 +490,10 @@ def time_gated_lora(args, device):
         w = (0.02 * torch.randn(N, K, generator=gen, device=device)).bfloat16()
         a = (0.05 * torch.randn(len(shards) * rank, K, generator=gen, device=device)).bfloat16()
         bs = [(0.5 * torch.randn(n, rank, generator=gen, device=device)).bfloat16() for n in shards]
-        sets.append((w, a, bs))
+        sets.append((w, a, bs, stack_b(bs)))   # B stacked once, as GatedLoraMethod does at install
     down_cfg = {"wave_frags": 1, "k_waves": 4, "split_k": 1, "unroll": 2}
 
-    def composed(w, a, bs):
+    def composed(w, a, bs, _b):
         out = hip_linear(x, w, cfg)
         hidden = hip_linear(x[gate:], a, down_cfg)
         col = 0
@@ -503,8 +503,8 @@ def time_gated_lora(args, device):
         return out
 
     res = {}
-    for name, fn in (("fused_us", lambda w, a, bs: gated_linear(x, w, a, bs, gate, cfg=cfg)), ("composed_us", composed),
-                     ("base_gemm_us", lambda w, a, bs: hip_linear(x, w, cfg))):
+    for name, fn in (("fused_us", lambda w, a, bs, b: gated_linear(x, w, a, bs, gate, cfg=cfg, lora_b=b)),
+                     ("composed_us", composed), ("base_gemm_us", lambda w, a, bs, b: hip_linear(x, w, cfg))):
         for st in sets:
             fn(*st)
         torch.cuda.synchronize()

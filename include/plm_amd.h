@@ -55,14 +55,22 @@ enum plm_status {
 /*
  * Tile configuration of one GEMM shape: the MI355X counterpart of the reference's
  * {BLOCK_M, BLOCK_N, BLOCK_K, SPLIT_K, num_warps, num_stages} dict (plm/fast_gemm.py:64).
- *   wave_frags : 16-row weight fragments per compute wavefront (1, 2 or 4). A workgroup has four
- *                compute wavefronts, so a tile is 64*wave_frags rows of W; each wavefront owns its
- *                rows over the whole K range of the tile (no reduction across wavefronts). A fifth
- *                wavefront runs the epilogue.
- *   k_waves    : compute wavefronts per workgroup (4).
- *   split_k    : workgroups splitting K; their fp32 partials are summed in split order
- *                0..split_k-1 by the last workgroup of the tile to finish (no float atomics).
- *   unroll     : 32-wide K steps per streamed chunk (2: one 128-byte line of every weight row).
+ * The fields mean different things to the two kernel families:
+ *   packed-weight kernel (plm_gemm_packed, plm_gemm_chain_packed, the verify over packed W):
+ *     wave_frags : 16-row weight fragments each wavefront streams per K step (1, 2 or 4).
+ *     k_waves    : workgroup layout. 4, 8 or 16: that many wavefronts split the K range of a
+ *                  16*wave_frags-row tile and their fp32 tiles are summed in LDS in wavefront order;
+ *                  1: four wavefronts each own 16*wave_frags rows of a 64*wave_frags-row tile over
+ *                  the whole K range and share one copy of X through LDS.
+ *     split_k    : workgroups splitting K (1..64); their fp32 partials are summed in split order
+ *                  0..split_k-1 by the last workgroup of the tile to finish (no float atomics).
+ *     unroll     : K steps of loads in flight per wavefront (2, 4, 6 or 8).
+ *   row-major streaming kernel (plm_gemm, plm_gemm_chain, plm_lm_head_verify):
+ *     wave_frags : 16-row fragments per compute wavefront; a workgroup has four compute wavefronts
+ *                  (tile = 64*wave_frags rows), four loader wavefronts and one epilogue wavefront.
+ *     k_waves    : 4 (the compute wavefronts).
+ *     split_k    : as above.
+ *     unroll     : 2 (one 128-byte line of every weight row per streamed chunk).
  */
 typedef struct plm_tile {
   int32_t wave_frags;
@@ -169,6 +177,12 @@ int plm_gemm_packed_resident_workgroups(int32_t dtype, int64_t M, const plm_tile
 int plm_gemm_chain_packed(int32_t dtype, const plm_chain_gemm* host_gemms, const plm_chain_gemm* device_gemms,
                           int32_t count, int64_t M, const plm_tile* tile, void* workspace, size_t workspace_bytes,
                           void* stream);
+/* How plm_gemm_chain_packed would make the linears of this chain wait for each other (host only,
+ * no device needed): 0 none reads another; 2 per-wavefront waits on the producer's tile-done flags
+ * (every linear after the first reads the one before it and every Y that is read starts on a
+ * 128-byte boundary with ldy a multiple of 64 elements); 1 a grid barrier after every linear that
+ * is read (any other pattern). A negative status for an invalid chain or tile. */
+int plm_gemm_chain_packed_sync_mode(const plm_chain_gemm* gemms, int32_t count, const plm_tile* tile);
 
 /*
  * Fills the derived fields of gemms[0..count) for the tile configuration (whose split_k is

@@ -167,15 +167,20 @@ int packed_entry(int32_t dtype, const void* x, int64_t ldx, const void* wp, void
 }
 
 // How the linears of a chain wait for the ones they read: 0 (none reads another), 2 (every linear
-// after the first reads the one before it, and none that is read has more tiles than a parity set
-// of tile flags holds: per-wavefront waits on the producer's tile-done flags; the last linear,
-// read by none, raises no flags), or 1 (otherwise: a grid barrier after every linear that is read).
+// after the first reads the one before it, none that is read has more tiles than a parity set of
+// tile flags holds, and every Y that is read starts on a 128-byte boundary with rows a multiple of
+// 128 bytes apart: per-wavefront waits on the producer's tile-done flags, widened to whole
+// 128-byte lines of one row; the last linear, read by none, raises no flags), or 1 (otherwise: a
+// grid barrier after every linear that is read).
 int packed_chain_mode(const plm_chain_gemm* g, int32_t count, const plm_tile& t) {
   bool any = false, pure = count > 1;
   for (int32_t i = 0; i < count; ++i) {
     any = any || g[i].dep >= 0;
     if (i > 0 && g[i].dep != i - 1) pure = false;
-    if (i + 1 < count && packed_tiles(g[i].N, t) > kPkTileFlags) pure = false;
+    if (i + 1 < count) {
+      if (packed_tiles(g[i].N, t) > kPkTileFlags) pure = false;
+      if ((reinterpret_cast<uintptr_t>(g[i].y) & 127) != 0 || g[i].ldy % 64 != 0) pure = false;
+    }
   }
   return pure ? 2 : (any ? 1 : 0);
 }
@@ -299,6 +304,12 @@ int64_t plm_gemm_chain_packed_prepare(plm_chain_gemm* gemms, int32_t count, int6
   if (gemms == nullptr || count < 1 || M < 1 || M > plm::kPackedMaxM) return PLM_ERR_ARGUMENT;
   if (!plm::packed_tile_valid(tile)) return PLM_ERR_TILE;
   return plm::packed_prepare(gemms, count, M, *tile);
+}
+
+int plm_gemm_chain_packed_sync_mode(const plm_chain_gemm* gemms, int32_t count, const plm_tile* tile) {
+  if (gemms == nullptr || count < 1) return PLM_ERR_ARGUMENT;
+  if (!plm::packed_tile_valid(tile)) return PLM_ERR_TILE;
+  return plm::packed_chain_mode(gemms, count, *tile);
 }
 
 int plm_gemm_chain_packed(int32_t dtype, const plm_chain_gemm* host_gemms, const plm_chain_gemm* device_gemms,

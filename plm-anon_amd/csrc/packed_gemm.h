@@ -495,6 +495,14 @@ __device__ __forceinline__ void packed_finish_rows(const PLinear& L, int M, int 
 
 extern __shared__ __attribute__((aligned(16))) f32x4 packed_lds[];
 
+// Whether an earlier bounded wait of this launch (or of an earlier launch whose flag nobody
+// cleared) gave up. Every wait checks it on entry and every kErrorCheckPolls polls, so once one wait
+// times out the rest of the chain drains at once instead of each link spinning its own limit.
+constexpr int kErrorCheckPolls = 256;
+__device__ __forceinline__ bool chain_failed(const PackedArgs& a) {
+  return __builtin_amdgcn_readfirstlane(collect(a.counters + kPkErrorSlot)) != 0;
+}
+
 // Grid barrier after the consumed linear with sequence number `seq`, in two halves so that the
 // wait can overlap weight traffic: barrier_arrive raises this workgroup's progress flag (its
 // stores are written through: the caller waited for them), barrier_wait polls every workgroup's
@@ -507,7 +515,7 @@ __device__ __forceinline__ void barrier_arrive(const PackedArgs& a, int64_t epoc
 
 __device__ __forceinline__ void barrier_wait(const PackedArgs& a, int64_t epoch, int seq, int lane) {
   const int64_t target = ((epoch + 1) << 16) + seq;
-  if (threadIdx.x < 64) {
+  if (threadIdx.x < 64 && !chain_failed(a)) {
     // Each lane polls G/64 flags with device-coherent loads, issued in batches of eight (one
     // batch covers 512 workgroups) before any of the batch is examined.
     const auto frs = make_rsrc(a.counters + kPackedBarrierBase, static_cast<uint32_t>(a.G) * 8u);
@@ -529,6 +537,7 @@ __device__ __forceinline__ void barrier_wait(const PackedArgs& a, int64_t epoch,
         if (lane == 0) publish(a.counters + kPkErrorSlot, 1);
         break;
       }
+      if (i % kErrorCheckPolls == kErrorCheckPolls - 1 && chain_failed(a)) break;
       __builtin_amdgcn_s_sleep(1);
     }
   }
@@ -564,7 +573,9 @@ __device__ __forceinline__ void warm_weights(const PLinear& Ln, int G, int wave,
 // read has raised its flag (bounded; error flag on timeout). The range covers every 128-byte
 // line the X loads touch, not only the columns they use: a line holding a column of an
 // unfinished neighbour tile would otherwise enter this XCD's L2 with that column's old value and
-// be served later to a wavefront that waited for the neighbour.
+// be served later to a wavefront that waited for the neighbour. The widening by 63 columns is
+// exact because the host picks this mode only when every consumed Y starts on a 128-byte boundary
+// and its rows are a multiple of 128 bytes apart, so no line spans two rows.
 template <int NF, int KW>
 __device__ __forceinline__ void wait_producer_tiles(const PackedArgs& a, const PLinear& L, const PLinear& P, int wave,
                                                     int lane) {
@@ -578,7 +589,7 @@ __device__ __forceinline__ void wait_producer_tiles(const PackedArgs& a, const P
       hi = max(hi, e);
     }
   }
-  if (lo >= hi) return;
+  if (lo >= hi || chain_failed(a)) return;
   constexpr int kCols = 16 * tile_frags<NF, KW>();  // Y columns of one producer tile
   constexpr int kLineCols = 64;                      // bf16 columns of a 128-byte line
   const int t0 = max(32 * lo - (kLineCols - 1), 0) / kCols;
@@ -598,6 +609,7 @@ __device__ __forceinline__ void wait_producer_tiles(const PackedArgs& a, const P
       if (lane == 0) publish(a.counters + kPkErrorSlot, 1);
       break;
     }
+    if (i % kErrorCheckPolls == kErrorCheckPolls - 1 && chain_failed(a)) break;
     __builtin_amdgcn_s_sleep(1);
   }
 }

@@ -40,6 +40,7 @@ EXPORTS = (
     "plm_gemm_packed_tile_supported",
     "plm_gemm_chain_packed_prepare",
     "plm_gemm_chain_packed",
+    "plm_gemm_chain_packed_sync_mode",
     "plm_gemm_packed_resident_workgroups",
     "plm_lm_head_verify",
     "plm_lm_head_verify_workspace_bytes",
@@ -109,6 +110,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.plm_gemm_chain_packed_prepare.restype = c_i64
     lib.plm_gemm_chain_packed.argtypes = [c_i32, chain_p, c_p, c_i32, c_i64, tile_p, c_p, c_sz, c_p]
     lib.plm_gemm_chain_packed.restype = ctypes.c_int
+    lib.plm_gemm_chain_packed_sync_mode.argtypes = [chain_p, c_i32, tile_p]
+    lib.plm_gemm_chain_packed_sync_mode.restype = ctypes.c_int
     lib.plm_gemm_packed_resident_workgroups.argtypes = [c_i32, c_i64, tile_p]
     lib.plm_gemm_packed_resident_workgroups.restype = ctypes.c_int
     lib.plm_lm_head_verify.argtypes = [c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, c_p, c_i32, ctypes.c_float,

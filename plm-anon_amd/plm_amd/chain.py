@@ -85,7 +85,29 @@ class LinearChain:
                        self._tile, self.ws.data_ptr(), self.ws.numel(), _lib.stream_handle(self.device))
         _lib.check(status, f"plm_gemm_chain({len(self.links)} linears, M={self.M}, cfg={self.cfg})")
 
+    @property
+    def sync_mode(self) -> int:
+        """How the launch makes linears wait for the ones they read (packed chains): 0 none, 1 grid
+        barriers, 2 tile-done flags (``plm_gemm_chain_packed_sync_mode``)."""
+        if not self.packed:
+            raise ValueError("sync_mode describes packed chains")
+        mode = int(_lib.lib().plm_gemm_chain_packed_sync_mode(self.host, len(self.links), self._tile))
+        if mode < 0:
+            _lib.check(mode, "plm_gemm_chain_packed_sync_mode")
+        return mode
+
     def error_flag(self) -> int:
         """The counter area's error flag (1 if a wait for another workgroup gave up); syncs."""
         torch.cuda.synchronize(self.device)
         return int(self.ws[: 4 * (_lib.ERROR_INDEX + 1)].view(torch.int32)[_lib.ERROR_INDEX].item())
+
+    def check(self) -> None:
+        """Raises if a launch since the last check had a wait give up (its outputs, and those of
+        every launch after it until this check, are invalid), and clears the flag so later
+        launches are judged on their own. Synchronises the device; call it outside graph capture,
+        after the launches (or graph replays) it vouches for."""
+        if self.error_flag():
+            self.ws[4 * _lib.ERROR_INDEX: 4 * (_lib.ERROR_INDEX + 1)].zero_()
+            torch.cuda.synchronize(self.device)
+            raise RuntimeError(f"a chained launch of {len(self.links)} linears had a wait for another workgroup give "
+                               "up (another process on the device, or the grid was not resident): outputs invalid")

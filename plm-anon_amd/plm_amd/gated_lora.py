@@ -40,40 +40,57 @@ def rows_from(first_gated_row: int | None) -> Iterator[None]:
         _rows_from = saved
 
 
-_stacked: dict[tuple, torch.Tensor] = {}
+# The small GEMM that forms h = x[g:] A^T inside plm_gemm_packed_lora (kLoraDownTile in
+# csrc/packed_api.hip): one 16-row fragment per wavefront, eight wavefronts splitting K, four K splits.
+LORA_DOWN_TILE = {"wave_frags": 1, "k_waves": 8, "split_k": 4, "unroll": 2}
+MAX_RANK = 1024
 
 
-def _stacked_b(lora_bs: list[torch.Tensor]) -> torch.Tensor:
-    """The shards' up-projections stacked by output column ([N, rank], row-major), made once per set
-    of tensors (and remade if any of them is modified in place)."""
-    key = tuple((id(b), b._version) for b in lora_bs)
-    got = _stacked.get(key)
-    if got is None:
-        got = torch.cat([b.contiguous() for b in lora_bs], dim=0).contiguous()
-        _stacked.clear()
-        _stacked[key] = got
-    return got
+def stack_b(lora_bs: list[torch.Tensor]) -> torch.Tensor:
+    """The shards' up-projections stacked by output column ([N, rank], row-major): the layout
+    ``plm_gemm_packed_lora`` reads. A new tensor; callers that apply the same adapter repeatedly
+    (``GatedLoraMethod``) stack once and pass it as ``lora_b``."""
+    return torch.cat([b.contiguous() for b in lora_bs], dim=0).contiguous()
+
+
+def _eligible(x, weight, lora_a, lora_bs, first_gated_row, bias, cfg) -> bool:
+    """Whether the fused HIP path takes this call: everything ``plm_gemm_packed_lora`` checks, so
+    that an ineligible call takes the reference's composition instead of failing."""
+    from .fast_gemm import tile_supported
+
+    shards = len(lora_bs)
+    if cfg is None or bias is not None or x.dim() != 2 or x.dtype not in HALF_DTYPES or not x.is_cuda:
+        return False
+    if weight.dtype != x.dtype or lora_a.dtype != x.dtype or any(b.dtype != x.dtype for b in lora_bs):
+        return False
+    if not 1 <= shards <= 3 or lora_a.shape[0] % shards:
+        return False
+    rank = lora_a.shape[0] // shards
+    if rank < 8 or rank > MAX_RANK or rank % 8 or any(b.dim() != 2 or b.shape[1] != rank for b in lora_bs):
+        return False
+    M, K = x.shape
+    if sum(b.shape[0] for b in lora_bs) != weight.shape[0] or K % 8:
+        return False
+    return tile_supported(M, K, cfg, x.dtype) and tile_supported(M - first_gated_row, K, LORA_DOWN_TILE, x.dtype)
 
 
 def gated_linear(x: torch.Tensor, weight: torch.Tensor, lora_a: torch.Tensor, lora_bs: list[torch.Tensor],
                  first_gated_row: int | None, bias: torch.Tensor | None = None,
-                 cfg: Config | None = None) -> torch.Tensor:
+                 cfg: Config | None = None, lora_b: torch.Tensor | None = None) -> torch.Tensor:
     """``x @ weight^T`` with rows ``first_gated_row..`` corrected by ``(x A^T) B_s^T`` per shard.
 
-    ``lora_a`` is ``[shards*rank, K]``, ``lora_bs[s]`` is ``[N_s, rank]`` with ``sum N_s = N``. The
-    HIP path runs when the call is eligible for the tuned GEMM (no bias, 2-D half-precision operands,
-    a tile in ``cfg`` or installed for ``(M, N, K)``); otherwise the reference's composition."""
+    ``lora_a`` is ``[shards*rank, K]``, ``lora_bs[s]`` is ``[N_s, rank]`` with ``sum N_s = N``;
+    ``lora_b`` may carry them already stacked (``stack_b``). The HIP path runs when the call is
+    eligible for the tuned GEMM (no bias, 2-D half-precision operands, a tile in ``cfg`` or
+    installed for ``(M, N, K)``, a rank the kernel takes); otherwise the reference's composition."""
     M = x.shape[0]
     if first_gated_row is None or first_gated_row >= M:
         return dispatch_unquantized_gemm()(None, x, weight, bias)
+    first_gated_row = max(int(first_gated_row), 0)
     cfg = cfg if cfg is not None else CONFIGS.get((M, weight.shape[0], weight.shape[1]))
     shards = len(lora_bs)
     rank = lora_a.shape[0] // shards
-    eligible = (cfg is not None and bias is None and x.dim() == 2 and x.dtype in HALF_DTYPES and
-                weight.dtype == x.dtype and lora_a.dtype == x.dtype and all(b.dtype == x.dtype for b in lora_bs) and
-                x.is_cuda and 1 <= shards <= 3 and lora_a.shape[0] == shards * rank and rank % 8 == 0 and
-                all(b.shape[1] == rank for b in lora_bs) and sum(b.shape[0] for b in lora_bs) == weight.shape[0])
-    if not eligible:
+    if not _eligible(x, weight, lora_a, lora_bs, first_gated_row, bias, cfg):
         gemm = dispatch_unquantized_gemm()
         output = gemm(None, x, weight, bias)
         hidden = gemm(None, x[first_gated_row:], lora_a)
@@ -82,18 +99,22 @@ def gated_linear(x: torch.Tensor, weight: torch.Tensor, lora_a: torch.Tensor, lo
             output[first_gated_row:, col:col + b.shape[0]].addmm_(hidden[:, s * rank:(s + 1) * rank], b.t().contiguous())
             col += b.shape[0]
         return output
-    x = x if (x.stride(1) == 1 and x.stride(0) % 8 == 0) else x.contiguous()
+    if not (x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0):
+        x = x.contiguous()
     N, K = weight.shape
     out = torch.empty(M, N, device=x.device, dtype=x.dtype)
-    b_cat = _stacked_b(lora_bs)
+    if lora_b is None:
+        lora_b = stack_b(lora_bs)
+    elif lora_b.shape != (N, rank) or lora_b.stride() != (rank, 1) or lora_b.data_ptr() % 16:
+        raise ValueError(f"lora_b must be the shards' B's stacked row-major as [{N}, {rank}]")
     tile = _lib.Tile.from_config(cfg)
     lib = _lib.lib()
-    g = max(int(first_gated_row), 0)
+    g = first_gated_row
     ws = workspace(x.device, int(lib.plm_gemm_packed_lora_workspace_bytes(M, N, K, g, rank, shards, tile)))
     sizes = (ctypes.c_int64 * shards)(*[b.shape[0] for b in lora_bs])
     status = lib.plm_gemm_packed_lora(_lib.DTYPE_CODES[x.dtype], x.data_ptr(), x.stride(0),
                                       packed_weight(weight).data_ptr(), out.data_ptr(), out.stride(0), M, N, K, g,
-                                      packed_weight(lora_a).data_ptr(), b_cat.data_ptr(), rank, shards, sizes, tile,
+                                      packed_weight(lora_a).data_ptr(), lora_b.data_ptr(), rank, shards, sizes, tile,
                                       ws.data_ptr(), ws.numel(), _lib.stream_handle(x.device))
     _lib.check(status, f"plm_gemm_packed_lora(M={M}, N={N}, K={K}, rank={rank}, shards={shards})")
     return out
@@ -106,6 +127,8 @@ class GatedLoraMethod:
     def __init__(self, inner, lora_bs: list[torch.Tensor]) -> None:
         self.inner = inner
         self.lora_bs = lora_bs
+        # Stacked once here, at install, so no call concatenates (or caches) during graph capture.
+        self.lora_b = stack_b(lora_bs)
 
     def __getattr__(self, name: str):
         return getattr(self.inner, name)
@@ -114,7 +137,7 @@ class GatedLoraMethod:
         first = _rows_from
         if first is None or first >= x.shape[0]:
             return self.inner.apply(layer, x, bias)
-        return gated_linear(x, layer.weight, layer.lora_a, self.lora_bs, first, bias)
+        return gated_linear(x, layer.weight, layer.lora_a, self.lora_bs, first, bias, lora_b=self.lora_b)
 
 
 def _module_names(tensors: dict[str, torch.Tensor], suffix: str) -> dict[str, torch.Tensor]:

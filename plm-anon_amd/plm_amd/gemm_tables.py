@@ -15,7 +15,9 @@ from pathlib import Path
 from . import fast_gemm
 
 TABLES = Path(__file__).resolve().parent / "gpu_tuning"
-VOCAB_PADDING = 64   # vLLM's ParallelLMHead pads the vocabulary to this multiple
+# The LM head's row count is the vocabulary rounded up to a multiple of this (the padded head the
+# serving engine allocates), so the table keys the head on the padded N.
+VOCAB_PADDING = 64
 WIDEST_TUNED_DOWN_ROUND = 72
 # Above W=72 the `down` projection uses this fixed tile instead of the table entry (the reference's
 # override, plm/gemm_tables.py:17-19, 41-42). On MI355X the split-K combine costs no extra launch,

@@ -301,3 +301,55 @@ def test_workload_bytes_match_the_published_roofline_table():
     assert workloads.ROUND_3B.bytes == 5_443_196_784
     for M, b in zip(workloads.M_SWEEP, (2_633_514_094, 2_645_256_412, 2_668_741_048, 2_692_225_684, 2_715_710_320)):
         assert workloads.ROUND_1P3B.at(M).bytes == b
+
+
+def _chain_table(widths, K0, base=1 << 30, pad=None, dep_prev=True):
+    """A chain of linears x -> y_0 -> y_1 -> ... over fake, never-dereferenced device pointers:
+    widths[i] output columns; rows of y_i ``pad(widths[i])`` elements apart (default: unpadded)."""
+    n = len(widths)
+    arr = (_lib.ChainGemm * n)()
+    addr = base
+    ldys = [pad(w) if pad else w for w in widths]
+    ys = []
+    for ld in ldys:
+        ys.append(addr)
+        addr += (56 * ld * 2 + 4095) // 4096 * 4096
+    for i, w in enumerate(widths):
+        g = arr[i]
+        g.x = base - (1 << 24) if i == 0 else ys[i - 1]
+        g.w = addr + (i << 26)
+        g.y = ys[i]
+        g.ldx = K0 if i == 0 else ldys[i - 1]
+        g.ldw = g.K = K0 if i == 0 else widths[i - 1]
+        g.ldy = ldys[i]
+        g.N = w
+        g.split_k = 1
+        g.dep = (i - 1) if (dep_prev and i > 0) else -1
+    return arr
+
+
+def test_chain_sync_mode_requires_line_aligned_consumed_rows():
+    """Tile-flag waits widen a wavefront's columns to whole 128-byte lines of one row; they are only
+    chosen when no line can span two rows of a consumed Y (y 128-byte aligned, ldy % 64 == 0)."""
+    lib = _lib.lib()
+    tile = _lib.Tile(2, 8, 1, 2)
+    mode = lambda arr: lib.plm_gemm_chain_packed_sync_mode(arr, len(arr), tile)  # noqa: E731
+    assert mode(_chain_table([2048, 8192, 2048], 2048)) == 2
+    # A consumed width that is not a multiple of 64 elements: rows 2000 B apart.
+    assert mode(_chain_table([1000, 2048, 512], 1024)) == 1
+    # The same widths with the rows padded to a multiple of 64 elements.
+    assert mode(_chain_table([1000, 2048, 512], 1024, pad=lambda w: -(-w // 64) * 64)) == 2
+    # The last linear is read by none: its Y may have any width.
+    assert mode(_chain_table([2048, 1000], 1024)) == 2
+    # A consumed Y that starts off a 128-byte boundary.
+    arr = _chain_table([2048, 2048, 512], 1024)
+    arr[0].y += 64
+    arr[1].x = arr[0].y
+    assert mode(arr) == 1
+    # No dependencies at all, and any other dependency pattern.
+    assert mode(_chain_table([2048, 2048], 1024, dep_prev=False)) == 0
+    arr = _chain_table([2048, 2048, 2048], 2048)
+    arr[2].dep = 0
+    assert mode(arr) == 1
+    assert lib.plm_gemm_chain_packed_sync_mode(arr, 0, tile) == -1
+    assert lib.plm_gemm_chain_packed_sync_mode(arr, 3, _lib.Tile(3, 8, 1, 2)) == -3

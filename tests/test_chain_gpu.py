@@ -93,6 +93,12 @@ def test_packed_chain_tiles(device, cfg):
     assert chain.error_flag() == 0
 
 
+def _padded_outputs(M, ws, device, dtype=torch.bfloat16):
+    """Outputs whose rows start 128 bytes apart (ldy a multiple of 64 elements): views of wider
+    buffers where N is not a multiple of 64, so a chain reading them keeps its tile-flag mode."""
+    return [torch.empty(M, -(-w.shape[0] // 64) * 64, device=device, dtype=dtype)[:, : w.shape[0]] for w in ws]
+
+
 def test_tile_flag_chain_long_and_wide_links(device):
     """The tile-flag chain with the round's tile: items of 2 to 32 K steps per wavefront, several
     items per workgroup (625 and 1250 tiles), a K that ends inside a step, a split link."""
@@ -101,12 +107,35 @@ def test_tile_flag_chain_long_and_wide_links(device):
     g = torch.Generator(device=device).manual_seed(40)
     x = torch.randn(M, 2048, generator=g, device=device).bfloat16()
     ws = _weights([(8192, 2048), (2048, 8192), (20000, 2048), (1000, 20000), (40000, 1000)], 41, device)
-    links, _ = _chain(x, ws, (1, 1, 1, 2, 1))
+    links, _ = _chain(x, ws, (1, 1, 1, 2, 1), ys=_padded_outputs(M, ws, device))
     chain = LinearChain(links, cfg, packed=True)
+    assert chain.sync_mode == 2
     for _ in range(2):
+        x.copy_(torch.randn(M, 2048, generator=g, device=device).bfloat16())
         chain.run()
         _check_against_single(links, cfg)
     assert chain.error_flag() == 0
+
+
+def test_unaligned_consumed_output_takes_grid_barriers(device):
+    """A consumed Y whose rows are not 128 bytes apart (N = 1000) would let a 128-byte line span the
+    tail of one row and the head of the next, outside the tile-flag wait's widening: the launch uses
+    grid barriers instead, and stays exact with new inputs on every launch."""
+    M = 56
+    cfg = {"wave_frags": 2, "k_waves": 8, "split_k": 1, "unroll": 2}
+    g = torch.Generator(device=device).manual_seed(42)
+    x = torch.randn(M, 1024, generator=g, device=device).bfloat16()
+    ws = _weights([(1000, 1024), (3000, 1000), (1000, 3000)], 43, device)
+    links, ys = _chain(x, ws, (1, 2, 1))
+    chain = LinearChain(links, cfg, packed=True)
+    assert chain.sync_mode == 1
+    for _ in range(3):
+        x.copy_(torch.randn(M, 1024, generator=g, device=device).bfloat16())
+        for y in ys:
+            y.fill_(float("nan"))
+        chain.run()
+        _check_against_single(links, cfg)
+    chain.check()
 
 
 def test_repeated_launches_and_external_input(device):
@@ -189,3 +218,66 @@ def test_fp32_last_link_and_fp16(device):
     chain.run()
     torch.testing.assert_close(y1.cpu(), oracle.linear_fp32(y0.cpu(), ws[1].cpu()), rtol=1e-4, atol=1e-4)
     assert chain.error_flag() == 0
+
+
+def _oracle_columns(x, w, y, cols):
+    """``y[:, cols]`` against the CPU oracle on those weight rows: within 1e-3 rel / 2e-2 abs, or one
+    output rounding step (at most 0.1 % of the sampled elements)."""
+    got = y[:, cols].cpu().float()
+    ref = oracle.linear(x.cpu(), w[cols].cpu()).float()
+    diff = (got - ref).abs()
+    in_tol = diff <= ATOL + RTOL * ref.abs()
+    step = 2.0 ** (torch.floor(torch.log2(ref.abs().clamp_min(2.0 ** -14))) - 7)
+    assert bool((in_tol | (diff <= step * 1.0001)).all()), f"max |got - oracle| {diff.max():.4g}"
+    assert int((~in_tol).sum()) <= max(1, got.numel() // 1000)
+
+
+def test_round_chain_graph_replays_with_new_inputs(device):
+    """The benchmark's chained round, all 96 block linears of the 1.3B-shape round at M = 56 in one
+    tile-flag launch, recorded as a HIP graph and replayed 8 times. Before every replay the round's
+    input is rewritten and every output filled with NaN, so a consumer that read a line before its
+    producer tiles were written (or a line left from an earlier replay) would show up: each replay
+    must equal per-linear launches bit for bit, and sampled columns of the first and last block
+    must match the CPU oracle."""
+    from plm_amd import _lib
+    from plm_amd.fast_gemm import _tile
+    from plm_amd.tiles import packed_chain_split, packed_chain_tile
+
+    M = 56
+    cfg = packed_chain_tile(M)
+    G = _lib.lib().plm_gemm_packed_resident_workgroups(_lib.PLM_BF16, M, _tile(cfg))
+    assert G > 0
+    block = workloads.gpt_block(2048, 8192)
+    shapes = [(gm.N, gm.K) for gm in block] * 24
+    ws = _weights(shapes, 60, device)
+    g = torch.Generator(device=device).manual_seed(61)
+    x = torch.randn(M, 2048, generator=g, device=device).bfloat16()
+    splits = [packed_chain_split(n, k, cfg, G) for n, k in shapes]
+    links, ys = _chain(x, ws, splits)
+    chain = LinearChain(links, cfg, packed=True)
+    assert chain.sync_mode == 2
+    chain.run()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        chain.run()
+    refs = [torch.empty_like(y) for y in ys]
+    sample = torch.randperm(2048, generator=torch.Generator().manual_seed(62))[:96]
+    for rep in range(8):
+        x.copy_(torch.randn(M, 2048, generator=g, device=device).bfloat16())
+        for y in ys:
+            y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for ln, ref in zip(links, refs):
+            hip_linear(ln.x, ln.w, dict(cfg, split_k=ln.split_k), ref)
+        torch.cuda.synchronize()
+        bad = [i for i, (y, r) in enumerate(zip(ys, refs)) if not torch.equal(y, r)]
+        assert not bad, f"replay {rep}: links {bad[:8]} differ from per-linear launches"
+        if rep in (0, 7):
+            for i in (0, 1, 2, 3, 92, 93, 94, 95):
+                cols = sample[sample < ws[i].shape[0]]
+                _oracle_columns(links[i].x, ws[i], ys[i], cols)
+    chain.check()
