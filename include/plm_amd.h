@@ -112,6 +112,19 @@ int plm_gemm_packed_f32out(int32_t dtype, const void* x, int64_t ldx, const void
                            int64_t M, int64_t N, int64_t K, const plm_tile* tile, void* workspace,
                            size_t workspace_bytes, void* stream);
 
+/*
+ * plm_gemm_packed without a workspace argument and without allocating: no counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). The split-K scratch is a device array inside the
+ * library, PLM_NOALLOC_SCRATCH_BYTES per device, held until the process ends; a shape and tile whose
+ * plm_gemm_packed_workspace_bytes exceeds it is rejected with PLM_ERR_WORKSPACE. Every call on one
+ * device shares that array, so calls that overlap on one device (other streams, other threads) race.
+ * Otherwise as plm_gemm_packed: same kernel, same results bit for bit.
+ */
+#define PLM_NOALLOC_SCRATCH_BYTES (PLM_WORKSPACE_COUNTER_BYTES + (8u << 20))
+int plm_gemm_packed_noalloc(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy,
+                            int64_t M, int64_t N, int64_t K, const plm_tile* tile, void* stream);
+
 /* Workspace bytes plm_gemm_packed needs for this shape and tile (0 without split-K), and whether a
  * kernel is compiled for the tile at this M. */
 size_t plm_gemm_packed_workspace_bytes(int64_t M, int64_t N, int64_t K, const plm_tile* tile);

@@ -239,6 +239,18 @@ PSpan pspan(const void* p, int64_t rows, int64_t ld, int64_t cols, int64_t elem)
 }
 
 }  // namespace
+
+int packed_gemm_call(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy, int64_t M,
+                     int64_t N, int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream,
+                     int out_f32) {
+  return packed_entry(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, out_f32);
+}
+
+int64_t packed_gemm_workspace(int64_t M, int64_t N, const plm_tile* tile) {
+  if (!packed_tile_valid(tile) || M < 1 || N < 1) return -1;
+  return packed_workspace(M, N, *tile);
+}
+
 }  // namespace plm
 
 extern "C" {

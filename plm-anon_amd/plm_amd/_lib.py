@@ -21,6 +21,9 @@ DTYPE_CODES = {torch.bfloat16: PLM_BF16, torch.float16: PLM_F16}
 # PLM_WORKSPACE_COUNTER_BYTES: the zero-between-calls counter area at the start of every workspace.
 COUNTER_BYTES = 1 << 18
 
+# PLM_NOALLOC_SCRATCH_BYTES: the device array plm_gemm_packed_noalloc uses instead of a workspace.
+NOALLOC_SCRATCH_BYTES = COUNTER_BYTES + (8 << 20)
+
 # PLM_WORKSPACE_ERROR_INDEX: the int in the counter area a chained launch sets when a wait gave up.
 ERROR_INDEX = 2
 
@@ -36,6 +39,7 @@ EXPORTS = (
     "plm_pack_weight",
     "plm_gemm_packed",
     "plm_gemm_packed_f32out",
+    "plm_gemm_packed_noalloc",
     "plm_gemm_packed_workspace_bytes",
     "plm_gemm_packed_tile_supported",
     "plm_gemm_chain_packed_prepare",
@@ -102,6 +106,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.plm_gemm_packed.restype = ctypes.c_int
     lib.plm_gemm_packed_f32out.argtypes = lib.plm_gemm_packed.argtypes
     lib.plm_gemm_packed_f32out.restype = ctypes.c_int
+    lib.plm_gemm_packed_noalloc.argtypes = [c_i32, c_p, c_i64, c_p, c_p, c_i64, c_i64, c_i64, c_i64, tile_p, c_p]
+    lib.plm_gemm_packed_noalloc.restype = ctypes.c_int
     lib.plm_gemm_packed_workspace_bytes.argtypes = [c_i64, c_i64, c_i64, tile_p]
     lib.plm_gemm_packed_workspace_bytes.restype = c_sz
     lib.plm_gemm_packed_tile_supported.argtypes = [c_i32, c_i64, c_i64, tile_p]
