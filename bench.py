@@ -46,6 +46,8 @@ def parse_args():
     ap.add_argument("--no-sweep", action="store_true", help="skip the partial-round M sweep")
     ap.add_argument("--no-verify", action="store_true", help="skip the fused LM-head verify timing")
     ap.add_argument("--no-llama", action="store_true", help="skip the reference's Llama-style linear sets")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the per-config lines (single GEMM, one block, the 32 x H2560 round)")
     ap.add_argument("--only-round", action="store_true", help="time the round only (for profiling runs)")
     ap.add_argument("--profile", choices=("eager", "copy", "verify"),
                     help="no JSON: 'eager' launches the round and the fused verify step --steps times without a "
@@ -150,6 +152,17 @@ def dominant_kernel_roofline(rnd, steps):
 def traffic_for(kernel: str):
     """HBM bytes per launch measured with rocprofv3 counters, if a committed summary holds them."""
     path = REPO / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    try:
+        return json.loads(path.read_text()).get(kernel)
+    except (OSError, ValueError):
+        return None
+
+
+def mfma_for(kernel: str):
+    """MFMA busy % and bf16 MFMA flops per dispatch from the committed rocprofv3 counter summary."""
+    path = REPO / "profiles" / "mfma.json"
     if not path.exists():
         return None
     try:
@@ -390,12 +403,151 @@ def main():
             print(f"[bench] M sweep: {sweep}", file=sys.stderr, flush=True)
         if not args.no_verify:
             result["verify"] = time_verify(weights[-1], args.hidden, device, args.steps)
+        if not args.no_configs:
+            result["configs"] = time_configs(args, device, rnd, chained, us_round, us_graph)
         if not args.no_llama:
             result["llama_rounds"] = time_llama_rounds(args, device)
             result["gated_lora"] = time_gated_lora(args, device)
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_baseline(args.hidden, args.mlp, args.M, args.cpu_seconds)
     print(json.dumps(result), flush=True)
+
+
+def cpu_linear_us(shapes, M, budget_s):
+    """Median microseconds of torch-CPU F.linear (the reference's --mode default op, via the oracle)
+    for each (N, K) at width M on this host's cores: one warm-up, then at least 5 repetitions within
+    the budget."""
+    import torch
+
+    import oracle
+    from plm_amd.workloads import normal
+
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    out = []
+    deadline = time.perf_counter() + budget_s
+    for i, (N, K) in enumerate(shapes):
+        x, w = normal((M, K), 7200 + K), normal((N, K), 7300 + i, 0.02)
+        oracle.linear(x, w)
+        times = []
+        while len(times) < 5 or (time.perf_counter() < deadline and len(times) < 30):
+            t0 = time.perf_counter()
+            oracle.linear(x, w)
+            times.append(time.perf_counter() - t0)
+        out.append(sorted(times)[len(times) // 2] * 1e6)
+    return out
+
+
+def _line(us, nbytes, cpu_us=None, **extra):
+    gbps = nbytes / (us * 1e-6) / 1e9
+    d = {"us": round(us, 2), "gbps": round(gbps, 1), "pct_of_hbm_peak": round(100.0 * gbps / HBM_PEAK_GBPS, 2),
+         "bytes": nbytes}
+    if cpu_us is not None:
+        d["cpu_us"] = round(cpu_us, 1)
+        d["speedup_vs_cpu"] = round(cpu_us / us, 1)
+    d.update(extra)
+    return d
+
+
+def time_configs(args, device, rnd, chained, us_round, us_graph):
+    """The BASELINE configs other than the headline round, each with its algorithmic bytes, GB/s,
+    % of the 8 TB/s peak and the torch-CPU time of the same linears on this host:
+      1  the single GEMM X[42,1024] x W[4096,1024]^T: a graph of 128 launches over 128 distinct
+         weight copies (1 GiB, four times the 256 MB Infinity Cache), per launch;
+      2  one 1.3B-shape block at M = 56 (QKV, attn-out, MLP up, down): the headline round's 96 block
+         linears (24 blocks of distinct weights) timed as the chained launch and as the per-GEMM
+         graph, per block;
+      4  the 32-block hidden-2560 round (QKV 2560->7680, attn-out, MLP up 2560->10240, down) + LM head
+         2560->50257 at M = 56, both implementations, with the chained launch's own roofline.
+    Config 3 is the headline; config 5 is `verify`."""
+    import torch
+
+    from plm_amd import gemm_tables
+    from plm_amd.fast_gemm import hip_linear
+    from plm_amd.workloads import GPT2_VOCAB, gpt_block
+
+    out = {}
+    budget = max(1.0, args.cpu_seconds / 4) if args.cpu_seconds > 0 else 0
+    # Config 1.
+    M, N, K = 42, 4096, 1024
+    cfg = gemm_tables.read_table(1024)[(M, N, K)]
+    gen = torch.Generator(device=device).manual_seed(1 + 1000)
+    x = torch.randn(M, K, generator=gen, device=device).bfloat16()
+    copies = [(0.02 * torch.randn(N, K, generator=gen, device=device)).bfloat16() for _ in range(128)]
+    y = torch.empty(M, N, device=device, dtype=torch.bfloat16)
+    graph = capture_graph(lambda: [hip_linear(x, w, cfg, y) for w in copies])
+    us = time_graph(graph, max(5, args.steps // 4), 2) * 1000.0 / len(copies)
+    del graph, copies
+    cpu = cpu_linear_us([(N, K)], M, budget)[0] if budget else None
+    out["1_single_gemm"] = _line(us, 2 * (N * K + M * K + M * N), cpu, shape="X[42,1024] x W[4096,1024]^T",
+                                 tile=cfg, timing="graph of 128 launches over 128 weight copies (1 GiB)")
+    print(f"[bench] config 1: {us:.2f} us", file=sys.stderr, flush=True)
+    # Config 2 from the headline round's 96 block linears.
+    block = gpt_block(args.hidden, args.mlp)
+    block_bytes = sum(g.bytes(rnd.M) for g in block)
+    n_blocks = len(rnd.gemms[:-1]) // len(block)
+    graph = capture_graph(lambda: rnd.launch(range(len(rnd.gemms) - 1)))
+    us_blocks = time_graph(graph, max(5, args.steps // 2), 2) * 1000.0
+    del graph
+    graph = capture_graph(chained.chain.run)
+    us_chain = time_graph(graph, max(5, args.steps // 2), 2) * 1000.0
+    del graph
+    cpu = sum(cpu_linear_us([(g.N, g.K) for g in block], rnd.M, budget)) if budget else None
+    out["2_block"] = {"chained": _line(us_chain / n_blocks, block_bytes, cpu),
+                      "per_gemm": _line(us_blocks / n_blocks, block_bytes, cpu),
+                      "shape": f"one {args.hidden}/{args.mlp} block at M={rnd.M}",
+                      "timing": f"the round's {n_blocks} blocks (distinct weights), per block"}
+    print(f"[bench] config 2: chained {us_chain / n_blocks:.2f} us, per-GEMM {us_blocks / n_blocks:.2f} us per block",
+          file=sys.stderr, flush=True)
+    # Config 4.
+    hidden, mlp, layers = 2560, 10240, 32
+    tables = gemm_tables.read_table(hidden)
+    gemms = [g for _ in range(layers) for g in gpt_block(hidden, mlp)]
+    gemms.append(type(gemms[0])("lm_head", GPT2_VOCAB, hidden))
+    gen = torch.Generator(device=device)
+    weights = []
+    for i, g in enumerate(gemms):
+        gen.manual_seed(1 + 1000 * 4 + i)
+        weights.append((0.02 * torch.randn(g.N, g.K, generator=gen, device=device)).bfloat16())
+    r4 = Round(rnd.M, hidden, mlp, layers, weights, tables, device)
+    c4 = ChainedRound(r4)
+    c4.run()
+    torch.cuda.synchronize()
+    chain_outs = [o.clone() for o in r4.outs]
+    for i, ln in enumerate(c4.chain.links):
+        hip_linear(ln.x, ln.w, dict(c4.chain.cfg, split_k=ln.split_k), r4.outs[i])
+    hip_linear(*c4.head)
+    torch.cuda.synchronize()
+    same = all(torch.equal(a, b) for a, b in zip(chain_outs, r4.outs))
+    c4.chain.check()
+    graph = capture_graph(c4.run)
+    us_c4 = time_graph(graph, max(5, args.steps // 2), 2) * 1000.0
+    del graph
+    graph = capture_graph(c4.chain.run)
+    us_c4_chain = time_graph(graph, max(5, args.steps // 2), 2) * 1000.0
+    del graph
+    graph = r4.capture()
+    us_g4 = time_graph(graph, max(5, args.steps // 2), 2) * 1000.0
+    del graph
+    cpu = None
+    if budget:
+        per = cpu_linear_us([(g.N, g.K) for g in gpt_block(hidden, mlp)] + [(GPT2_VOCAB, hidden)], rnd.M, budget)
+        cpu = layers * sum(per[:4]) + per[4]
+    achieved = c4.chain_bytes / (us_c4_chain * 1e-6) / 1e9
+    out["4_round_h2560"] = {
+        "chained": _line(us_c4, r4.bytes, cpu, launches=2, chain_matches_per_linear=bool(same)),
+        "per_gemm": _line(us_g4, r4.bytes, cpu, launches=len(gemms)),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "kernel": "chained launch of the 128 block linears",
+                     "us_per_launch": round(us_c4_chain, 2), "bytes_per_launch": c4.chain_bytes},
+        "shape": f"{layers} GPT-style blocks of hidden {hidden} (QKV {3 * hidden}, MLP {mlp}) + LM head "
+                 f"{hidden}->{GPT2_VOCAB}, M={rnd.M}",
+        "cpu_note": "torch CPU F.linear: one block + LM head timed, round = 32 x block + LM head" if cpu else None}
+    print(f"[bench] config 4: chained {us_c4:.1f} us, per-GEMM {us_g4:.1f} us", file=sys.stderr, flush=True)
+    del r4, c4, weights, chain_outs
+    torch.cuda.empty_cache()
+    out["3_round_1p3b"] = {"chained": _line(us_round, rnd.bytes), "per_gemm": _line(us_graph, rnd.bytes),
+                           "note": "the headline; cpu_baseline holds its CPU figure"}
+    return out
 
 
 def profile_verify(args, device):
@@ -563,8 +715,13 @@ def time_verify(w_lm, hidden, device, steps):
             rv(x, w, verify_tokens, *state)
     ms_round = time_graph(graph, max(5, steps // 2), 2) / len(copies)
     del graph, copies
+    mfma = mfma_for("verify_packed_main_kernel<bf16, MT=4, NF=2, D=2>") or {}
+    head = mfma_for("packed_gemm_kernel<bf16, MT=4, NF=4, D=8, KW=1>") or {}
     return {"us": round(ms * 1000.0, 2), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
-            "bytes": nbytes, "accepted": int(acc.sum().item()), "round_us": round(ms_round * 1000.0, 2)}
+            "pct_of_hbm_peak": round(100.0 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 2),
+            "bytes": nbytes, "accepted": int(acc.sum().item()), "round_us": round(ms_round * 1000.0, 2),
+            "mfma_busy_pct": mfma.get("mfma_busy_pct"), "lm_head_gemm_mfma_busy_pct": head.get("mfma_busy_pct"),
+            "mfma_source": "profiles/mfma.json (rocprofv3 --pmc MfmaUtil MfmaFlopsBF16)"}
 
 
 if __name__ == "__main__":

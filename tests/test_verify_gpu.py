@@ -83,7 +83,13 @@ def test_config5_fused_verify(device, mode, packed):
     gap = (top2[:, 0] - top2[:, 1]).numpy()
     safe_acc = torch.from_numpy(margin > 1e-4)
     safe_am = torch.from_numpy(gap > 1e-3)
-    assert safe_acc.sum() >= 50 and safe_am.sum() >= 50
+    # Rows left out as rounding-sensitive (their decision turns on a difference smaller than the
+    # fp32 sums' reordering error): at most two of 56 at config 5 in either rounding mode.
+    excluded_acc, excluded_am = int((~safe_acc).sum()), int((~safe_am).sum())
+    print(f"config 5 {mode} {'packed' if packed else 'rowmajor'}: rows excluded as rounding-sensitive: "
+          f"{excluded_acc} for accept, {excluded_am} for argmax; differing there: "
+          f"{int((acc != ref_acc)[~safe_acc].sum())}, {int((am != ref_am)[~safe_am].sum())}")
+    assert excluded_acc <= 2 and excluded_am <= 2
     assert torch.equal(acc[safe_acc], ref_acc[safe_acc])
     assert torch.equal(am[safe_am], ref_am[safe_am])
     assert 0 < int(acc.sum()) < 56
