@@ -260,6 +260,21 @@ int plm_lm_head_verify_packed(int32_t dtype, const void* x, int64_t ldx, const v
                               void* stream);
 
 /*
+ * plm_lm_head_verify_packed for a round whose verify rows decode through the auxiliary scheme
+ * (RoundDecoder._steady_round, plm/decoder.py:316-322): only rows r < pending_rows decide on
+ * pending[r] (the others are never accepted), and the logits of rows [0, logit_rows) are written
+ * to `logits` (row stride ld_logits) in the model dtype, rounded from the same fp32 accumulators
+ * the decision reads — the `logits[:K]` the decode takes (decoder.py:318-320), without writing the
+ * other rows'. round_mode must be the model dtype's (PLM_ROUND_BF16 for bf16, PLM_ROUND_F16 for
+ * fp16); ld_logits % 8 == 0, logits 16-byte aligned. Workspace as plm_lm_head_verify_workspace_bytes.
+ */
+int plm_lm_head_verify_packed_logits(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, int64_t R,
+                                     int64_t V, int64_t K, const int64_t* pending, int64_t pending_rows, int32_t rule,
+                                     float p, int32_t round_mode, uint8_t* accept, int64_t* argmax, void* logits,
+                                     int64_t ld_logits, int64_t logit_rows, const plm_tile* tile, void* workspace,
+                                     size_t workspace_bytes, void* stream);
+
+/*
  * One round's bookkeeping after the verify step, on the device: RoundDecoder._epilogue
  * (plm/decoder.py:351-365) from the verify kernel's outputs. With k proposals per round
  * (round width k + k*k):
@@ -316,6 +331,80 @@ int plm_gemm_packed_lora(int32_t dtype, const void* x, int64_t ldx, const void* 
                          void* workspace, size_t workspace_bytes, void* stream);
 size_t plm_gemm_packed_lora_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t gated_from, int64_t rank,
                                             int32_t shards, const plm_tile* tile);
+
+/*
+ * The verify rows' auxiliary decode, logit-Voronoi scheme with the `iterate` engine
+ * (LogitVoronoiAuxiliary.decode_unmasked, plm/auxiliary.py:67-75, over Voronoi.assign,
+ * plm/iterate.py:322-342). A problem is one row of logits[n_problems, n_vocab] (bf16 or fp16,
+ * row stride ld_logits); `table` is the engine's contiguous [n_vocab, n_items] cost table in the
+ * same dtype (auxiliary.py:62-63: -(auxiliary_vocabulary . W^T)^T).
+ *
+ * Sizes (the reference's limits, auxiliary.py:24-25 and iterate.py:298-300, and this build's):
+ * n_targets and k powers of two, k <= n_targets <= 128, k <= 16; n_items a power of two in
+ * [64, 8192] with k * max(1, n_items / 1024) <= 32; n_targets <= n_vocab <= 65536;
+ * 1 <= n_problems <= 65535. All pointers are device pointers. `table` has n_vocab rows; token ids
+ * handed in (tokens[]) are clamped into [0, n_vocab), so no input reads outside it.
+ *
+ * Ties the reference leaves to torch (topk, an unstable argsort) are fixed: the shortlist is the
+ * n_targets largest logits by (value descending, token id ascending); equal quota remainders rank
+ * by shortlist position. The fit's per-token loads are exact fixed-point sums (2^-48 units), so
+ * every output is reproducible bit for bit.
+ */
+
+/* Voronoi.shortlist + spread + prior (iterate.py:248-290) in one launch: tokens[N, M] (int64),
+ * counts[N, M] (int64, summing to n_items per row), unit[N], prior[N, M] (float; weight is the
+ * prior's weight, 0.1 in assign); values[N, M] (the shortlisted logits) and normaliser[N]
+ * (max + log sum exp) are optional (NULL: not written). */
+int plm_voronoi_shortlist(int32_t dtype, const void* logits, int64_t ld_logits, const void* table, int64_t n_problems,
+                          int64_t n_vocab, int64_t n_items, int64_t n_targets, float weight, int64_t* tokens,
+                          int64_t* counts, float* values, float* unit, float* prior, float* normaliser, void* stream);
+
+/* Voronoi.spread (iterate.py:275-284): unit[N] = mean over the first min(sample, 64, n_items)
+ * items of the gap between the worst and best of the row's targets, the gap in the table's dtype.
+ * Voronoi.prior (iterate.py:286-290): prior[N, M] = -weight * unit * log(max(counts / n_items,
+ * 1e-9)) for counts > 0, else 1000 * unit. plm_voronoi_shortlist computes both in its launch. */
+int plm_voronoi_spread(int32_t dtype, const void* table, int64_t n_vocab, int64_t n_items, const int64_t* tokens,
+                       int64_t n_problems, int64_t n_targets, int64_t sample, float* unit, void* stream);
+int plm_voronoi_prior(const int64_t* counts, const float* unit, int64_t n_problems, int64_t n_targets, int64_t n_items,
+                      float weight, float* prior, void* stream);
+
+/* condense (iterate.py:195-211): key[N, k, n_items] (int32), each item's k smallest packed keys of
+ * table[tokens[m], item] + offset[m] (the cost's order-preserving bits with the low 7 replaced by
+ * m), ascending. */
+int plm_voronoi_condense(int32_t dtype, const void* table, int64_t n_vocab, int64_t n_items, const int64_t* tokens,
+                         const float* offset, int64_t n_problems, int64_t n_targets, int64_t k, int32_t* key,
+                         void* stream);
+
+/* Voronoi.fit (iterate.py:292-312): `iterations` annealed Sinkhorn sweeps from temperature
+ * epsilon * unit down by (endpoint / epsilon)^(1/iterations) per sweep, each factor's step clamped
+ * to +-limit * unit and over-relaxed by `relax`; out[N, M] = offset + correction. The reference's
+ * defaults are relax 1.9, endpoint 0.0087, limit 0.25. */
+int plm_voronoi_fit(const int32_t* key, const int64_t* counts, const float* offset, const float* unit,
+                    int64_t n_problems, int64_t n_targets, int64_t k, int64_t n_items, int64_t iterations,
+                    float epsilon, float relax, float endpoint, float limit, float* out, void* stream);
+
+/* Voronoi.argmin (iterate.py:314-320): sigma[N, n_items] = argmin_m table[tokens[m], a] + bias[m]
+ * (int64, lowest m on ties). */
+int plm_voronoi_argmin(int32_t dtype, const void* table, int64_t n_vocab, int64_t n_items, const int64_t* tokens,
+                       const float* bias, int64_t n_problems, int64_t n_targets, int64_t* sigma, void* stream);
+
+/*
+ * Voronoi.assign (iterate.py:322-342) and decode_unmasked (auxiliary.py:67-75): shortlist, then
+ * `rounds` of condense + fit (the first from epsilon, later ones from epsilon * refocus), all on
+ * `stream`. Outputs, each optional (NULL: not written): decoded[N] = tokens[sigma[values[n]]] with
+ * values clamped to [0, n_items) (values and decoded go together); tokens_out[N, M], counts_out[N, M],
+ * bias_out[N, M] (the fitted factors); sigma[N, n_items] (one more launch). The reference's defaults
+ * are n_targets 128, k 8, rounds 2, iterations 12, weight 0.1, epsilon 0.15, refocus 0.35, relax 1.9,
+ * endpoint 0.0087, limit 0.25. Workspace: plm_voronoi_assign_workspace_bytes, 16-byte aligned; its
+ * counter area is not touched (the scratch after it is), so the GEMMs' workspace can be shared.
+ */
+int plm_voronoi_assign(int32_t dtype, const void* logits, int64_t ld_logits, const void* table, int64_t n_problems,
+                       int64_t n_vocab, int64_t n_items, int64_t n_targets, int64_t k, int64_t rounds,
+                       int64_t iterations, float weight, float epsilon, float refocus, float relax, float endpoint,
+                       float limit, const int64_t* values, int64_t* decoded, int64_t* tokens_out,
+                       int64_t* counts_out, float* bias_out, int64_t* sigma, void* workspace, size_t workspace_bytes,
+                       void* stream);
+size_t plm_voronoi_assign_workspace_bytes(int64_t n_problems, int64_t n_targets, int64_t k, int64_t n_items);
 
 /* Human-readable name of a status code. */
 const char* plm_status_string(int32_t status);

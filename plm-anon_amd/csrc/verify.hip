@@ -53,6 +53,9 @@ struct VerifyArgs {
   float* gstate;       // packed verify: [groups][R][3], the merged state of each group
   int* gstate_idx;     // packed verify: [groups][R]
   RoundEpilogue round;  // packed verify: k > 0 runs the round's epilogue after the last merge
+  uint16_t* logits;     // packed verify: rows [0, logit_rows) of the logits in the model dtype, or null
+  int64_t ld_logits;
+  int logit_rows;
 };
 
 // Online-softmax state of one row: maximum, sum of exp(l - max), sum of exp(l - max) over l > l_own,
@@ -500,6 +503,35 @@ __device__ __forceinline__ void fold_columns(const f32x4 (&acc)[NF][MT], int n0,
   }
 }
 
+// Writes the logits of rows [0, logit_rows) that this wavefront's accumulators hold, rounded to the
+// model dtype (the values the decision reads when the round mode is the model dtype's): lane l
+// holds vocabulary rows n0 + 16f + i, i = 0..3, of row 16t + l%16, one 8-byte store each.
+template <int DT, int MT, int NF>
+__device__ __forceinline__ void store_logits(const f32x4 (&acc)[NF][MT], int n0, const VerifyArgs& a) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    if (16 * t >= a.logit_rows) break;
+    const int m = 16 * t + (lane & 15);
+    if (m >= a.logit_rows) continue;
+    uint16_t* dst = a.logits + static_cast<int64_t>(m) * a.ld_logits;
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const int n = n0 + 16 * f;
+      if (n + 3 < a.V) {
+        u32x2 v;
+        v[0] = static_cast<uint32_t>(to_bits16<DT>(acc[f][t][0])) | (static_cast<uint32_t>(to_bits16<DT>(acc[f][t][1])) << 16);
+        v[1] = static_cast<uint32_t>(to_bits16<DT>(acc[f][t][2])) | (static_cast<uint32_t>(to_bits16<DT>(acc[f][t][3])) << 16);
+        *reinterpret_cast<u32x2*>(dst + n) = v;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (n + i < a.V) dst[n + i] = to_bits16<DT>(acc[f][t][i]);
+      }
+    }
+  }
+}
+
 template <int MT, int NF, int D>
 constexpr bool verify_packed_compiled() {
   return MT >= 1 && MT <= 4 && (NF == 2 || NF == 4) && (D == 2 || D == 4 || D == 8) && packed_compiled<MT, NF, D, 1>();
@@ -587,6 +619,7 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D
       // Fold this wavefront's 16*NF columns into the row states (rounding mode resolved once per
       // item, not per element).
       const int n0 = (cp.item * kPackedWaves + wave) * NF * 16 + 4 * (lane >> 4);
+      if (a.logit_rows > 0) store_logits<DT, MT, NF>(acc, n0, a);
       if (a.round_mode == PLM_ROUND_BF16)
         fold_columns<MT, NF, PLM_ROUND_BF16>(acc, n0, a.V, own_l, rs);
       else if (a.round_mode == PLM_ROUND_F16)
@@ -812,7 +845,14 @@ namespace {
 int packed_verify_entry(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, int64_t R, int64_t V,
                         int64_t K, const int64_t* pending, int64_t pending_rows, int32_t rule, float p,
                         int32_t round_mode, uint8_t* accept, int64_t* argmax, const plm::RoundEpilogue& round,
-                        const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream) {
+                        const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream,
+                        void* logits = nullptr, int64_t ld_logits = 0, int64_t logit_rows = 0) {
+  if (logit_rows < 0 || logit_rows > R || (logit_rows > 0 && logits == nullptr)) return PLM_ERR_ARGUMENT;
+  if (logit_rows > 0) {
+    // The logits handed out are the ones the decision reads: the round mode is the model dtype.
+    if (round_mode != (dtype == PLM_BF16 ? PLM_ROUND_BF16 : PLM_ROUND_F16) || ld_logits < V) return PLM_ERR_ARGUMENT;
+    if (ld_logits % 8 != 0 || !plm::aligned16_ptr(logits)) return PLM_ERR_ALIGNMENT;
+  }
   if (x == nullptr || packed_w == nullptr || (pending_rows > 0 && pending == nullptr) || tile == nullptr)
     return PLM_ERR_ARGUMENT;
   if (dtype != PLM_BF16 && dtype != PLM_F16) return PLM_ERR_ARGUMENT;
@@ -845,6 +885,9 @@ int packed_verify_entry(int32_t dtype, const void* x, int64_t ldx, const void* p
   a.accept = accept;
   a.argmax = argmax;
   a.round = round;
+  a.logits = logit_rows > 0 ? static_cast<uint16_t*>(logits) : nullptr;
+  a.ld_logits = ld_logits;
+  a.logit_rows = static_cast<int>(logit_rows);
   char* ws = static_cast<char*>(workspace);
   a.counter = reinterpret_cast<int*>(ws) + plm::kVerifyCounter;
   a.own = reinterpret_cast<float*>(ws + own_off);
@@ -876,6 +919,17 @@ int plm_lm_head_verify_packed(int32_t dtype, const void* x, int64_t ldx, const v
   if (pending == nullptr || accept == nullptr || argmax == nullptr) return PLM_ERR_ARGUMENT;
   return packed_verify_entry(dtype, x, ldx, packed_w, R, V, K, pending, R, rule, p, round_mode, accept, argmax,
                              plm::RoundEpilogue{}, tile, workspace, workspace_bytes, stream);
+}
+
+int plm_lm_head_verify_packed_logits(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, int64_t R,
+                                     int64_t V, int64_t K, const int64_t* pending, int64_t pending_rows, int32_t rule,
+                                     float p, int32_t round_mode, uint8_t* accept, int64_t* argmax, void* logits,
+                                     int64_t ld_logits, int64_t logit_rows, const plm_tile* tile, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  if (accept == nullptr || argmax == nullptr || pending_rows < 0 || pending_rows > R) return PLM_ERR_ARGUMENT;
+  return packed_verify_entry(dtype, x, ldx, packed_w, R, V, K, pending, pending_rows, rule, p, round_mode, accept,
+                             argmax, plm::RoundEpilogue{}, tile, workspace, workspace_bytes, stream, logits, ld_logits,
+                             logit_rows);
 }
 
 int plm_round_verify_packed(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, int64_t k, int64_t V,

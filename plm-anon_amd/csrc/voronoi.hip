@@ -1,0 +1,931 @@
+// Logit-Voronoi auxiliary decode on gfx950: the token a verify row's auxiliary value decodes to,
+// from that row's logits and the (V, A) cost table (plm/auxiliary.py:67-75 over the ``iterate``
+// engine, plm/iterate.py:176-342).
+//
+// A problem is one verify row. Per problem:
+//   1. voronoi_shortlist_kernel, one 1024-thread workgroup: the row's softmax normaliser, its
+//      n_targets largest logits (value descending, token id ascending), their largest-remainder
+//      quotas of the A items, the cost unit and the prior factor (iterate.py:248-290) in one launch.
+//      The row stays in registers as 16-bit order keys; a threshold (the n_targets-th largest
+//      per-thread maximum, found by bisection over the 16-bit key space) keeps every element of
+//      the top n_targets, and only the few elements above it are sorted (bitonic, in LDS).
+//   2. voronoi_condense_kernel, items spread over workgroups: each item's k cheapest packed keys
+//      of cost + offset (iterate.py:87-107).
+//   3. voronoi_fit_kernel, one 1024-thread workgroup: the annealed Sinkhorn sweeps on the condensed
+//      problem (iterate.py:110-159). Each thread owns items and all their k slots, so an item's
+//      softmax needs no exchange. The per-token loads are summed in 64-bit fixed point (units of
+//      2^-48) with integer LDS atomics: integer addition is associative, so the sums, and the
+//      fitted factors, are the same bit for bit whatever order the lanes add in (the reference's
+//      fp32 atomics are not, iterate.py:8-9).
+//   2-3 repeat per round; the last fit also resolves the problem's one auxiliary value.
+//   4. voronoi_argmin_kernel (only when sigma is asked for): the assignment of every item.
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cmath>
+
+#include "plm_amd.h"
+#include "tile.h"
+
+namespace plm {
+namespace {
+
+constexpr int kRowThreads = 1024;  // shortlist and fit workgroups
+constexpr int kRowWaves = kRowThreads / 64;
+constexpr int kCandidateCap = 2048;
+constexpr int kMaxTargets = 128;   // the packed key keeps the target in its low 7 bits
+constexpr int kMaxVocab = 65536;   // token ids ride in the low 16 bits of the sort key
+constexpr int kMaxItems = 8192;
+constexpr int kMinItems = 64;
+constexpr int kMaxSlots = 16;
+constexpr int kItemThreads = 256;  // condense and argmin workgroups
+constexpr int kSpreadSample = 64;  // iterate.py:275
+constexpr float kBlocked = 1e3f;   // iterate.py:25
+constexpr float kLoadFloor = 1e-2f;
+constexpr float kEmpty = -1e30f;   // iterate.py:26
+constexpr double kFixedUnit = 1.0 / 281474976710656.0;  // 2^-48
+
+// Order-preserving 16-bit key of a bf16 or fp16 value (both keep the sign in bit 15): a larger
+// value has a larger key. -0 is folded onto +0 first so equal values have equal keys.
+__device__ __forceinline__ uint32_t order_key16(uint32_t bits) {
+  if (bits == 0x8000u) bits = 0;
+  return bits ^ ((bits & 0x8000u) ? 0xFFFFu : 0x8000u);
+}
+__device__ __forceinline__ uint32_t key16_bits(uint32_t key) { return key ^ ((key & 0x8000u) ? 0x8000u : 0xFFFFu); }
+
+// A caller's token id as a table row, clamped into [0, V) so no input reads outside the table.
+__device__ __forceinline__ int64_t table_row(int64_t token, int V) { return token < 0 ? 0 : (token >= V ? V - 1 : token); }
+
+// -------------------------------------------------------------------------- block reductions
+// 1024 threads. Every thread gets the result; each call ends with one barrier and alternates
+// between two scratch rows, so consecutive calls need no barrier between them.
+
+struct BlockScratch {
+  int i[2][kRowWaves];
+  float f[2][kRowWaves];
+  uint32_t u[2][kRowWaves];
+};
+
+__device__ __forceinline__ int block_count(bool pred, BlockScratch& s, int& parity) {
+  const int n = __popcll(__ballot(pred));
+  if ((threadIdx.x & 63) == 0) s.i[parity][threadIdx.x >> 6] = n;
+  __syncthreads();
+  int total = 0;
+#pragma unroll
+  for (int w = 0; w < kRowWaves; ++w) total += s.i[parity][w];
+  parity ^= 1;
+  return total;
+}
+
+__device__ __forceinline__ int block_sum_int(int v, BlockScratch& s, int& parity) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  if ((threadIdx.x & 63) == 0) s.i[parity][threadIdx.x >> 6] = v;
+  __syncthreads();
+  int total = 0;
+#pragma unroll
+  for (int w = 0; w < kRowWaves; ++w) total += s.i[parity][w];
+  parity ^= 1;
+  return total;
+}
+
+// Butterfly within the wavefront (a + b == b + a bit for bit, so every lane ends equal), then the
+// wavefront sums in wavefront order: a fixed summation order.
+__device__ __forceinline__ float block_sum_float(float v, BlockScratch& s, int& parity) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  if ((threadIdx.x & 63) == 0) s.f[parity][threadIdx.x >> 6] = v;
+  __syncthreads();
+  float total = 0.f;
+#pragma unroll
+  for (int w = 0; w < kRowWaves; ++w) total += s.f[parity][w];
+  parity ^= 1;
+  return total;
+}
+
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t v, BlockScratch& s, int& parity) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), off, 64)));
+  if ((threadIdx.x & 63) == 0) s.u[parity][threadIdx.x >> 6] = v;
+  __syncthreads();
+  uint32_t total = 0;
+#pragma unroll
+  for (int w = 0; w < kRowWaves; ++w) total = max(total, s.u[parity][w]);
+  parity ^= 1;
+  return total;
+}
+
+// Exclusive prefix sum over the workgroup in thread order; `total` gets the sum.
+__device__ __forceinline__ int block_exclusive_scan(int v, int& total, BlockScratch& s, int& parity) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int inc = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(inc, off, 64);
+    if (lane >= off) inc += y;
+  }
+  if (lane == 63) s.i[parity][wave] = inc;
+  __syncthreads();
+  int base = 0;
+  total = 0;
+#pragma unroll
+  for (int w = 0; w < kRowWaves; ++w) {
+    const int c = s.i[parity][w];
+    base += w < wave ? c : 0;
+    total += c;
+  }
+  parity ^= 1;
+  return base + inc - v;
+}
+
+// Descending bitonic sort of s[0, n), n a power of two.
+__device__ void bitonic_descending(uint32_t* s, int n) {
+  for (int size = 2; size <= n; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = threadIdx.x; i < (n >> 1); i += kRowThreads) {
+        const int lo = 2 * i - (i & (stride - 1));
+        const int hi = lo + stride;
+        const bool descending = (lo & size) == 0;
+        const uint32_t x = s[lo], y = s[hi];
+        if ((x < y) == descending) {
+          s[lo] = y;
+          s[hi] = x;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ float round_model(float v) {
+  if constexpr (DT == DT_BF16) return static_cast<float>(static_cast<__bf16>(v));
+  return static_cast<float>(static_cast<_Float16>(v));
+}
+
+// Spread (iterate.py:275-284): the mean over the first min(sample, A) items of the gap between the
+// worst and best of the M targets tok_s[] (in LDS), the gap rounded to the table's dtype as the
+// reference subtracts in it. Called by all 1024 threads.
+template <int DT>
+__device__ float spread_unit(const uint16_t* table, int A, const int* tok_s, int M, int sample,
+                             float (*lo_s)[kSpreadSample], float (*hi_s)[kSpreadSample], BlockScratch& red,
+                             int& parity) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int cols = min(min(sample, kSpreadSample), A);
+  float lo = INFINITY, hi = -INFINITY;
+  if (lane < cols) {
+    for (int m = wave; m < M; m += kRowWaves) {
+      const float v = from_bits16<DT>(table[static_cast<int64_t>(tok_s[m]) * A + lane]);
+      lo = fminf(lo, v);
+      hi = fmaxf(hi, v);
+    }
+  }
+  lo_s[wave][lane] = lo;
+  hi_s[wave][lane] = hi;
+  __syncthreads();
+  float gap = 0.f;
+  if (wave == 0) {
+    lo = lo_s[0][lane];
+    hi = hi_s[0][lane];
+#pragma unroll
+    for (int g = 1; g < kRowWaves; ++g) {
+      lo = fminf(lo, lo_s[g][lane]);
+      hi = fmaxf(hi, hi_s[g][lane]);
+    }
+    gap = lane < cols ? round_model<DT>(hi - lo) : 0.f;
+  }
+  return block_sum_float(gap, red, parity) / static_cast<float>(cols);
+}
+
+// Prior (iterate.py:286-290), in the reference's operation order.
+__device__ __forceinline__ float prior_factor(int64_t count, float unit, int A, float weight) {
+  const float share = fmaxf(static_cast<float>(count) / static_cast<float>(A), 1e-9f);
+  const float scale = -weight * unit;
+  return count > 0 ? scale * logf(share) : kBlocked * unit;
+}
+
+// -------------------------------------------------------------------------- 1. shortlist
+
+struct ShortArgs {
+  const uint16_t* logits;
+  int64_t ld;
+  const uint16_t* table;
+  int V, A, M;
+  float weight;
+  int64_t* tokens;   // [N][M]
+  int64_t* counts;   // [N][M]
+  float* values;     // [N][M] or null
+  float* unit;       // [N]
+  float* prior;      // [N][M]
+  float* normaliser; // [N] or null
+};
+
+// JT = elements per thread (a multiple of 8 covering V / 1024).
+template <int DT, int JT>
+__global__ __launch_bounds__(kRowThreads) void voronoi_shortlist_kernel(ShortArgs a) {
+  __shared__ uint32_t cand[kCandidateCap];
+  __shared__ BlockScratch red;
+  __shared__ float lo_s[kRowWaves][kSpreadSample], hi_s[kRowWaves][kSpreadSample];
+  __shared__ float rem_s[kMaxTargets];
+  __shared__ int tok_s[kMaxTargets];
+  int parity = 0;
+  const int t = threadIdx.x;
+  const int64_t p = blockIdx.x;
+  const int M = a.M;
+  const uint16_t* row = a.logits + p * a.ld;
+
+  // The row as order keys, two per register; key 0 marks a position past the vocabulary.
+  // Element j of this thread is token t + 1024 j.
+  uint32_t kk[JT / 2];
+  uint32_t kmax = 0;
+#pragma unroll
+  for (int j = 0; j < JT; ++j) {
+    const int i = t + kRowThreads * j;
+    const uint32_t k = i < a.V ? order_key16(row[i]) : 0u;
+    if (j & 1)
+      kk[j >> 1] |= k << 16;
+    else
+      kk[j >> 1] = k;
+    kmax = max(kmax, k);
+  }
+  auto key_of = [&](int j) -> uint32_t { return (kk[j >> 1] >> (16 * (j & 1))) & 0xFFFFu; };
+
+  // Normaliser max + log(sum exp(l - max)) (iterate.py:56-80), values clamped to the reference's
+  // finite stand-in for -inf.
+  const uint32_t bmax = block_max_u32(kmax, red, parity);
+  const float mx = fmaxf(from_bits16<DT>(static_cast<uint16_t>(key16_bits(bmax))), kEmpty);
+  float se = 0.f;
+#pragma unroll
+  for (int j = 0; j < JT; ++j) {
+    const uint32_t k = key_of(j);
+    if (k != 0) se += __expf(fmaxf(from_bits16<DT>(static_cast<uint16_t>(key16_bits(k))), kEmpty) - mx);
+  }
+  se = block_sum_float(se, red, parity);
+  const float norm = mx + logf(se);
+
+  // Threshold: the M-th largest per-thread maximum. At least M elements reach it, so the M
+  // largest elements all do.
+  uint32_t tau = 0;
+  for (int bit = 15; bit >= 0; --bit) {
+    const uint32_t c = tau | (1u << bit);
+    if (block_count(kmax >= c, red, parity) >= M) tau = c;
+  }
+  int mine = 0;
+#pragma unroll
+  for (int j = 0; j < JT; ++j) {
+    const uint32_t k = key_of(j);
+    mine += (k != 0 && k >= tau) ? 1 : 0;
+  }
+  int total = 0;
+  int off = block_exclusive_scan(mine, total, red, parity);
+  // Sort key: value key above, 0xFFFF - token below, so equal values order by ascending token id.
+  if (total > kCandidateCap) {
+    // Many elements tie at the threshold (flat logits): bisect the full 32-bit sort key instead,
+    // which leaves exactly M elements at or above it. Rare, so the passes re-read the row rather
+    // than hold sort keys in registers.
+    auto sort_key = [&](int i) -> uint32_t {
+      const uint32_t k = order_key16(row[i]);
+      return k == 0 ? 0u : ((k << 16) | (0xFFFFu - static_cast<uint32_t>(i)));
+    };
+    uint32_t kappa = 0;
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t c = kappa | (1u << bit);
+      int n = 0;
+      for (int i = t; i < a.V; i += kRowThreads) n += sort_key(i) >= c ? 1 : 0;
+      if (block_sum_int(n, red, parity) >= M) kappa = c;
+    }
+    mine = 0;
+    for (int i = t; i < a.V; i += kRowThreads) mine += sort_key(i) >= kappa ? 1 : 0;
+    off = block_exclusive_scan(mine, total, red, parity);
+    for (int i = t; i < a.V; i += kRowThreads) {
+      const uint32_t sk = sort_key(i);
+      if (sk >= kappa && sk != 0) cand[off++] = sk;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < JT; ++j) {
+      const uint32_t k = key_of(j);
+      if (k != 0 && k >= tau) cand[off++] = (k << 16) | (0xFFFFu - static_cast<uint32_t>(t + kRowThreads * j));
+    }
+  }
+  int n_sort = M;
+  while (n_sort < total) n_sort <<= 1;
+  for (int i = total + t; i < n_sort; i += kRowThreads) cand[i] = 0u;
+  __syncthreads();
+  bitonic_descending(cand, n_sort);
+
+  // Quotas (iterate.py:214-223, 272-273): threads < M hold target t.
+  float val = 0.f, pr = 0.f;
+  if (t < M) {
+    const uint32_t sk = cand[t];
+    tok_s[t] = min(static_cast<int>(0xFFFFu - (sk & 0xFFFFu)), a.V - 1);  // in range even for a degenerate row
+    val = from_bits16<DT>(static_cast<uint16_t>(key16_bits(sk >> 16)));
+    pr = expf(val - norm);
+  }
+  const float psum = block_sum_float(pr, red, parity);
+  float rem = 0.f;
+  int cnt = 0;
+  if (t < M) {
+    const float exact = (pr / psum) * static_cast<float>(a.A);
+    const float fl = floorf(exact);
+    cnt = static_cast<int>(fl);
+    rem = exact - fl;
+    rem_s[t] = rem;
+  }
+  const int remaining = a.A - block_sum_int(cnt, red, parity);  // barrier also publishes rem_s / tok_s
+  if (t < M) {
+    int rank = 0;
+    for (int j = 0; j < M; ++j) {
+      const float r = rem_s[j];
+      rank += (r > rem || (r == rem && j < t)) ? 1 : 0;
+    }
+    cnt += rank < remaining ? 1 : 0;
+  }
+
+  const float unit = spread_unit<DT>(a.table, a.A, tok_s, M, kSpreadSample, lo_s, hi_s, red, parity);
+  if (t < M) {
+    const int64_t o = p * M + t;
+    a.prior[o] = prior_factor(cnt, unit, a.A, a.weight);
+    a.tokens[o] = tok_s[t];
+    a.counts[o] = cnt;
+    if (a.values != nullptr) a.values[o] = val;
+  }
+  if (t == 0) {
+    a.unit[p] = unit;
+    if (a.normaliser != nullptr) a.normaliser[p] = norm;
+  }
+}
+
+// Standalone spread and prior, for callers that run the engine's steps one by one.
+struct SpreadArgs {
+  const uint16_t* table;
+  const int64_t* tokens;
+  float* unit;
+  int V, M, A, sample;
+};
+
+template <int DT>
+__global__ __launch_bounds__(kRowThreads) void voronoi_spread_kernel(SpreadArgs a) {
+  __shared__ BlockScratch red;
+  __shared__ float lo_s[kRowWaves][kSpreadSample], hi_s[kRowWaves][kSpreadSample];
+  __shared__ int tok_s[kMaxTargets];
+  int parity = 0;
+  const int64_t p = blockIdx.x;
+  if (threadIdx.x < a.M) tok_s[threadIdx.x] = static_cast<int>(table_row(a.tokens[p * a.M + threadIdx.x], a.V));
+  __syncthreads();
+  const float unit = spread_unit<DT>(a.table, a.A, tok_s, a.M, a.sample, lo_s, hi_s, red, parity);
+  if (threadIdx.x == 0) a.unit[p] = unit;
+}
+
+__global__ __launch_bounds__(kMaxTargets) void voronoi_prior_kernel(const int64_t* counts, const float* unit,
+                                                                     float* prior, int M, int A, float weight) {
+  const int64_t p = blockIdx.x;
+  if (threadIdx.x < M) prior[p * M + threadIdx.x] = prior_factor(counts[p * M + threadIdx.x], unit[p], A, weight);
+}
+
+// -------------------------------------------------------------------------- 2. condense
+
+struct CondenseArgs {
+  const uint16_t* table;
+  const int64_t* tokens;  // [N][M]
+  const float* offset;    // [N][M]
+  int32_t* key;           // [N][K][A]
+  int V, M, A;
+};
+
+__device__ __forceinline__ int32_t pack_cost(float c, int target) {
+  const int32_t bits = __builtin_bit_cast(int32_t, c);
+  const int32_t ordered = bits >= 0 ? bits : (bits ^ 0x7FFFFFFF);
+  return (ordered & ~0x7F) | target;
+}
+
+template <int DT, int K>
+__global__ __launch_bounds__(kItemThreads) void voronoi_condense_kernel(CondenseArgs a) {
+  __shared__ int64_t row_s[kMaxTargets];
+  __shared__ float off_s[kMaxTargets];
+  const int t = threadIdx.x;
+  const int64_t p = blockIdx.y;
+  if (t < a.M) {
+    row_s[t] = table_row(a.tokens[p * a.M + t], a.V) * a.A;
+    off_s[t] = a.offset[p * a.M + t];
+  }
+  __syncthreads();
+  const int item = blockIdx.x * kItemThreads + t;
+  if (item >= a.A) return;
+  int32_t best[K];
+#pragma unroll
+  for (int s = 0; s < K; ++s) best[s] = INT_MAX;
+  constexpr int kBatch = 8;
+  for (int m0 = 0; m0 < a.M; m0 += kBatch) {
+    uint16_t raw[kBatch];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) raw[b] = m0 + b < a.M ? a.table[row_s[m0 + b] + item] : 0;
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      if (m0 + b >= a.M) break;
+      int32_t x = pack_cost(from_bits16<DT>(raw[b]) + off_s[m0 + b], m0 + b);
+#pragma unroll
+      for (int s = 0; s < K; ++s) {
+        const int32_t lo = min(best[s], x);
+        x = max(best[s], x);
+        best[s] = lo;
+      }
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < K; ++s) a.key[(p * K + s) * a.A + item] = best[s];
+}
+
+// -------------------------------------------------------------------------- 3. fit
+
+struct FitArgs {
+  const int32_t* key;     // [N][K][A]
+  const int64_t* counts;  // [N][M]
+  const float* offset;    // [N][M]
+  const float* unit;      // [N]
+  float* out;             // [N][M]
+  int V, M, A, iterations;
+  float epsilon, anneal, relax, limit;
+  // Resolve one item per problem after the sweeps (null table: no).
+  const uint16_t* table;
+  const int64_t* tokens;  // [N][M]
+  const int64_t* values;  // [N]
+  int64_t* decoded;       // [N]
+};
+
+// w in [0, 1 + 2^-23] -> units of 2^-48, exactly for w >= 2^-24 (every bit of its float32).
+__device__ __forceinline__ unsigned long long to_fixed48(float w) {
+  const float s = w * 65536.f;
+  const float hi = floorf(s);
+  const uint32_t lo = static_cast<uint32_t>((s - hi) * 4294967296.f);
+  return (static_cast<unsigned long long>(static_cast<uint32_t>(hi)) << 32) | lo;
+}
+
+// One target's sweep state: its factor correction and its load accumulator, 16 bytes so that one
+// register (the target's byte offset) addresses both with immediate offsets.
+struct alignas(16) TargetCell {
+  float corr;
+  float unused;
+  unsigned long long load;
+};
+
+template <int DT, int K, int IPT>
+__global__ __launch_bounds__(kRowThreads) void voronoi_fit_kernel(FitArgs a) {
+  __shared__ TargetCell cell[kMaxTargets];
+  __shared__ float share_s[kMaxTargets];
+  __shared__ int live_s[kMaxTargets];
+  __shared__ float best_v[kMaxTargets / 64];
+  __shared__ int best_i[kMaxTargets / 64];
+  const int t = threadIdx.x, lane = t & 63;
+  const int64_t p = blockIdx.x;
+  const int M = a.M, A = a.A;
+  if (t < M) {
+    const int64_t c = a.counts[p * M + t];
+    live_s[t] = c > 0;
+    share_s[t] = logf(fmaxf(static_cast<float>(c), 1e-9f));
+    cell[t].corr = 0.f;
+  }
+  const float u = a.unit[p];
+  float temperature = a.epsilon * u;
+  const float bound = a.limit * u;
+
+  // The condensed problem, decoded once (iterate.py:130-134): item t + 1024 q, slot (j + lane) % K
+  // in register j — the rotation spreads each wavefront's cheapest-slot targets over the K
+  // atomic instructions. A target is kept as its cell's byte offset.
+  float base[IPT][K];
+  uint32_t at[IPT][K];
+  bool valid[IPT];
+#pragma unroll
+  for (int q = 0; q < IPT; ++q) {
+    const int item = t + kRowThreads * q;
+    valid[q] = item < A;
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      const int s = (j + lane) & (K - 1);
+      const int32_t key = valid[q] ? a.key[(p * K + s) * A + item] : 0;
+      const int32_t carried = key & ~0x7F;
+      base[q][j] = __builtin_bit_cast(float, carried >= 0 ? carried : (carried ^ 0x7FFFFFFF));
+      at[q][j] = static_cast<uint32_t>(key & 0x7F) * static_cast<uint32_t>(sizeof(TargetCell));
+    }
+  }
+  char* cells = reinterpret_cast<char*>(cell);
+  __syncthreads();
+
+  for (int it = 0; it < a.iterations; ++it) {
+    if (t < M) cell[t].load = 0ull;
+    __syncthreads();
+    const float inv_t = 1.f / temperature;
+#pragma unroll
+    for (int q = 0; q < IPT; ++q) {
+      if (!valid[q]) continue;
+      float x[K];
+      float xm = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < K; ++j) {
+        x[j] = -(base[q][j] + *reinterpret_cast<const float*>(cells + at[q][j])) * inv_t;
+        xm = fmaxf(xm, x[j]);
+      }
+      float se = 0.f;
+#pragma unroll
+      for (int j = 0; j < K; ++j) {
+        x[j] = __expf(x[j] - xm);
+        se += x[j];
+      }
+      const float r = 1.f / se;
+#pragma unroll
+      for (int j = 0; j < K; ++j)
+        __hip_atomic_fetch_add(reinterpret_cast<unsigned long long*>(cells + at[q][j] + 8), to_fixed48(x[j] * r),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    __syncthreads();
+    if (t < M) {
+      const float load = static_cast<float>(static_cast<double>(cell[t].load) * kFixedUnit);
+      float step = temperature * (logf(fmaxf(load, kLoadFloor)) - share_s[t]);
+      step = fminf(fmaxf(step, -bound), bound);
+      const float c = cell[t].corr + a.relax * step;
+      cell[t].corr = live_s[t] ? c : 0.f;
+    }
+    __syncthreads();
+    temperature *= a.anneal;
+  }
+
+  float bias = 0.f;
+  if (t < M) {
+    bias = a.offset[p * M + t] + cell[t].corr;
+    a.out[p * M + t] = bias;
+  }
+  if (a.table == nullptr) return;
+  // auxiliary.py:70-75 for this problem's one value: argmin_m C[m, a] + b[m], lowest m on ties.
+  if (t < ((M + 63) & ~63)) {
+    int64_t item = a.values[p];
+    item = item < 0 ? 0 : (item > A - 1 ? A - 1 : item);
+    float v = INFINITY;
+    int idx = INT_MAX;
+    if (t < M) {
+      v = from_bits16<DT>(a.table[table_row(a.tokens[p * M + t], a.V) * A + item]) + bias;
+      idx = t;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(v, off, 64);
+      const int oi = __shfl_xor(idx, off, 64);
+      if (ov < v || (ov == v && oi < idx)) {
+        v = ov;
+        idx = oi;
+      }
+    }
+    if (lane == 0) {
+      best_v[t >> 6] = v;
+      best_i[t >> 6] = idx;
+    }
+  }
+  __syncthreads();
+  if (t == 0) {
+    float v = best_v[0];
+    int idx = best_i[0];
+    for (int w = 1; w < (M + 63) / 64; ++w)
+      if (best_v[w] < v || (best_v[w] == v && best_i[w] < idx)) {
+        v = best_v[w];
+        idx = best_i[w];
+      }
+    a.decoded[p] = a.tokens[p * M + idx];
+  }
+}
+
+// -------------------------------------------------------------------------- 4. argmin
+
+struct ArgminArgs {
+  const uint16_t* table;
+  const int64_t* tokens;  // [N][M]
+  const float* bias;      // [N][M]
+  int64_t* sigma;         // [N][A]
+  int V, M, A;
+};
+
+template <int DT>
+__global__ __launch_bounds__(kItemThreads) void voronoi_argmin_kernel(ArgminArgs a) {
+  __shared__ int64_t row_s[kMaxTargets];
+  __shared__ float bias_s[kMaxTargets];
+  const int t = threadIdx.x;
+  const int64_t p = blockIdx.y;
+  if (t < a.M) {
+    row_s[t] = table_row(a.tokens[p * a.M + t], a.V) * a.A;
+    bias_s[t] = a.bias[p * a.M + t];
+  }
+  __syncthreads();
+  const int item = blockIdx.x * kItemThreads + t;
+  if (item >= a.A) return;
+  float best = from_bits16<DT>(a.table[row_s[0] + item]) + bias_s[0];
+  int arg = 0;
+  for (int m = 1; m < a.M; ++m) {
+    const float c = from_bits16<DT>(a.table[row_s[m] + item]) + bias_s[m];
+    if (c < best) {
+      best = c;
+      arg = m;
+    }
+  }
+  a.sigma[p * a.A + item] = arg;
+}
+
+// -------------------------------------------------------------------------- host side
+
+bool pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
+
+template <int DT>
+hipError_t launch_shortlist(const ShortArgs& a, int64_t n, hipStream_t s) {
+  const int jt = static_cast<int>((a.V + kRowThreads - 1) / kRowThreads + 7) / 8 * 8;
+  const dim3 grid(static_cast<unsigned>(n)), block(kRowThreads);
+  switch (jt) {
+#define PLM_VOR_JT(J) \
+  case J: hipLaunchKernelGGL((voronoi_shortlist_kernel<DT, J>), grid, block, 0, s, a); break;
+    PLM_VOR_JT(8)
+    PLM_VOR_JT(16)
+    PLM_VOR_JT(24)
+    PLM_VOR_JT(32)
+    PLM_VOR_JT(40)
+    PLM_VOR_JT(48)
+    PLM_VOR_JT(56)
+    PLM_VOR_JT(64)
+#undef PLM_VOR_JT
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_condense(const CondenseArgs& a, int k, int64_t n, hipStream_t s) {
+  const dim3 grid((a.A + kItemThreads - 1) / kItemThreads, static_cast<unsigned>(n)), block(kItemThreads);
+  switch (k) {
+    case 1: hipLaunchKernelGGL((voronoi_condense_kernel<DT, 1>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((voronoi_condense_kernel<DT, 2>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((voronoi_condense_kernel<DT, 4>), grid, block, 0, s, a); break;
+    case 8: hipLaunchKernelGGL((voronoi_condense_kernel<DT, 8>), grid, block, 0, s, a); break;
+    case 16: hipLaunchKernelGGL((voronoi_condense_kernel<DT, 16>), grid, block, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <int DT, int K, int IPT>
+hipError_t launch_fit_kt(const FitArgs& a, int64_t n, hipStream_t s) {
+  if constexpr (K * IPT > 32) {
+    return hipErrorInvalidValue;
+  } else {
+    hipLaunchKernelGGL((voronoi_fit_kernel<DT, K, IPT>), dim3(static_cast<unsigned>(n)), dim3(kRowThreads), 0, s, a);
+    return hipGetLastError();
+  }
+}
+
+template <int DT, int K>
+hipError_t launch_fit_k(const FitArgs& a, int64_t n, hipStream_t s) {
+  switch (a.A > kRowThreads ? a.A / kRowThreads : 1) {
+    case 1: return launch_fit_kt<DT, K, 1>(a, n, s);
+    case 2: return launch_fit_kt<DT, K, 2>(a, n, s);
+    case 4: return launch_fit_kt<DT, K, 4>(a, n, s);
+    case 8: return launch_fit_kt<DT, K, 8>(a, n, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int DT>
+hipError_t launch_fit(const FitArgs& a, int k, int64_t n, hipStream_t s) {
+  switch (k) {
+    case 1: return launch_fit_k<DT, 1>(a, n, s);
+    case 2: return launch_fit_k<DT, 2>(a, n, s);
+    case 4: return launch_fit_k<DT, 4>(a, n, s);
+    case 8: return launch_fit_k<DT, 8>(a, n, s);
+    case 16: return launch_fit_k<DT, 16>(a, n, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int DT>
+hipError_t launch_argmin(const ArgminArgs& a, int64_t n, hipStream_t s) {
+  const dim3 grid((a.A + kItemThreads - 1) / kItemThreads, static_cast<unsigned>(n)), block(kItemThreads);
+  hipLaunchKernelGGL((voronoi_argmin_kernel<DT>), grid, block, 0, s, a);
+  return hipGetLastError();
+}
+
+int to_status(hipError_t e) { return e == hipSuccess ? PLM_OK : (e == hipErrorInvalidValue ? PLM_ERR_ARGUMENT : PLM_ERR_LAUNCH); }
+
+// Sizes the engine supports (the reference's own limits, auxiliary.py:24-25 and iterate.py:298-300,
+// plus the ones this implementation adds): n_targets and k powers of two with k <= n_targets <= 128,
+// k <= 16; A a power of two in [64, 8192] with k * max(1, A / 1024) <= 32 (the fit holds a thread's
+// k * A / 1024 condensed entries in registers); n_targets <= V <= 65536.
+bool sizes_ok(int64_t n, int64_t V, int64_t A, int64_t M, int64_t k) {
+  if (n < 1 || n > 65535) return false;
+  if (!pow2(M) || M > kMaxTargets || V < M || V > kMaxVocab) return false;
+  if (!pow2(A) || A < kMinItems || A > kMaxItems) return false;
+  if (k != 0 && (!pow2(k) || k > M || k > kMaxSlots || k * std::max<int64_t>(1, A / kRowThreads) > 32)) return false;
+  return true;
+}
+
+float anneal_factor(double endpoint, double epsilon, int64_t iterations) {
+  return static_cast<float>(std::pow(endpoint / epsilon, 1.0 / static_cast<double>(std::max<int64_t>(iterations, 1))));
+}
+
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+struct AssignLayout {
+  size_t tokens, counts, unit, bias0, bias1, key, total;
+};
+
+// After the shared workspace's counter area (left untouched), like every other entry point's.
+AssignLayout assign_layout(int64_t n, int64_t M, int64_t k, int64_t A) {
+  AssignLayout l{};
+  size_t o = kCounterBytes;
+  l.tokens = o;
+  o += align256(n * M * sizeof(int64_t));
+  l.counts = o;
+  o += align256(n * M * sizeof(int64_t));
+  l.unit = o;
+  o += align256(n * sizeof(float));
+  l.bias0 = o;
+  o += align256(n * M * sizeof(float));
+  l.bias1 = o;
+  o += align256(n * M * sizeof(float));
+  l.key = o;
+  o += align256(n * k * A * sizeof(int32_t));
+  l.total = o;
+  return l;
+}
+
+}  // namespace
+}  // namespace plm
+
+extern "C" {
+
+int plm_voronoi_shortlist(int32_t dtype, const void* logits, int64_t ld_logits, const void* table, int64_t n_problems,
+                          int64_t n_vocab, int64_t n_items, int64_t n_targets, float weight, int64_t* tokens,
+                          int64_t* counts, float* values, float* unit, float* prior, float* normaliser, void* stream) {
+  if (logits == nullptr || table == nullptr || tokens == nullptr || counts == nullptr || unit == nullptr ||
+      prior == nullptr)
+    return PLM_ERR_ARGUMENT;
+  if (dtype != PLM_BF16 && dtype != PLM_F16) return PLM_ERR_ARGUMENT;
+  if (!plm::sizes_ok(n_problems, n_vocab, n_items, n_targets, 0) || ld_logits < n_vocab) return PLM_ERR_ARGUMENT;
+  plm::ShortArgs a{static_cast<const uint16_t*>(logits), ld_logits, static_cast<const uint16_t*>(table),
+                   static_cast<int>(n_vocab), static_cast<int>(n_items), static_cast<int>(n_targets), weight,
+                   tokens, counts, values, unit, prior, normaliser};
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  return plm::to_status(dtype == PLM_BF16 ? plm::launch_shortlist<plm::DT_BF16>(a, n_problems, s)
+                                          : plm::launch_shortlist<plm::DT_F16>(a, n_problems, s));
+}
+
+int plm_voronoi_spread(int32_t dtype, const void* table, int64_t n_vocab, int64_t n_items, const int64_t* tokens,
+                       int64_t n_problems, int64_t n_targets, int64_t sample, float* unit, void* stream) {
+  if (table == nullptr || tokens == nullptr || unit == nullptr) return PLM_ERR_ARGUMENT;
+  if (dtype != PLM_BF16 && dtype != PLM_F16) return PLM_ERR_ARGUMENT;
+  if (!plm::sizes_ok(n_problems, n_vocab, n_items, n_targets, 0) || sample < 1 || sample > 64) return PLM_ERR_ARGUMENT;
+  plm::SpreadArgs a{static_cast<const uint16_t*>(table), tokens, unit, static_cast<int>(n_vocab),
+                    static_cast<int>(n_targets), static_cast<int>(n_items), static_cast<int>(sample)};
+  const dim3 grid(static_cast<unsigned>(n_problems)), block(1024);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == PLM_BF16)
+    hipLaunchKernelGGL((plm::voronoi_spread_kernel<plm::DT_BF16>), grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL((plm::voronoi_spread_kernel<plm::DT_F16>), grid, block, 0, s, a);
+  return plm::to_status(hipGetLastError());
+}
+
+int plm_voronoi_prior(const int64_t* counts, const float* unit, int64_t n_problems, int64_t n_targets, int64_t n_items,
+                      float weight, float* prior, void* stream) {
+  if (counts == nullptr || unit == nullptr || prior == nullptr) return PLM_ERR_ARGUMENT;
+  if (!plm::sizes_ok(n_problems, n_targets, n_items, n_targets, 0)) return PLM_ERR_ARGUMENT;
+  hipLaunchKernelGGL(plm::voronoi_prior_kernel, dim3(static_cast<unsigned>(n_problems)), dim3(128), 0,
+                     static_cast<hipStream_t>(stream), counts, unit, prior, static_cast<int>(n_targets),
+                     static_cast<int>(n_items), weight);
+  return plm::to_status(hipGetLastError());
+}
+
+int plm_voronoi_condense(int32_t dtype, const void* table, int64_t n_vocab, int64_t n_items, const int64_t* tokens,
+                         const float* offset, int64_t n_problems, int64_t n_targets, int64_t k, int32_t* key,
+                         void* stream) {
+  if (table == nullptr || tokens == nullptr || offset == nullptr || key == nullptr) return PLM_ERR_ARGUMENT;
+  if (dtype != PLM_BF16 && dtype != PLM_F16) return PLM_ERR_ARGUMENT;
+  if (!plm::sizes_ok(n_problems, n_vocab, n_items, n_targets, k) || k < 1) return PLM_ERR_ARGUMENT;
+  plm::CondenseArgs a{static_cast<const uint16_t*>(table), tokens, offset, key, static_cast<int>(n_vocab),
+                      static_cast<int>(n_targets), static_cast<int>(n_items)};
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  return plm::to_status(dtype == PLM_BF16 ? plm::launch_condense<plm::DT_BF16>(a, static_cast<int>(k), n_problems, s)
+                                          : plm::launch_condense<plm::DT_F16>(a, static_cast<int>(k), n_problems, s));
+}
+
+int plm_voronoi_fit(const int32_t* key, const int64_t* counts, const float* offset, const float* unit,
+                    int64_t n_problems, int64_t n_targets, int64_t k, int64_t n_items, int64_t iterations,
+                    float epsilon, float relax, float endpoint, float limit, float* out, void* stream) {
+  if (key == nullptr || counts == nullptr || offset == nullptr || unit == nullptr || out == nullptr)
+    return PLM_ERR_ARGUMENT;
+  if (!plm::sizes_ok(n_problems, n_targets, n_items, n_targets, k) || k < 1 || iterations < 0 ||
+      iterations > (1 << 20) || !(epsilon > 0.f) || !(endpoint > 0.f))
+    return PLM_ERR_ARGUMENT;
+  plm::FitArgs a{};
+  a.key = key;
+  a.counts = counts;
+  a.offset = offset;
+  a.unit = unit;
+  a.out = out;
+  a.M = static_cast<int>(n_targets);
+  a.A = static_cast<int>(n_items);
+  a.iterations = static_cast<int>(iterations);
+  a.epsilon = epsilon;
+  a.anneal = plm::anneal_factor(endpoint, epsilon, iterations);
+  a.relax = relax;
+  a.limit = limit;
+  return plm::to_status(plm::launch_fit<plm::DT_BF16>(a, static_cast<int>(k), n_problems, static_cast<hipStream_t>(stream)));
+}
+
+int plm_voronoi_argmin(int32_t dtype, const void* table, int64_t n_vocab, int64_t n_items, const int64_t* tokens,
+                       const float* bias, int64_t n_problems, int64_t n_targets, int64_t* sigma, void* stream) {
+  if (table == nullptr || tokens == nullptr || bias == nullptr || sigma == nullptr) return PLM_ERR_ARGUMENT;
+  if (dtype != PLM_BF16 && dtype != PLM_F16) return PLM_ERR_ARGUMENT;
+  if (!plm::sizes_ok(n_problems, n_vocab, n_items, n_targets, 0)) return PLM_ERR_ARGUMENT;
+  plm::ArgminArgs a{static_cast<const uint16_t*>(table), tokens, bias, sigma, static_cast<int>(n_vocab),
+                    static_cast<int>(n_targets), static_cast<int>(n_items)};
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  return plm::to_status(dtype == PLM_BF16 ? plm::launch_argmin<plm::DT_BF16>(a, n_problems, s)
+                                          : plm::launch_argmin<plm::DT_F16>(a, n_problems, s));
+}
+
+size_t plm_voronoi_assign_workspace_bytes(int64_t n_problems, int64_t n_targets, int64_t k, int64_t n_items) {
+  if (n_problems < 1 || n_targets < 1 || k < 1 || n_items < 1) return 0;
+  return plm::assign_layout(n_problems, n_targets, k, n_items).total;
+}
+
+int plm_voronoi_assign(int32_t dtype, const void* logits, int64_t ld_logits, const void* table, int64_t n_problems,
+                       int64_t n_vocab, int64_t n_items, int64_t n_targets, int64_t k, int64_t rounds,
+                       int64_t iterations, float weight, float epsilon, float refocus, float relax, float endpoint,
+                       float limit, const int64_t* values, int64_t* decoded, int64_t* tokens_out,
+                       int64_t* counts_out, float* bias_out, int64_t* sigma, void* workspace, size_t workspace_bytes,
+                       void* stream) {
+  if (logits == nullptr || table == nullptr) return PLM_ERR_ARGUMENT;
+  if (dtype != PLM_BF16 && dtype != PLM_F16) return PLM_ERR_ARGUMENT;
+  if ((values == nullptr) != (decoded == nullptr)) return PLM_ERR_ARGUMENT;
+  if (!plm::sizes_ok(n_problems, n_vocab, n_items, n_targets, k) || k < 1 || ld_logits < n_vocab) return PLM_ERR_ARGUMENT;
+  if (rounds < 1 || rounds > 64 || iterations < 0 || iterations > (1 << 20) || !(epsilon > 0.f) || !(endpoint > 0.f) ||
+      !(refocus > 0.f))
+    return PLM_ERR_ARGUMENT;
+  const plm::AssignLayout l = plm::assign_layout(n_problems, n_targets, k, n_items);
+  if (workspace == nullptr || workspace_bytes < l.total || !plm::aligned16_ptr(workspace)) return PLM_ERR_WORKSPACE;
+  char* ws = static_cast<char*>(workspace);
+  int64_t* tokens = tokens_out != nullptr ? tokens_out : reinterpret_cast<int64_t*>(ws + l.tokens);
+  int64_t* counts = counts_out != nullptr ? counts_out : reinterpret_cast<int64_t*>(ws + l.counts);
+  float* unit = reinterpret_cast<float*>(ws + l.unit);
+  float* bias[2] = {reinterpret_cast<float*>(ws + l.bias0), reinterpret_cast<float*>(ws + l.bias1)};
+  int32_t* key = reinterpret_cast<int32_t*>(ws + l.key);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool bf16 = dtype == PLM_BF16;
+
+  plm::ShortArgs sa{static_cast<const uint16_t*>(logits), ld_logits, static_cast<const uint16_t*>(table),
+                    static_cast<int>(n_vocab), static_cast<int>(n_items), static_cast<int>(n_targets), weight,
+                    tokens, counts, nullptr, unit, bias[0], nullptr};
+  hipError_t err = bf16 ? plm::launch_shortlist<plm::DT_BF16>(sa, n_problems, s)
+                        : plm::launch_shortlist<plm::DT_F16>(sa, n_problems, s);
+  if (err != hipSuccess) return plm::to_status(err);
+  // iterate.py:336-340: each round condenses against the current factors and refits them; the
+  // second and later rounds anneal from epsilon * refocus.
+  for (int64_t r = 0; r < rounds; ++r) {
+    float* offset = bias[r & 1];
+    const bool last = r == rounds - 1;
+    float* out = last && bias_out != nullptr ? bias_out : bias[(r + 1) & 1];
+    plm::CondenseArgs ca{static_cast<const uint16_t*>(table), tokens, offset, key, static_cast<int>(n_vocab),
+                         static_cast<int>(n_targets), static_cast<int>(n_items)};
+    err = bf16 ? plm::launch_condense<plm::DT_BF16>(ca, static_cast<int>(k), n_problems, s)
+               : plm::launch_condense<plm::DT_F16>(ca, static_cast<int>(k), n_problems, s);
+    if (err != hipSuccess) return plm::to_status(err);
+    const double eps = r == 0 ? static_cast<double>(epsilon) : static_cast<double>(epsilon) * static_cast<double>(refocus);
+    plm::FitArgs fa{};
+    fa.key = key;
+    fa.counts = counts;
+    fa.offset = offset;
+    fa.unit = unit;
+    fa.out = out;
+    fa.V = static_cast<int>(n_vocab);
+    fa.M = static_cast<int>(n_targets);
+    fa.A = static_cast<int>(n_items);
+    fa.iterations = static_cast<int>(iterations);
+    fa.epsilon = static_cast<float>(eps);
+    fa.anneal = plm::anneal_factor(endpoint, eps, iterations);
+    fa.relax = relax;
+    fa.limit = limit;
+    if (last && values != nullptr) {
+      fa.table = static_cast<const uint16_t*>(table);
+      fa.tokens = tokens;
+      fa.values = values;
+      fa.decoded = decoded;
+    }
+    err = bf16 ? plm::launch_fit<plm::DT_BF16>(fa, static_cast<int>(k), n_problems, s)
+               : plm::launch_fit<plm::DT_F16>(fa, static_cast<int>(k), n_problems, s);
+    if (err != hipSuccess) return plm::to_status(err);
+    if (last && out != bias[(r + 1) & 1]) bias[(r + 1) & 1] = out;
+  }
+  if (sigma != nullptr) {
+    plm::ArgminArgs aa{static_cast<const uint16_t*>(table), tokens, bias[rounds & 1], sigma,
+                       static_cast<int>(n_vocab), static_cast<int>(n_targets), static_cast<int>(n_items)};
+    err = bf16 ? plm::launch_argmin<plm::DT_BF16>(aa, n_problems, s) : plm::launch_argmin<plm::DT_F16>(aa, n_problems, s);
+    if (err != hipSuccess) return plm::to_status(err);
+  }
+  return PLM_OK;
+}
+
+}  // extern "C"

@@ -49,10 +49,19 @@ EXPORTS = (
     "plm_lm_head_verify",
     "plm_lm_head_verify_workspace_bytes",
     "plm_lm_head_verify_packed",
+    "plm_lm_head_verify_packed_logits",
     "plm_round_epilogue",
     "plm_round_verify_packed",
     "plm_gemm_packed_lora",
     "plm_gemm_packed_lora_workspace_bytes",
+    "plm_voronoi_shortlist",
+    "plm_voronoi_spread",
+    "plm_voronoi_prior",
+    "plm_voronoi_condense",
+    "plm_voronoi_fit",
+    "plm_voronoi_argmin",
+    "plm_voronoi_assign",
+    "plm_voronoi_assign_workspace_bytes",
     "plm_status_string",
 )
 
@@ -140,6 +149,29 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.plm_gemm_packed_lora.restype = ctypes.c_int
     lib.plm_gemm_packed_lora_workspace_bytes.argtypes = [c_i64, c_i64, c_i64, c_i64, c_i64, c_i32, tile_p]
     lib.plm_gemm_packed_lora_workspace_bytes.restype = c_sz
+    lib.plm_lm_head_verify_packed_logits.argtypes = [c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_p, c_i64, c_i32,
+                                                     ctypes.c_float, c_i32, c_p, c_p, c_p, c_i64, c_i64, tile_p, c_p,
+                                                     c_sz, c_p]
+    lib.plm_lm_head_verify_packed_logits.restype = ctypes.c_int
+    c_f = ctypes.c_float
+    lib.plm_voronoi_shortlist.argtypes = [c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p,
+                                          c_p, c_p, c_p]
+    lib.plm_voronoi_shortlist.restype = ctypes.c_int
+    lib.plm_voronoi_spread.argtypes = [c_i32, c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_i64, c_p, c_p]
+    lib.plm_voronoi_spread.restype = ctypes.c_int
+    lib.plm_voronoi_prior.argtypes = [c_p, c_p, c_i64, c_i64, c_i64, c_f, c_p, c_p]
+    lib.plm_voronoi_prior.restype = ctypes.c_int
+    lib.plm_voronoi_condense.argtypes = [c_i32, c_p, c_i64, c_i64, c_p, c_p, c_i64, c_i64, c_i64, c_p, c_p]
+    lib.plm_voronoi_condense.restype = ctypes.c_int
+    lib.plm_voronoi_fit.argtypes = [c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_i64, c_f, c_f, c_f, c_f, c_p, c_p]
+    lib.plm_voronoi_fit.restype = ctypes.c_int
+    lib.plm_voronoi_argmin.argtypes = [c_i32, c_p, c_i64, c_i64, c_p, c_p, c_i64, c_i64, c_p, c_p]
+    lib.plm_voronoi_argmin.restype = ctypes.c_int
+    lib.plm_voronoi_assign.argtypes = [c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_f, c_f,
+                                       c_f, c_f, c_f, c_f, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_sz, c_p]
+    lib.plm_voronoi_assign.restype = ctypes.c_int
+    lib.plm_voronoi_assign_workspace_bytes.argtypes = [c_i64, c_i64, c_i64, c_i64]
+    lib.plm_voronoi_assign_workspace_bytes.restype = c_sz
     lib.plm_status_string.argtypes = [c_i32]
     lib.plm_status_string.restype = ctypes.c_char_p
 

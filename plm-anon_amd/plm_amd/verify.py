@@ -207,3 +207,86 @@ class RoundVerify:
             self.accept.data_ptr(), self.argmax.data_ptr(), _ptr(accepted, "accepted", k - 1, _U8, dev),
             _ptr(num_correct, "num_correct", 1, _I64, dev), tile, ws.data_ptr(), ws.numel(), _lib.stream_handle(dev))
         _lib.check(status, f"plm_round_verify_packed(k={k}, V={V}, K={K})")
+
+
+def lm_head_verify_logits(x: torch.Tensor, w: torch.Tensor, pending: torch.Tensor, pending_rows: int, p: float,
+                          logits: torch.Tensor, logit_rows: int, rule: str = "nucleus", cfg: Config | None = None,
+                          accept: torch.Tensor | None = None,
+                          argmax: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """``lm_head_verify`` over the packed weight for a round whose verify rows decode through the
+    auxiliary scheme: rows ``r < pending_rows`` decide on ``pending[r]`` (the rest are never
+    accepted) and the logits of rows ``[0, logit_rows)`` land in ``logits`` (model dtype, rounded as
+    the decision reads them) — the reference's ``logits[:K]`` (plm/decoder.py:318-320) without the
+    other rows' logits ever being written. The decision reads model-dtype logits."""
+    if x.dim() != 2 or w.dim() != 2 or x.shape[1] != w.shape[1]:
+        raise ValueError(f"lm_head_verify_logits expects x[R,K] and w[V,K], got {tuple(x.shape)} and {tuple(w.shape)}")
+    if x.dtype not in HALF_DTYPES or w.dtype != x.dtype or logits.dtype != x.dtype:
+        raise TypeError(f"lm_head_verify_logits needs matching bf16/fp16 operands, got {x.dtype}, {w.dtype}, "
+                        f"{logits.dtype}")
+    if rule not in RULES:
+        raise ValueError(f"rule must be one of {sorted(RULES)}")
+    R, K = x.shape
+    V = w.shape[0]
+    if not 0 <= pending_rows <= R or not 0 <= logit_rows <= R:
+        raise ValueError(f"pending_rows and logit_rows must be in [0, {R}]")
+    if pending.dtype != torch.int64 or pending.numel() < pending_rows or not pending.is_contiguous():
+        raise ValueError(f"pending must be a contiguous int64 tensor of >= {pending_rows} entries")
+    if logits.dim() != 2 or logits.shape[0] < logit_rows or logits.shape[1] < V or logits.stride(1) != 1:
+        raise ValueError(f"logits must be a row-major [>= {logit_rows}, >= {V}] tensor, got {tuple(logits.shape)}")
+    if not (x.is_cuda and w.is_cuda and logits.is_cuda):
+        raise RuntimeError("lm_head_verify_logits runs on the GPU only; got a CPU tensor")
+    cfg = VERIFY_CONFIG if cfg is None else cfg
+    tile = _lib.Tile.from_config(cfg)
+    x = x if (x.stride(1) == 1 and x.stride(0) % 8 == 0) else x.contiguous()
+    accept = torch.empty(R, dtype=torch.bool, device=x.device) if accept is None else accept
+    argmax = torch.empty(R, dtype=torch.int64, device=x.device) if argmax is None else argmax
+    _ptr(accept, "accept", R, _U8, x.device)
+    _ptr(argmax, "argmax", R, _I64, x.device)
+    lib = _lib.lib()
+    ws = workspace(x.device, int(lib.plm_lm_head_verify_workspace_bytes(R, V, K, tile)))
+    mode = _lib.PLM_ROUND_BF16 if x.dtype == torch.bfloat16 else _lib.PLM_ROUND_F16
+    status = lib.plm_lm_head_verify_packed_logits(
+        _lib.DTYPE_CODES[x.dtype], x.data_ptr(), x.stride(0), packed_weight(w).data_ptr(), R, V, K,
+        pending.data_ptr() if pending_rows > 0 else 0, pending_rows, RULES[rule], float(p), mode, accept.data_ptr(),
+        argmax.data_ptr(), logits.data_ptr(), logits.stride(0), logit_rows, tile, ws.data_ptr(), ws.numel(),
+        _lib.stream_handle(x.device))
+    _lib.check(status, f"plm_lm_head_verify_packed_logits(R={R}, V={V}, K={K}, logit_rows={logit_rows})")
+    return accept, argmax
+
+
+class AuxRoundVerify:
+    """The LM-head end of a steady round whose verify rows decode through the logit-Voronoi scheme
+    (RoundDecoder._steady_round, plm/decoder.py:316-322): one verify launch pair over the round's
+    ``k + k*k`` rows that also writes the ``k`` verify rows' logits, the scheme's decode of those rows
+    (``LogitVoronoiAuxiliary.decode_unmasked``), and the epilogue (plm/decoder.py:351-365). Buffers
+    are allocated once, so a call can be captured in a HIP graph after one eager call."""
+
+    def __init__(self, k: int, scheme, vocab: int, rule: str = "nucleus", threshold: float = -1.0,
+                 dtype: torch.dtype = torch.bfloat16, device: torch.device | str = "cuda", cfg: Config | None = None):
+        if not 1 <= k <= 7:
+            raise ValueError(f"k must be in [1, 7] (a round of at most 64 rows), got {k}")
+        if rule not in RULES:
+            raise ValueError(f"rule must be one of {sorted(RULES)}")
+        self.k, self.width, self.scheme = k, k + k * k, scheme
+        self.rule, self.threshold, self.cfg = rule, float(threshold), cfg
+        ld = (vocab + 7) // 8 * 8
+        self.logits = torch.empty(k, ld, dtype=dtype, device=device)
+        self.verify_tokens = torch.zeros(k, dtype=torch.int64, device=device)
+        self.accept = torch.zeros(self.width, dtype=torch.bool, device=device)
+        self.argmax = torch.zeros(self.width, dtype=torch.int64, device=device)
+        self.vocab = vocab
+
+    def __call__(self, hidden: torch.Tensor, w: torch.Tensor, values: torch.Tensor, pending: torch.Tensor,
+                 anchor: torch.Tensor, out: torch.Tensor, base_t: torch.Tensor, offset_t: torch.Tensor,
+                 round_sequence: torch.Tensor | None = None, sequence_step: torch.Tensor | None = None,
+                 accepted: torch.Tensor | None = None, num_correct: torch.Tensor | None = None) -> torch.Tensor:
+        """``values[k]``: the verify rows' auxiliary values. Returns the decoded verify tokens."""
+        k, W = self.k, self.width
+        if hidden.dim() != 2 or hidden.shape[0] != W or w.shape[0] != self.vocab:
+            raise ValueError(f"hidden must be [{W}, K] and w [{self.vocab}, K]")
+        lm_head_verify_logits(hidden, w, pending, k - 1, self.threshold, self.logits, k, self.rule, self.cfg,
+                              accept=self.accept, argmax=self.argmax)
+        self.scheme.decode_unmasked(self.logits[:, : self.vocab], None, w, values, out=self.verify_tokens)
+        round_epilogue(k, self.accept[: max(k - 1, 0)], self.argmax[k:], self.verify_tokens, pending, anchor, out,
+                       base_t, offset_t, round_sequence, sequence_step, accepted, num_correct)
+        return self.verify_tokens
