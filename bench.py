@@ -49,11 +49,13 @@ def parse_args():
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the per-config lines (single GEMM, one block, the 32 x H2560 round)")
     ap.add_argument("--only-round", action="store_true", help="time the round only (for profiling runs)")
-    ap.add_argument("--profile", choices=("eager", "copy", "verify"),
+    ap.add_argument("--no-voronoi", action="store_true", help="skip the verify rows' auxiliary decode timing")
+    ap.add_argument("--profile", choices=("eager", "copy", "verify", "voronoi"),
                     help="no JSON: 'eager' launches the round and the fused verify step --steps times without a "
                          "graph (for rocprofv3 counter runs); 'copy' runs a 1 GiB device copy, the reference "
                          "kernel that scales the HBM byte counters; 'verify' runs the fused verify step and the "
-                         "LM-head GEMM --steps times each over six LM-head copies (for kernel traces)")
+                         "LM-head GEMM --steps times each over six LM-head copies (for kernel traces); "
+                         "'voronoi' runs the verify rows' auxiliary decode --steps times")
     return ap.parse_args()
 
 
@@ -280,6 +282,9 @@ def main():
     if args.profile == "verify":
         profile_verify(args, device)
         return
+    if args.profile == "voronoi":
+        profile_voronoi(args, device)
+        return
     tables = gemm_tables.read_table(args.hidden)
     gemms = [g for _ in range(args.layers) for g in gpt_block(args.hidden, args.mlp)]
     gemms.append(type(gemms[0])("lm_head", GPT2_VOCAB, args.hidden))
@@ -403,6 +408,8 @@ def main():
             print(f"[bench] M sweep: {sweep}", file=sys.stderr, flush=True)
         if not args.no_verify:
             result["verify"] = time_verify(weights[-1], args.hidden, device, args.steps)
+        if not args.no_voronoi:
+            result["voronoi"] = time_voronoi(args, device, weights[-1])
         if not args.no_configs:
             result["configs"] = time_configs(args, device, rnd, chained, us_round, us_graph)
         if not args.no_llama:
@@ -669,6 +676,95 @@ def time_gated_lora(args, device):
         del graph
     print(f"[bench] gated LoRA qkv: {res}", file=sys.stderr, flush=True)
     return dict(res, shape=f"M={M} N={N} K={K} rank={rank} shards={list(shards)} gate={gate}")
+
+
+# The auxiliary decode's workload: the k = 7 verify rows of a width-56 round, the GPT-2 vocabulary,
+# the reference's engine defaults, and an auxiliary vocabulary of 1024 cells. The released
+# checkpoints' size is not in the reference's sources; its fit holds a k x A tile in one 32-warp
+# program, which keeps A near 1024 on the GPU it ran on. 4096 is timed beside it.
+VORONOI = {"rows": 7, "n_items": 1024, "n_targets": 128, "k": 8, "rounds": 2, "iterations": 12}
+VORONOI_LARGE_ITEMS = 4096
+
+
+def voronoi_inputs(device, vocab, seed=7000, n_items=None):
+    import torch
+
+    n_items = n_items or VORONOI["n_items"]
+    gen = torch.Generator(device=device).manual_seed(seed)
+    table = torch.randn(vocab, n_items, generator=gen, device=device).bfloat16()
+    logits = (2.5 * torch.randn(VORONOI["rows"], vocab, generator=gen, device=device)).bfloat16()
+    values = torch.randint(0, n_items, (VORONOI["rows"],), generator=gen, device=device)
+    return table, logits, values
+
+
+def profile_voronoi(args, device):
+    """The auxiliary decode of the verify rows, eager, --steps times (for kernel traces)."""
+    import torch
+
+    from plm_amd.voronoi import Voronoi
+    from plm_amd.workloads import GPT2_VOCAB
+
+    table, logits, values = voronoi_inputs(device, GPT2_VOCAB)
+    eng = Voronoi.from_table(table)
+    out = torch.empty(VORONOI["rows"], dtype=torch.int64, device=device)
+    for _ in range(max(1, args.steps)):
+        eng.decode(logits, values, out)
+    torch.cuda.synchronize()
+    print(f"[bench] voronoi decode x {max(1, args.steps)}", file=sys.stderr)
+
+
+def time_voronoi(args, device, w_lm):
+    """The verify rows' auxiliary decode (LogitVoronoiAuxiliary.decode_unmasked: shortlist, two
+    rounds of condense + fit, the decode) for the 7 verify rows of a width-56 round, as a graph; the
+    round's whole LM-head end with it (verify + the verify rows' logits, the decode, the epilogue);
+    and the oracle's time for the same decode on the host."""
+    import torch
+
+    from plm_amd.verify import AuxRoundVerify
+    from plm_amd.voronoi import LogitVoronoiAuxiliary, Voronoi
+    from plm_amd.workloads import GPT2_VOCAB, TOP_P, proposals
+
+    n = VORONOI["rows"]
+    table, logits, values = voronoi_inputs(device, GPT2_VOCAB)
+    eng = Voronoi.from_table(table)
+    out = torch.empty(n, dtype=torch.int64, device=device)
+    graph = capture_graph(lambda: eng.decode(logits, values, out))
+    us = time_graph(graph, max(20, args.steps), 5) * 1000.0
+    del graph
+    line = {"us": round(us, 2), "us_per_verify_row": round(us / n, 2), **VORONOI, "vocab": GPT2_VOCAB}
+    big_table, big_logits, big_values = voronoi_inputs(device, GPT2_VOCAB, 7002, VORONOI_LARGE_ITEMS)
+    big = Voronoi.from_table(big_table)
+    graph = capture_graph(lambda: big.decode(big_logits, big_values, out))
+    us_big = time_graph(graph, max(20, args.steps), 5) * 1000.0
+    del graph, big, big_table
+    line[f"us_n_items_{VORONOI_LARGE_ITEMS}"] = round(us_big, 2)
+    # The steady round's LM-head end with the decode in it (k = 7, width 56): one fused verify that
+    # also writes the 7 verify rows' logits, the decode, the epilogue.
+    gen = torch.Generator().manual_seed(7001)
+    scheme = LogitVoronoiAuxiliary(VORONOI["n_items"], w_lm.shape[1], GPT2_VOCAB, dtype=torch.bfloat16).to(device)
+    scheme.auxiliary_vocabulary.copy_((0.02 * torch.randn(VORONOI["n_items"], w_lm.shape[1], generator=gen))
+                                      .to(torch.bfloat16))
+    x = torch.randn(56, w_lm.shape[1], generator=gen).to(torch.bfloat16).to(device)
+    rv = AuxRoundVerify(n, scheme, GPT2_VOCAB, "nucleus", TOP_P, device=device)
+    state = [proposals(n)[: n - 1].clone().to(device), torch.zeros(1, dtype=torch.int64, device=device),
+             torch.full((1 << 17,), -1, dtype=torch.int64, device=device),
+             torch.zeros((), dtype=torch.int64, device=device), torch.zeros((), dtype=torch.int64, device=device)]
+    graph = capture_graph(lambda: rv(x, w_lm, values, *state))
+    line["aux_round_us"] = round(time_graph(graph, max(10, args.steps // 2), 3) * 1000.0, 2)
+    del graph
+    if args.cpu_seconds > 0:
+        import numpy as np
+
+        from oracle import voronoi_oracle as vo
+
+        tab, lg = table.float().cpu().numpy(), logits.float().cpu().numpy()
+        t0 = time.perf_counter()
+        vo.decode_unmasked(tab, lg, values.cpu().numpy(), "bf16")
+        line["oracle_cpu_us"] = round((time.perf_counter() - t0) * 1e6, 1)
+        line["oracle_cpu_note"] = "numpy oracle, one decode of the same 7 rows, host cores"
+        del np
+    print(f"[bench] voronoi decode: {line}", file=sys.stderr, flush=True)
+    return line
 
 
 def time_verify(w_lm, hidden, device, steps):

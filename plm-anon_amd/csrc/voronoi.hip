@@ -43,7 +43,6 @@ constexpr int kSpreadSample = 64;  // iterate.py:275
 constexpr float kBlocked = 1e3f;   // iterate.py:25
 constexpr float kLoadFloor = 1e-2f;
 constexpr float kEmpty = -1e30f;   // iterate.py:26
-constexpr double kFixedUnit = 1.0 / 281474976710656.0;  // 2^-48
 
 // Order-preserving 16-bit key of a bf16 or fp16 value (both keep the sign in bit 15): a larger
 // value has a larger key. -0 is folded onto +0 first so equal values have equal keys.
@@ -56,84 +55,159 @@ __device__ __forceinline__ uint32_t key16_bits(uint32_t key) { return key ^ ((ke
 // A caller's token id as a table row, clamped into [0, V) so no input reads outside the table.
 __device__ __forceinline__ int64_t table_row(int64_t token, int V) { return token < 0 ? 0 : (token >= V ? V - 1 : token); }
 
-// -------------------------------------------------------------------------- block reductions
-// 1024 threads. Every thread gets the result; each call ends with one barrier and alternates
-// between two scratch rows, so consecutive calls need no barrier between them.
+// -------------------------------------------------------------------------- reductions
+// Wavefront reductions run on the VALU: DPP lane permutations inside each row of 16 lanes, then the
+// four rows' results read out and combined in row order. A butterfly step adds a + b on one lane
+// and b + a on its partner, equal bit for bit, so every lane ends with the same value and the
+// summation order is fixed.
 
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7 - i within each half row
+constexpr int kDppMirror = 0x140;     // lane i <-> 15 - i within each row
+constexpr int kDppShr1 = 0x111, kDppShr2 = 0x112, kDppShr4 = 0x114, kDppShr8 = 0x118;
+constexpr int kDppBcast15 = 0x142, kDppBcast31 = 0x143;
+
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ int dpp(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROWS, 0xF, true);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, dpp<CTRL>(__builtin_bit_cast(int, v)));
+}
+__device__ __forceinline__ int lane_value(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Every lane of a fully active wavefront gets the sum / maximum of all 64 lanes.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  v += dpp<kDppMirror>(v);
+  return ((lane_value(v, 0) + lane_value(v, 16)) + lane_value(v, 32)) + lane_value(v, 48);
+}
+__device__ __forceinline__ int wave_sum(int v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  v += dpp<kDppMirror>(v);
+  return lane_value(v, 0) + lane_value(v, 16) + lane_value(v, 32) + lane_value(v, 48);
+}
+__device__ __forceinline__ uint32_t wave_max(uint32_t u) {
+  int v = static_cast<int>(u);
+  v = static_cast<int>(max(static_cast<uint32_t>(v), static_cast<uint32_t>(dpp<kDppXor1>(v))));
+  v = static_cast<int>(max(static_cast<uint32_t>(v), static_cast<uint32_t>(dpp<kDppXor2>(v))));
+  v = static_cast<int>(max(static_cast<uint32_t>(v), static_cast<uint32_t>(dpp<kDppHalfMirror>(v))));
+  v = static_cast<int>(max(static_cast<uint32_t>(v), static_cast<uint32_t>(dpp<kDppMirror>(v))));
+  return max(max(static_cast<uint32_t>(lane_value(v, 0)), static_cast<uint32_t>(lane_value(v, 16))),
+             max(static_cast<uint32_t>(lane_value(v, 32)), static_cast<uint32_t>(lane_value(v, 48))));
+}
+__device__ __forceinline__ uint32_t wave_min(uint32_t u) {
+  int v = static_cast<int>(u);
+  v = static_cast<int>(min(static_cast<uint32_t>(v), static_cast<uint32_t>(dpp<kDppXor1>(v))));
+  v = static_cast<int>(min(static_cast<uint32_t>(v), static_cast<uint32_t>(dpp<kDppXor2>(v))));
+  v = static_cast<int>(min(static_cast<uint32_t>(v), static_cast<uint32_t>(dpp<kDppHalfMirror>(v))));
+  v = static_cast<int>(min(static_cast<uint32_t>(v), static_cast<uint32_t>(dpp<kDppMirror>(v))));
+  return min(min(static_cast<uint32_t>(lane_value(v, 0)), static_cast<uint32_t>(lane_value(v, 16))),
+             min(static_cast<uint32_t>(lane_value(v, 32)), static_cast<uint32_t>(lane_value(v, 48))));
+}
+
+// Inclusive prefix sum over the 64 lanes (row-wise shifts, then the row carries broadcast).
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  v += dpp<kDppShr1>(v);
+  v += dpp<kDppShr2>(v);
+  v += dpp<kDppShr4>(v);
+  v += dpp<kDppShr8>(v);
+  v += dpp<kDppBcast15, 0xA>(v);
+  v += dpp<kDppBcast31, 0xC>(v);
+  return v;
+}
+
+// Block-wide versions for 1024 threads: every thread gets the result. Each wavefront reduces its
+// lanes, lane 0 posts the wavefront's value, and after one barrier every wavefront reads the 16
+// posts (one per lane) and reduces them the same way. Calls alternate between two scratch rows,
+// so consecutive calls need no barrier between them.
 struct BlockScratch {
-  int i[2][kRowWaves];
+  int i[2][3][kRowWaves];
   float f[2][kRowWaves];
   uint32_t u[2][kRowWaves];
 };
 
+__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x & 63); }
+
 __device__ __forceinline__ int block_count(bool pred, BlockScratch& s, int& parity) {
   const int n = __popcll(__ballot(pred));
-  if ((threadIdx.x & 63) == 0) s.i[parity][threadIdx.x >> 6] = n;
+  if (lane_id() == 0) s.i[parity][0][threadIdx.x >> 6] = n;
   __syncthreads();
-  int total = 0;
-#pragma unroll
-  for (int w = 0; w < kRowWaves; ++w) total += s.i[parity][w];
+  const int total = wave_sum(lane_id() < kRowWaves ? s.i[parity][0][lane_id()] : 0);
   parity ^= 1;
   return total;
+}
+
+// Three counts in one barrier.
+__device__ __forceinline__ void block_count3(bool p0, bool p1, bool p2, int (&n)[3], BlockScratch& s, int& parity) {
+  const int c0 = __popcll(__ballot(p0)), c1 = __popcll(__ballot(p1)), c2 = __popcll(__ballot(p2));
+  if (lane_id() == 0) {
+    s.i[parity][0][threadIdx.x >> 6] = c0;
+    s.i[parity][1][threadIdx.x >> 6] = c1;
+    s.i[parity][2][threadIdx.x >> 6] = c2;
+  }
+  __syncthreads();
+  const bool in = lane_id() < kRowWaves;
+  n[0] = wave_sum(in ? s.i[parity][0][lane_id()] : 0);
+  n[1] = wave_sum(in ? s.i[parity][1][lane_id()] : 0);
+  n[2] = wave_sum(in ? s.i[parity][2][lane_id()] : 0);
+  parity ^= 1;
 }
 
 __device__ __forceinline__ int block_sum_int(int v, BlockScratch& s, int& parity) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  if ((threadIdx.x & 63) == 0) s.i[parity][threadIdx.x >> 6] = v;
+  v = wave_sum(v);
+  if (lane_id() == 0) s.i[parity][0][threadIdx.x >> 6] = v;
   __syncthreads();
-  int total = 0;
-#pragma unroll
-  for (int w = 0; w < kRowWaves; ++w) total += s.i[parity][w];
+  const int total = wave_sum(lane_id() < kRowWaves ? s.i[parity][0][lane_id()] : 0);
   parity ^= 1;
   return total;
 }
 
-// Butterfly within the wavefront (a + b == b + a bit for bit, so every lane ends equal), then the
-// wavefront sums in wavefront order: a fixed summation order.
 __device__ __forceinline__ float block_sum_float(float v, BlockScratch& s, int& parity) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  if ((threadIdx.x & 63) == 0) s.f[parity][threadIdx.x >> 6] = v;
+  v = wave_sum(v);
+  if (lane_id() == 0) s.f[parity][threadIdx.x >> 6] = v;
   __syncthreads();
-  float total = 0.f;
-#pragma unroll
-  for (int w = 0; w < kRowWaves; ++w) total += s.f[parity][w];
+  const float total = wave_sum(lane_id() < kRowWaves ? s.f[parity][lane_id()] : 0.f);
   parity ^= 1;
   return total;
 }
 
 __device__ __forceinline__ uint32_t block_max_u32(uint32_t v, BlockScratch& s, int& parity) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), off, 64)));
-  if ((threadIdx.x & 63) == 0) s.u[parity][threadIdx.x >> 6] = v;
+  v = wave_max(v);
+  if (lane_id() == 0) s.u[parity][threadIdx.x >> 6] = v;
   __syncthreads();
-  uint32_t total = 0;
-#pragma unroll
-  for (int w = 0; w < kRowWaves; ++w) total = max(total, s.u[parity][w]);
+  const uint32_t total = wave_max(lane_id() < kRowWaves ? s.u[parity][lane_id()] : 0u);
+  parity ^= 1;
+  return total;
+}
+
+__device__ __forceinline__ uint32_t block_min_u32(uint32_t v, BlockScratch& s, int& parity) {
+  v = wave_min(v);
+  if (lane_id() == 0) s.u[parity][threadIdx.x >> 6] = v;
+  __syncthreads();
+  const uint32_t total = wave_min(lane_id() < kRowWaves ? s.u[parity][lane_id()] : 0xFFFFFFFFu);
   parity ^= 1;
   return total;
 }
 
 // Exclusive prefix sum over the workgroup in thread order; `total` gets the sum.
 __device__ __forceinline__ int block_exclusive_scan(int v, int& total, BlockScratch& s, int& parity) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int inc = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(inc, off, 64);
-    if (lane >= off) inc += y;
-  }
-  if (lane == 63) s.i[parity][wave] = inc;
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  const int inc = wave_inclusive_scan(v);
+  if (lane == 63) s.i[parity][0][wave] = inc;
   __syncthreads();
-  int base = 0;
-  total = 0;
-#pragma unroll
-  for (int w = 0; w < kRowWaves; ++w) {
-    const int c = s.i[parity][w];
-    base += w < wave ? c : 0;
-    total += c;
-  }
+  const int c = lane < kRowWaves ? s.i[parity][0][lane] : 0;
+  const int base = wave_sum(lane < wave ? c : 0);
+  total = wave_sum(c);
   parity ^= 1;
   return base + inc - v;
 }
@@ -173,9 +247,17 @@ __device__ float spread_unit(const uint16_t* table, int A, const int* tok_s, int
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int cols = min(min(sample, kSpreadSample), A);
   float lo = INFINITY, hi = -INFINITY;
-  if (lane < cols) {
-    for (int m = wave; m < M; m += kRowWaves) {
-      const float v = from_bits16<DT>(table[static_cast<int64_t>(tok_s[m]) * A + lane]);
+  // Every read of this lane in flight at once (rows of a large table: each one an HBM round trip).
+  uint16_t raw[kMaxTargets / kRowWaves];
+#pragma unroll
+  for (int i = 0; i < kMaxTargets / kRowWaves; ++i) {
+    const int m = wave + kRowWaves * i;
+    raw[i] = (lane < cols && m < M) ? table[static_cast<int64_t>(tok_s[m]) * A + lane] : 0;
+  }
+#pragma unroll
+  for (int i = 0; i < kMaxTargets / kRowWaves; ++i) {
+    if (lane < cols && wave + kRowWaves * i < M) {
+      const float v = from_bits16<DT>(raw[i]);
       lo = fminf(lo, v);
       hi = fmaxf(hi, v);
     }
@@ -220,13 +302,19 @@ struct ShortArgs {
   float* normaliser; // [N] or null
 };
 
+// Candidate sets up to this size are ranked by counting (each candidate counts the larger ones);
+// larger ones go through a bitonic sort.
+constexpr int kRankCap = 256;
+
 // JT = elements per thread (a multiple of 8 covering V / 1024).
 template <int DT, int JT>
 __global__ __launch_bounds__(kRowThreads) void voronoi_shortlist_kernel(ShortArgs a) {
-  __shared__ uint32_t cand[kCandidateCap];
+  __shared__ __align__(16) uint32_t cand[kCandidateCap];
+  __shared__ uint32_t top[kMaxTargets];
   __shared__ BlockScratch red;
   __shared__ float lo_s[kRowWaves][kSpreadSample], hi_s[kRowWaves][kSpreadSample];
-  __shared__ float rem_s[kMaxTargets];
+  __shared__ __align__(16) float rem_s[kMaxTargets];
+  __shared__ int rank_s[kMaxTargets];
   __shared__ int tok_s[kMaxTargets];
   int parity = 0;
   const int t = threadIdx.x;
@@ -234,42 +322,73 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_shortlist_kernel(ShortArg
   const int M = a.M;
   const uint16_t* row = a.logits + p * a.ld;
 
-  // The row as order keys, two per register; key 0 marks a position past the vocabulary.
-  // Element j of this thread is token t + 1024 j.
+  // The row as order keys, two per register; key 0 marks a position past the vocabulary. Element
+  // j of this thread is token 8 (t + 1024 (j / 8)) + j % 8: eight consecutive tokens per 16-byte
+  // load when the row is 16-byte aligned.
   uint32_t kk[JT / 2];
   uint32_t kmax = 0;
+  const bool vec = (reinterpret_cast<uintptr_t>(row) & 15u) == 0;
+  auto token_of = [&](int j) -> int { return 8 * (t + kRowThreads * (j >> 3)) + (j & 7); };
 #pragma unroll
-  for (int j = 0; j < JT; ++j) {
-    const int i = t + kRowThreads * j;
-    const uint32_t k = i < a.V ? order_key16(row[i]) : 0u;
-    if (j & 1)
-      kk[j >> 1] |= k << 16;
-    else
-      kk[j >> 1] = k;
-    kmax = max(kmax, k);
+  for (int c = 0; c < JT / 8; ++c) {
+    const int i0 = 8 * (t + kRowThreads * c);
+    uint32_t h[8];
+    if (vec && i0 + 8 <= a.V) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(row + i0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        h[2 * e] = w[e] & 0xFFFFu;
+        h[2 * e + 1] = w[e] >> 16;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) h[e] = i0 + e < a.V ? row[i0 + e] : 0x8000u;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t k = i0 + e < a.V ? order_key16(h[e]) : 0u;
+      const int j = 8 * c + e;
+      if (j & 1)
+        kk[j >> 1] |= k << 16;
+      else
+        kk[j >> 1] = k;
+      kmax = max(kmax, k);
+    }
   }
   auto key_of = [&](int j) -> uint32_t { return (kk[j >> 1] >> (16 * (j & 1))) & 0xFFFFu; };
 
-  // Normaliser max + log(sum exp(l - max)) (iterate.py:56-80), values clamped to the reference's
-  // finite stand-in for -inf.
-  const uint32_t bmax = block_max_u32(kmax, red, parity);
-  const float mx = fmaxf(from_bits16<DT>(static_cast<uint16_t>(key16_bits(bmax))), kEmpty);
-  float se = 0.f;
+  // The normaliser max + log(sum exp(l - max)) (iterate.py:56-80, values clamped to the reference's
+  // finite stand-in for -inf), only when the caller asks for it: the quotas below use the shortlist's
+  // softmax directly, which the normaliser cancels out of (iterate.py:272-273).
+  if (a.normaliser != nullptr) {
+    const uint32_t bmax = block_max_u32(kmax, red, parity);
+    const float mx = fmaxf(from_bits16<DT>(static_cast<uint16_t>(key16_bits(bmax))), kEmpty);
+    float se = 0.f;
 #pragma unroll
-  for (int j = 0; j < JT; ++j) {
-    const uint32_t k = key_of(j);
-    if (k != 0) se += __expf(fmaxf(from_bits16<DT>(static_cast<uint16_t>(key16_bits(k))), kEmpty) - mx);
+    for (int j = 0; j < JT; ++j) {
+      const uint32_t k = key_of(j);
+      if (k != 0) se += __expf(fmaxf(from_bits16<DT>(static_cast<uint16_t>(key16_bits(k))), kEmpty) - mx);
+    }
+    se = block_sum_float(se, red, parity);
+    if (t == 0) a.normaliser[p] = mx + logf(se);
   }
-  se = block_sum_float(se, red, parity);
-  const float norm = mx + logf(se);
 
-  // Threshold: the M-th largest per-thread maximum. At least M elements reach it, so the M
-  // largest elements all do.
-  uint32_t tau = 0;
-  for (int bit = 15; bit >= 0; --bit) {
-    const uint32_t c = tau | (1u << bit);
-    if (block_count(kmax >= c, red, parity) >= M) tau = c;
+  // Threshold: the M-th largest per-thread maximum. At least M elements reach it, so the M largest
+  // elements all do. The thread maxima share the key bits above the highest bit where the smallest
+  // and largest differ; the rest is found two bits per barrier.
+  const uint32_t klo = block_min_u32(kmax, red, parity);
+  const uint32_t khi = block_max_u32(kmax, red, parity);
+  int bits = klo == khi ? 0 : 32 - __clz(klo ^ khi);
+  uint32_t tau = klo & ~((1u << bits) - 1u);
+  while (bits >= 2) {
+    bits -= 2;
+    int n[3];
+    block_count3(kmax >= (tau | (1u << bits)), kmax >= (tau | (2u << bits)), kmax >= (tau | (3u << bits)), n, red,
+                 parity);
+    tau |= (n[2] >= M ? 3u : n[1] >= M ? 2u : n[0] >= M ? 1u : 0u) << bits;
   }
+  if (bits == 1 && block_count(kmax >= (tau | 1u), red, parity) >= M) tau |= 1u;
+
   int mine = 0;
 #pragma unroll
   for (int j = 0; j < JT; ++j) {
@@ -305,22 +424,48 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_shortlist_kernel(ShortArg
 #pragma unroll
     for (int j = 0; j < JT; ++j) {
       const uint32_t k = key_of(j);
-      if (k != 0 && k >= tau) cand[off++] = (k << 16) | (0xFFFFu - static_cast<uint32_t>(t + kRowThreads * j));
+      if (k != 0 && k >= tau) cand[off++] = (k << 16) | (0xFFFFu - static_cast<uint32_t>(token_of(j)));
     }
   }
-  int n_sort = M;
-  while (n_sort < total) n_sort <<= 1;
-  for (int i = total + t; i < n_sort; i += kRowThreads) cand[i] = 0u;
+  if (total <= kRankCap) {
+    // Rank by counting: sort keys are unique, so a candidate's rank is the number of larger ones.
+    const int padded = (total + 3) & ~3;
+    if (t >= total && t < padded) cand[t] = 0u;
+    __syncthreads();
+    // Thread 4 i + g counts, for candidate i, the larger keys among every fourth group of four.
+    {
+      const int i = t >> 2, g = t & 3;
+      const uint32_t key = i < total ? cand[i] : 0xFFFFFFFFu;
+      int rank = 0;
+      for (int j = 4 * g; j < padded; j += 16) {
+        const u32x4 c4 = *reinterpret_cast<const u32x4*>(&cand[j]);
+        rank += (c4[0] > key) + (c4[1] > key) + (c4[2] > key) + (c4[3] > key);
+      }
+      rank += dpp<kDppXor1>(rank);
+      rank += dpp<kDppXor2>(rank);
+      if (g == 0 && i < total && rank < M) top[rank] = key;
+    }
+    // fewer than M candidates only for a degenerate row (NaN keys): those slots read as key 0
+    if (t < M && t >= total) top[t] = 0u;
+  } else {
+    int n_sort = M;
+    while (n_sort < total) n_sort <<= 1;
+    for (int i = total + t; i < n_sort; i += kRowThreads) cand[i] = 0u;
+    __syncthreads();
+    bitonic_descending(cand, n_sort);
+    if (t < M) top[t] = cand[t];
+  }
   __syncthreads();
-  bitonic_descending(cand, n_sort);
 
-  // Quotas (iterate.py:214-223, 272-273): threads < M hold target t.
+  // Quotas (iterate.py:214-223, 272-273): threads < M hold target t. The shortlist's softmax is
+  // formed against its largest logit.
+  const float v0 = from_bits16<DT>(static_cast<uint16_t>(key16_bits(top[0] >> 16)));
   float val = 0.f, pr = 0.f;
   if (t < M) {
-    const uint32_t sk = cand[t];
+    const uint32_t sk = top[t];
     tok_s[t] = min(static_cast<int>(0xFFFFu - (sk & 0xFFFFu)), a.V - 1);  // in range even for a degenerate row
     val = from_bits16<DT>(static_cast<uint16_t>(key16_bits(sk >> 16)));
-    pr = expf(val - norm);
+    pr = expf(val - v0);
   }
   const float psum = block_sum_float(pr, red, parity);
   float rem = 0.f;
@@ -332,15 +477,29 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_shortlist_kernel(ShortArg
     rem = exact - fl;
     rem_s[t] = rem;
   }
-  const int remaining = a.A - block_sum_int(cnt, red, parity);  // barrier also publishes rem_s / tok_s
-  if (t < M) {
-    int rank = 0;
-    for (int j = 0; j < M; ++j) {
-      const float r = rem_s[j];
-      rank += (r > rem || (r == rem && j < t)) ? 1 : 0;
+  const int remaining = a.A - block_sum_int(cnt, red, parity);  // its barrier also publishes rem_s / tok_s
+  // Remainder ranks: thread 8 m + g compares target m's remainder with targets [16 g, 16 g + 16);
+  // the eight partial counts of m sit in one lane octet and add up there.
+  {
+    const int m = t >> 3, g = t & 7;
+    int part = 0;
+    if (m < M) {
+      const float mine_rem = rem_s[m];
+#pragma unroll
+      for (int j = 16 * g; j < 16 * g + 16; j += 4) {
+        const f32x4 r4 = *reinterpret_cast<const f32x4*>(&rem_s[j]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          part += (j + u < M && (r4[u] > mine_rem || (r4[u] == mine_rem && j + u < m))) ? 1 : 0;
+      }
     }
-    cnt += rank < remaining ? 1 : 0;
+    part += dpp<kDppXor1>(part);
+    part += dpp<kDppXor2>(part);
+    part += dpp<kDppHalfMirror>(part);
+    if (g == 0 && m < M) rank_s[m] = part;
   }
+  __syncthreads();
+  if (t < M) cnt += rank_s[t] < remaining ? 1 : 0;
 
   const float unit = spread_unit<DT>(a.table, a.A, tok_s, M, kSpreadSample, lo_s, hi_s, red, parity);
   if (t < M) {
@@ -350,10 +509,7 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_shortlist_kernel(ShortArg
     a.counts[o] = cnt;
     if (a.values != nullptr) a.values[o] = val;
   }
-  if (t == 0) {
-    a.unit[p] = unit;
-    if (a.normaliser != nullptr) a.normaliser[p] = norm;
-  }
+  if (t == 0) a.unit[p] = unit;
 }
 
 // Standalone spread and prior, for callers that run the engine's steps one by one.
@@ -399,39 +555,55 @@ __device__ __forceinline__ int32_t pack_cost(float c, int target) {
   return (ordered & ~0x7F) | target;
 }
 
+// A workgroup takes 64 items; its four wavefronts each rank a quarter of the targets for them (all
+// of a lane's table reads in flight at once), and the four sorted lists merge in LDS.
+constexpr int kCondenseItems = 64;
+constexpr int kCondenseWaves = kItemThreads / 64;
+constexpr int kTargetsPerWave = kMaxTargets / kCondenseWaves;
+
+template <int K>
+__device__ __forceinline__ void insert_key(int32_t (&best)[K], int32_t x) {
+#pragma unroll
+  for (int s = 0; s < K; ++s) {
+    const int32_t lo = min(best[s], x);
+    x = max(best[s], x);
+    best[s] = lo;
+  }
+}
+
 template <int DT, int K>
 __global__ __launch_bounds__(kItemThreads) void voronoi_condense_kernel(CondenseArgs a) {
   __shared__ int64_t row_s[kMaxTargets];
   __shared__ float off_s[kMaxTargets];
-  const int t = threadIdx.x;
+  __shared__ int32_t part[kCondenseWaves][K][kCondenseItems];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int64_t p = blockIdx.y;
   if (t < a.M) {
     row_s[t] = table_row(a.tokens[p * a.M + t], a.V) * a.A;
     off_s[t] = a.offset[p * a.M + t];
   }
   __syncthreads();
-  const int item = blockIdx.x * kItemThreads + t;
-  if (item >= a.A) return;
+  const int item = blockIdx.x * kCondenseItems + lane;
+  const bool live = item < a.A;
+  const int per = (a.M + kCondenseWaves - 1) / kCondenseWaves;
+  const int m0 = wave * per, m1 = min(a.M, m0 + per);
   int32_t best[K];
 #pragma unroll
   for (int s = 0; s < K; ++s) best[s] = INT_MAX;
-  constexpr int kBatch = 8;
-  for (int m0 = 0; m0 < a.M; m0 += kBatch) {
-    uint16_t raw[kBatch];
+  uint16_t raw[kTargetsPerWave];
 #pragma unroll
-    for (int b = 0; b < kBatch; ++b) raw[b] = m0 + b < a.M ? a.table[row_s[m0 + b] + item] : 0;
+  for (int b = 0; b < kTargetsPerWave; ++b) raw[b] = (live && m0 + b < m1) ? a.table[row_s[m0 + b] + item] : 0;
 #pragma unroll
-    for (int b = 0; b < kBatch; ++b) {
-      if (m0 + b >= a.M) break;
-      int32_t x = pack_cost(from_bits16<DT>(raw[b]) + off_s[m0 + b], m0 + b);
+  for (int b = 0; b < kTargetsPerWave; ++b)
+    if (m0 + b < m1) insert_key<K>(best, pack_cost(from_bits16<DT>(raw[b]) + off_s[m0 + b], m0 + b));
 #pragma unroll
-      for (int s = 0; s < K; ++s) {
-        const int32_t lo = min(best[s], x);
-        x = max(best[s], x);
-        best[s] = lo;
-      }
-    }
-  }
+  for (int s = 0; s < K; ++s) part[wave][s][lane] = best[s];
+  __syncthreads();
+  if (wave != 0 || !live) return;
+#pragma unroll
+  for (int w = 1; w < kCondenseWaves; ++w)
+#pragma unroll
+    for (int s = 0; s < K; ++s) insert_key<K>(best, part[w][s][lane]);
 #pragma unroll
   for (int s = 0; s < K; ++s) a.key[(p * K + s) * a.A + item] = best[s];
 }
@@ -453,47 +625,73 @@ struct FitArgs {
   int64_t* decoded;       // [N]
 };
 
-// w in [0, 1 + 2^-23] -> units of 2^-48, exactly for w >= 2^-24 (every bit of its float32).
-__device__ __forceinline__ unsigned long long to_fixed48(float w) {
-  const float s = w * 65536.f;
-  const float hi = floorf(s);
-  const uint32_t lo = static_cast<uint32_t>((s - hi) * 4294967296.f);
-  return (static_cast<unsigned long long>(static_cast<uint32_t>(hi)) << 32) | lo;
+// The condensed problem of one problem holds k * A <= 32768 entries (item, slot). The fit keeps
+// their sweep weights in LDS ordered by target, so a target's load is the sum of its segment; the
+// segments are cut at every multiple of the piece length L into pieces, one thread per piece, so
+// the sums are balanced however unequal the targets' shares are. L is the smallest of 16, 32, 64
+// that keeps the pieces (at most entries / L + 128) within the workgroup.
+constexpr int kMaxEntries = 32768;
+constexpr int kMaxPieces = kRowThreads;
+__device__ __forceinline__ int piece_shift(int entries) {
+  return entries + kMaxTargets * 16 <= kRowThreads * 16 ? 4 : (entries + kMaxTargets * 32 <= kRowThreads * 32 ? 5 : 6);
 }
+// LDS slot of position i: one word of skew every L positions, so the lanes summing consecutive
+// pieces (L apart) read different banks, and a piece (inside one L-block) is contiguous.
+__device__ __forceinline__ int skewed(int i, int shift) { return i + (i >> shift); }
+constexpr int kWsumSlots = kMaxEntries + kMaxEntries / 64 + 8;  // + reads past the last piece
 
-// One target's sweep state: its factor correction and its load accumulator, 16 bytes so that one
-// register (the target's byte offset) addresses both with immediate offsets.
-struct alignas(16) TargetCell {
-  float corr;
-  float unused;
-  unsigned long long load;
-};
+// Entry layout in registers: base cost (float) and, packed, during the setup the entry's target
+// (bits 0..7) and its rank (bits 8..); for the sweeps the byte offset of its target's correction
+// (target * 4, bits 0..8) and of its weight's LDS slot (bits 9..).
+__device__ __forceinline__ int entry_target(uint32_t packed) { return static_cast<int>(packed & 0xFFu); }
+__device__ __forceinline__ int entry_pos(uint32_t packed) { return static_cast<int>(packed >> 8); }
+__device__ __forceinline__ uint32_t corr_offset(uint32_t packed) { return packed & 0x1FFu; }
+__device__ __forceinline__ uint32_t slot_offset(uint32_t packed) { return packed >> 9; }
+
+// Exclusive prefix sum of v over threads 0..127 (the targets), run by the first two wavefronts;
+// thread 127's inclusive value is the total. Every thread calls it (it holds one barrier).
+__device__ __forceinline__ int target_exclusive_scan(int v, int* carry) {
+  const int t = threadIdx.x, lane = t & 63;
+  int inc = 0;
+  if (t < kMaxTargets) {
+    inc = wave_inclusive_scan(v);
+    if (t == 63) *carry = inc;
+  }
+  __syncthreads();
+  return (t >= 64 && t < kMaxTargets ? *carry : 0) + inc - v + 0 * lane;
+}
 
 template <int DT, int K, int IPT>
 __global__ __launch_bounds__(kRowThreads) void voronoi_fit_kernel(FitArgs a) {
-  __shared__ TargetCell cell[kMaxTargets];
+  // wsum: the sweep's weights in target order (target m's segment is [seg[m], seg[m+1])). Before
+  // the sweeps the same storage holds the setup's per-wavefront target masks and counts.
+  __shared__ float wsum[kWsumSlots];
+  __shared__ float psum[kMaxPieces];
+  __shared__ float corr[kMaxTargets];
   __shared__ float share_s[kMaxTargets];
   __shared__ int live_s[kMaxTargets];
+  __shared__ int seg[kMaxTargets + 1];
+  __shared__ int pstart[kMaxTargets + 1];
+  __shared__ int carry[2];
   __shared__ float best_v[kMaxTargets / 64];
   __shared__ int best_i[kMaxTargets / 64];
-  const int t = threadIdx.x, lane = t & 63;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int64_t p = blockIdx.x;
   const int M = a.M, A = a.A;
-  if (t < M) {
-    const int64_t c = a.counts[p * M + t];
+  if (t < kMaxTargets) {
+    const int64_t c = t < M ? a.counts[p * M + t] : 0;
     live_s[t] = c > 0;
     share_s[t] = logf(fmaxf(static_cast<float>(c), 1e-9f));
-    cell[t].corr = 0.f;
+    corr[t] = 0.f;
   }
   const float u = a.unit[p];
   float temperature = a.epsilon * u;
   const float bound = a.limit * u;
 
-  // The condensed problem, decoded once (iterate.py:130-134): item t + 1024 q, slot (j + lane) % K
-  // in register j — the rotation spreads each wavefront's cheapest-slot targets over the K
-  // atomic instructions. A target is kept as its cell's byte offset.
+  // The condensed problem, decoded once (iterate.py:130-134): thread t holds items t + 1024 q and
+  // their K slots.
   float base[IPT][K];
-  uint32_t at[IPT][K];
+  uint32_t ent[IPT][K];
   bool valid[IPT];
 #pragma unroll
   for (int q = 0; q < IPT; ++q) {
@@ -501,20 +699,114 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_fit_kernel(FitArgs a) {
     valid[q] = item < A;
 #pragma unroll
     for (int j = 0; j < K; ++j) {
-      const int s = (j + lane) & (K - 1);
-      const int32_t key = valid[q] ? a.key[(p * K + s) * A + item] : 0;
+      const int32_t key = valid[q] ? a.key[(p * K + j) * A + item] : 0;
       const int32_t carried = key & ~0x7F;
       base[q][j] = __builtin_bit_cast(float, carried >= 0 ? carried : (carried ^ 0x7FFFFFFF));
-      at[q][j] = static_cast<uint32_t>(key & 0x7F) * static_cast<uint32_t>(sizeof(TargetCell));
+      ent[q][j] = static_cast<uint32_t>(key & 0x7F);
     }
   }
-  char* cells = reinterpret_cast<char*>(cell);
-  __syncthreads();
+
+  const int shift = piece_shift(K * A);
+  // Target order, item order within a target: deterministic, so the float sums below are too. An
+  // item lists a target at most once, so an entry's rank in its target's segment is the number of
+  // earlier items listing the target: a 64-bit lane mask per (q, wavefront, target) gives the rank
+  // among the wavefront's items, a prefix over (q, wavefront) the rest.
+  constexpr int J = IPT * kRowWaves;  // (q, wavefront) slots, in item order
+  unsigned long long* mask = reinterpret_cast<unsigned long long*>(wsum);      // [16][128]
+  int* wcount = reinterpret_cast<int*>(wsum + 2 * kRowWaves * kMaxTargets);     // [J][128]
+  int* gsum = wcount + J * kMaxTargets;                                         // [8][128]
+#pragma unroll
+  for (int q = 0; q < IPT; ++q) {
+    mask[wave * kMaxTargets + lane] = 0ull;
+    mask[wave * kMaxTargets + 64 + lane] = 0ull;
+    __syncthreads();
+    if (valid[q]) {
+#pragma unroll
+      for (int j = 0; j < K; ++j)
+        __hip_atomic_fetch_or(&mask[wave * kMaxTargets + entry_target(ent[q][j])], 1ull << lane, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    __syncthreads();
+    const unsigned long long below = (1ull << lane) - 1ull;
+    if (valid[q]) {
+#pragma unroll
+      for (int j = 0; j < K; ++j) {
+        const int m = entry_target(ent[q][j]);
+        ent[q][j] |= static_cast<uint32_t>(__popcll(mask[wave * kMaxTargets + m] & below)) << 8;
+      }
+    }
+    wcount[(q * kRowWaves + wave) * kMaxTargets + lane] = __popcll(mask[wave * kMaxTargets + lane]);
+    wcount[(q * kRowWaves + wave) * kMaxTargets + 64 + lane] = __popcll(mask[wave * kMaxTargets + 64 + lane]);
+    __syncthreads();
+  }
+  // Per target, exclusive prefix over the J slots: thread (g, m) (8 groups x 128 targets) scans J / 8
+  // consecutive slots, then adds the groups before it.
+  {
+    constexpr int SPAN = J / 8;
+    const int m = t & (kMaxTargets - 1), g = t >> 7;
+    int run = 0;
+#pragma unroll
+    for (int i = 0; i < SPAN; ++i) {
+      int* c = &wcount[(g * SPAN + i) * kMaxTargets + m];
+      const int n = *c;
+      *c = run;
+      run += n;
+    }
+    gsum[g * kMaxTargets + m] = run;
+    __syncthreads();
+    int before = 0, len = 0;
+#pragma unroll
+    for (int h = 0; h < 8; ++h) {
+      const int n = gsum[h * kMaxTargets + m];
+      before += h < g ? n : 0;
+      len += n;
+    }
+#pragma unroll
+    for (int i = 0; i < SPAN; ++i) wcount[(g * SPAN + i) * kMaxTargets + m] += before;
+    // Segment starts and piece starts: exclusive scans over the targets of their lengths.
+    const int start = target_exclusive_scan(len, &carry[0]);
+    // Pieces of this target: the L-blocks its segment [start, start + len) overlaps.
+    const int pieces = len > 0 ? ((start + len - 1) >> shift) - (start >> shift) + 1 : 0;
+    const int pfirst = target_exclusive_scan(pieces, &carry[1]);
+    if (t < kMaxTargets) {
+      seg[t] = start;
+      pstart[t] = pfirst;
+      if (t == kMaxTargets - 1) {
+        seg[kMaxTargets] = start + len;
+        pstart[kMaxTargets] = pfirst + pieces;
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int q = 0; q < IPT; ++q) {
+    if (!valid[q]) continue;
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      const int m = entry_target(ent[q][j]);
+      const int pos = seg[m] + wcount[(q * kRowWaves + wave) * kMaxTargets + m] + entry_pos(ent[q][j]);
+      ent[q][j] = (static_cast<uint32_t>(4 * skewed(pos, shift)) << 9) | static_cast<uint32_t>(4 * m);
+    }
+  }
+  // This thread's piece: [piece_lo, piece_hi) of wsum (empty past the last piece).
+  int piece_lo = 0, piece_hi = 0;
+  if (t < pstart[kMaxTargets]) {
+    int m = 0;
+#pragma unroll
+    for (int stride = kMaxTargets / 2; stride >= 1; stride >>= 1)
+      if (pstart[m + stride] <= t) m += stride;
+    const int block = (seg[m] >> shift) + (t - pstart[m]);
+    piece_lo = max(seg[m], block << shift);
+    piece_hi = min(seg[m + 1], (block + 1) << shift);
+  }
+  __syncthreads();  // the setup's storage becomes wsum
 
   for (int it = 0; it < a.iterations; ++it) {
-    if (t < M) cell[t].load = 0ull;
-    __syncthreads();
-    const float inv_t = 1.f / temperature;
+    // Each item's softmax over its K slots (iterate.py:142-145), into target order.
+    // exp(-cost / T - max) as exp2 of cost * (-log2(e) / T) less its maximum.
+    const float scale = -1.4426950408889634f / temperature;
+    const char* corr_b = reinterpret_cast<const char*>(corr);
+    char* wsum_b = reinterpret_cast<char*>(wsum);
 #pragma unroll
     for (int q = 0; q < IPT; ++q) {
       if (!valid[q]) continue;
@@ -522,28 +814,55 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_fit_kernel(FitArgs a) {
       float xm = -INFINITY;
 #pragma unroll
       for (int j = 0; j < K; ++j) {
-        x[j] = -(base[q][j] + *reinterpret_cast<const float*>(cells + at[q][j])) * inv_t;
+        x[j] = (base[q][j] + *reinterpret_cast<const float*>(corr_b + corr_offset(ent[q][j]))) * scale;
         xm = fmaxf(xm, x[j]);
       }
       float se = 0.f;
 #pragma unroll
       for (int j = 0; j < K; ++j) {
-        x[j] = __expf(x[j] - xm);
+        x[j] = __builtin_amdgcn_exp2f(x[j] - xm);
         se += x[j];
       }
       const float r = 1.f / se;
 #pragma unroll
-      for (int j = 0; j < K; ++j)
-        __hip_atomic_fetch_add(reinterpret_cast<unsigned long long*>(cells + at[q][j] + 8), to_fixed48(x[j] * r),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      for (int j = 0; j < K; ++j) *reinterpret_cast<float*>(wsum_b + slot_offset(ent[q][j])) = x[j] * r;
     }
     __syncthreads();
+    // The loads (iterate.py:146-149): piece sums, then each target adds its pieces in order.
+    if (piece_hi > piece_lo) {
+      // The piece is contiguous in LDS and ends inside its L-block (or at the block's last slot,
+      // followed by the skew word): reads eight at a time past its end stay inside the array and
+      // are masked out of the sum, which runs in position order.
+      const float* src = wsum + skewed(piece_lo, shift);
+      const int len = piece_hi - piece_lo;
+      float sum = 0.f;
+#pragma unroll 1
+      for (int i = 0; i < len; i += 8) {
+        float v[8];
+#pragma unroll
+        for (int w = 0; w < 8; ++w) v[w] = src[i + w];
+#pragma unroll
+        for (int w = 0; w < 8; ++w) sum += i + w < len ? v[w] : 0.f;
+      }
+      psum[t] = sum;
+    }
+    __syncthreads();
+    // The factor step (iterate.py:150-154).
     if (t < M) {
-      const float load = static_cast<float>(static_cast<double>(cell[t].load) * kFixedUnit);
+      float load = 0.f;
+      const int hi = pstart[t + 1];
+#pragma unroll 1
+      for (int i = pstart[t]; i < hi; i += 8) {
+        float v[8];
+#pragma unroll
+        for (int w = 0; w < 8; ++w) v[w] = psum[min(i + w, hi - 1)];
+#pragma unroll
+        for (int w = 0; w < 8; ++w) load += i + w < hi ? v[w] : 0.f;
+      }
       float step = temperature * (logf(fmaxf(load, kLoadFloor)) - share_s[t]);
       step = fminf(fmaxf(step, -bound), bound);
-      const float c = cell[t].corr + a.relax * step;
-      cell[t].corr = live_s[t] ? c : 0.f;
+      const float c = corr[t] + a.relax * step;
+      corr[t] = live_s[t] ? c : 0.f;
     }
     __syncthreads();
     temperature *= a.anneal;
@@ -551,7 +870,7 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_fit_kernel(FitArgs a) {
 
   float bias = 0.f;
   if (t < M) {
-    bias = a.offset[p * M + t] + cell[t].corr;
+    bias = a.offset[p * M + t] + corr[t];
     a.out[p * M + t] = bias;
   }
   if (a.table == nullptr) return;
@@ -655,7 +974,7 @@ hipError_t launch_shortlist(const ShortArgs& a, int64_t n, hipStream_t s) {
 
 template <int DT>
 hipError_t launch_condense(const CondenseArgs& a, int k, int64_t n, hipStream_t s) {
-  const dim3 grid((a.A + kItemThreads - 1) / kItemThreads, static_cast<unsigned>(n)), block(kItemThreads);
+  const dim3 grid((a.A + kCondenseItems - 1) / kCondenseItems, static_cast<unsigned>(n)), block(kItemThreads);
   switch (k) {
     case 1: hipLaunchKernelGGL((voronoi_condense_kernel<DT, 1>), grid, block, 0, s, a); break;
     case 2: hipLaunchKernelGGL((voronoi_condense_kernel<DT, 2>), grid, block, 0, s, a); break;
