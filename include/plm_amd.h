@@ -341,7 +341,7 @@ size_t plm_gemm_packed_lora_workspace_bytes(int64_t M, int64_t N, int64_t K, int
  *
  * Sizes (the reference's limits, auxiliary.py:24-25 and iterate.py:298-300, and this build's):
  * n_targets and k powers of two, k <= n_targets <= 128, k <= 16; n_items a power of two in
- * [64, 8192] with k * max(1, n_items / 1024) <= 32; n_targets <= n_vocab <= 65536;
+ * [64, 8192] with k * max(1, n_items / 1024) <= 32; n_targets <= n_vocab <= 65528;
  * 1 <= n_problems <= 65535. All pointers are device pointers. `table` has n_vocab rows; token ids
  * handed in (tokens[]) are clamped into [0, n_vocab), so no input reads outside it.
  *

@@ -34,7 +34,8 @@ constexpr int kRowThreads = 1024;  // shortlist and fit workgroups
 constexpr int kRowWaves = kRowThreads / 64;
 constexpr int kCandidateCap = 2048;
 constexpr int kMaxTargets = 128;   // the packed key keeps the target in its low 7 bits
-constexpr int kMaxVocab = 65536;   // token ids ride in the low 16 bits of the sort key
+constexpr int kMaxVocab = 65528;   // token ids ride in the low 16 bits of the sort key; the row + 7
+                                   // tokens of alignment fits 64 elements per thread
 constexpr int kMaxItems = 8192;
 constexpr int kMinItems = 64;
 constexpr int kMaxSlots = 16;
@@ -322,19 +323,22 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_shortlist_kernel(ShortArg
   const int M = a.M;
   const uint16_t* row = a.logits + p * a.ld;
 
-  // The row as order keys, two per register; key 0 marks a position past the vocabulary. Element
-  // j of this thread is token 8 (t + 1024 (j / 8)) + j % 8: eight consecutive tokens per 16-byte
-  // load when the row is 16-byte aligned.
+  // The row as order keys, two per register; key 0 marks a position outside the vocabulary. The
+  // row is read in 16-byte pieces from the 16-byte boundary at or below its start, which lies
+  // `shift` tokens before it: element j of this thread is token 8 (t + 1024 (j / 8)) + j % 8 - shift.
+  // Pieces lying wholly inside the row are one load; the (at most two) straddling an end are read
+  // token by token.
   uint32_t kk[JT / 2];
   uint32_t kmax = 0;
-  const bool vec = (reinterpret_cast<uintptr_t>(row) & 15u) == 0;
-  auto token_of = [&](int j) -> int { return 8 * (t + kRowThreads * (j >> 3)) + (j & 7); };
+  const int shift = static_cast<int>((reinterpret_cast<uintptr_t>(row) & 15u) >> 1);
+  const uint16_t* base = row - shift;
+  auto token_of = [&](int j) -> int { return 8 * (t + kRowThreads * (j >> 3)) + (j & 7) - shift; };
 #pragma unroll
   for (int c = 0; c < JT / 8; ++c) {
-    const int i0 = 8 * (t + kRowThreads * c);
+    const int i0 = 8 * (t + kRowThreads * c) - shift;
     uint32_t h[8];
-    if (vec && i0 + 8 <= a.V) {
-      const u32x4 w = *reinterpret_cast<const u32x4*>(row + i0);
+    if (i0 >= 0 && i0 + 8 <= a.V) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(base + 8 * (t + kRowThreads * c));
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         h[2 * e] = w[e] & 0xFFFFu;
@@ -342,11 +346,11 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_shortlist_kernel(ShortArg
       }
     } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) h[e] = i0 + e < a.V ? row[i0 + e] : 0x8000u;
+      for (int e = 0; e < 8; ++e) h[e] = (i0 + e >= 0 && i0 + e < a.V) ? row[i0 + e] : 0x8000u;
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const uint32_t k = i0 + e < a.V ? order_key16(h[e]) : 0u;
+      const uint32_t k = (i0 + e >= 0 && i0 + e < a.V) ? order_key16(h[e]) : 0u;
       const int j = 8 * c + e;
       if (j & 1)
         kk[j >> 1] |= k << 16;
@@ -847,22 +851,33 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_fit_kernel(FitArgs a) {
       psum[t] = sum;
     }
     __syncthreads();
-    // The factor step (iterate.py:150-154).
-    if (t < M) {
+    // The factor step (iterate.py:150-154). Eight threads per target (8 m + g) add contiguous
+    // shares of its pieces; the octet combines them in a fixed butterfly.
+    {
+      const int m = t >> 3, g = t & 7;
       float load = 0.f;
-      const int hi = pstart[t + 1];
+      if (m < M) {
+        const int first = pstart[m], count = pstart[m + 1] - first;
+        const int share = (count + 7) >> 3;
+        const int lo = first + min(count, g * share), hi = first + min(count, (g + 1) * share);
 #pragma unroll 1
-      for (int i = pstart[t]; i < hi; i += 8) {
-        float v[8];
+        for (int i = lo; i < hi; i += 8) {
+          float v[8];
 #pragma unroll
-        for (int w = 0; w < 8; ++w) v[w] = psum[min(i + w, hi - 1)];
+          for (int w = 0; w < 8; ++w) v[w] = psum[min(i + w, hi - 1)];
 #pragma unroll
-        for (int w = 0; w < 8; ++w) load += i + w < hi ? v[w] : 0.f;
+          for (int w = 0; w < 8; ++w) load += i + w < hi ? v[w] : 0.f;
+        }
       }
-      float step = temperature * (logf(fmaxf(load, kLoadFloor)) - share_s[t]);
-      step = fminf(fmaxf(step, -bound), bound);
-      const float c = corr[t] + a.relax * step;
-      corr[t] = live_s[t] ? c : 0.f;
+      load += dpp<kDppXor1>(load);
+      load += dpp<kDppXor2>(load);
+      load += dpp<kDppHalfMirror>(load);
+      if (g == 0 && m < M) {
+        float step = temperature * (logf(fmaxf(load, kLoadFloor)) - share_s[m]);
+        step = fminf(fmaxf(step, -bound), bound);
+        const float c = corr[m] + a.relax * step;
+        corr[m] = live_s[m] ? c : 0.f;
+      }
     }
     __syncthreads();
     temperature *= a.anneal;
@@ -952,7 +967,8 @@ bool pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
 
 template <int DT>
 hipError_t launch_shortlist(const ShortArgs& a, int64_t n, hipStream_t s) {
-  const int jt = static_cast<int>((a.V + kRowThreads - 1) / kRowThreads + 7) / 8 * 8;
+  // elements per thread: the row plus up to 7 tokens before it (the aligned start), in multiples of 8
+  const int jt = static_cast<int>((a.V + 7 + kRowThreads - 1) / kRowThreads + 7) / 8 * 8;
   const dim3 grid(static_cast<unsigned>(n)), block(kRowThreads);
   switch (jt) {
 #define PLM_VOR_JT(J) \
