@@ -353,3 +353,63 @@ def test_chain_sync_mode_requires_line_aligned_consumed_rows():
     assert mode(arr) == 1
     assert lib.plm_gemm_chain_packed_sync_mode(arr, 0, tile) == -1
     assert lib.plm_gemm_chain_packed_sync_mode(arr, 3, _lib.Tile(3, 8, 1, 2)) == -3
+
+
+def test_voronoi_argument_validation_happens_before_launch():
+    lib = _lib.lib()
+    fake = 1 << 20  # never dereferenced: every call below fails validation first
+
+    def assign(n=7, V=50257, A=1024, M=128, k=8, rounds=2, values=fake, decoded=fake, ws=fake, ws_bytes=1 << 30,
+               dtype=0, ld=50264):
+        return lib.plm_voronoi_assign(dtype, fake, ld, fake, n, V, A, M, k, rounds, 12, 0.1, 0.15, 0.35, 1.9, 0.0087,
+                                      0.25, values, decoded, None, None, None, None, ws, ws_bytes, None)
+
+    assert assign(M=100) == -1                       # n_targets a power of two
+    assert assign(M=256) == -1                       # at most 128 (the key's 7 target bits)
+    assert assign(k=3) == -1 and assign(k=32) == -1  # k a power of two <= 16
+    assert assign(A=1000) == -1 and assign(A=16384) == -1
+    assert assign(A=8192, k=8) == -1                 # k * A / 1024 <= 32
+    assert assign(V=65529) == -1 and assign(V=64) == -1
+    assert assign(n=0) == -1 and assign(rounds=0) == -1
+    assert assign(dtype=2) == -1
+    assert assign(ld=50000) == -1                    # a row stride below the vocabulary
+    assert assign(values=None) == -1                 # values and decoded go together
+    assert assign(ws=None) == -4 and assign(ws_bytes=1024) == -4
+    need = lib.plm_voronoi_assign_workspace_bytes(7, 128, 8, 1024)
+    assert need >= _lib.COUNTER_BYTES + 7 * 8 * 1024 * 4
+    assert lib.plm_voronoi_assign_workspace_bytes(0, 128, 8, 1024) == 0
+    assert lib.plm_voronoi_fit(fake, fake, fake, fake, 7, 128, 8, 1024, 12, -0.1, 1.9, 0.0087, 0.25, fake, None) == -1
+    assert lib.plm_voronoi_fit(fake, fake, fake, fake, 7, 128, 16, 4096, 12, 0.15, 1.9, 0.0087, 0.25, fake, None) == -1
+    assert lib.plm_voronoi_condense(0, fake, 50257, 1024, fake, fake, 7, 128, 256, fake, None) == -1
+    assert lib.plm_voronoi_spread(0, fake, 50257, 1024, fake, 7, 128, 65, fake, None) == -1
+    assert lib.plm_voronoi_shortlist(0, fake, 50257, fake, 7, 50257, 1024, 128, 0.1, None, fake, None, fake, fake,
+                                     None, None) == -1
+    tile = _lib.Tile(2, 1, 1, 2)
+    # The verify rows' logits are the model dtype's: fp32 rounding is refused, as are misaligned rows.
+    assert lib.plm_lm_head_verify_packed_logits(0, fake, 2048, fake, 56, 50257, 2048, fake, 6, 0, 0.94, 0, fake, fake,
+                                                fake, 50264, 7, tile, fake, 1 << 30, None) == -1
+    assert lib.plm_lm_head_verify_packed_logits(0, fake, 2048, fake, 56, 50257, 2048, fake, 6, 0, 0.94, 1, fake, fake,
+                                                fake, 50260, 7, tile, fake, 1 << 30, None) == -2
+    assert lib.plm_lm_head_verify_packed_logits(0, fake, 2048, fake, 56, 50257, 2048, fake, 57, 0, 0.94, 1, fake, fake,
+                                                fake, 50264, 7, tile, fake, 1 << 30, None) == -1
+
+
+def test_voronoi_host_checks_refuse_cpu_and_bad_sizes():
+    from plm_amd import voronoi
+
+    with pytest.raises(RuntimeError, match="GPU only"):
+        voronoi.Voronoi.from_table(torch.zeros(300, 64, dtype=torch.bfloat16))
+    with pytest.raises(TypeError):
+        voronoi.Voronoi.from_table(torch.zeros(300, 64, dtype=torch.float32))
+    with pytest.raises(ValueError):
+        voronoi._check_sizes(7, 50257, 1000, 128)
+    with pytest.raises(ValueError):
+        voronoi._check_sizes(7, 50257, 8192, 128, 8)
+    voronoi._check_sizes(7, 50257, 8192, 128, 4)
+    with pytest.raises(ValueError):
+        voronoi.LogitVoronoiAuxiliary(1024, 64, 1000, top_m=96)
+    with pytest.raises(ValueError):
+        voronoi.LogitVoronoiAuxiliary(1024, 64, 1000, backend="exact")
+    scheme = voronoi.LogitVoronoiAuxiliary(1024, 64, 1000)
+    assert scheme.masked_value == 1024 and scheme.placeholder_token_id == 1000
+    assert set(scheme.state_dict()) == {"auxiliary_vocabulary", "mask_auxiliary"}
