@@ -554,7 +554,44 @@ def time_configs(args, device, rnd, chained, us_round, us_graph):
     torch.cuda.empty_cache()
     out["3_round_1p3b"] = {"chained": _line(us_round, rnd.bytes), "per_gemm": _line(us_graph, rnd.bytes),
                            "note": "the headline; cpu_baseline holds its CPU figure"}
+    out["round_w110"] = time_wide_round(args, device, rnd)
     return out
+
+
+def time_wide_round(args, device, rnd):
+    """The headline round's linears (the same 24 blocks + LM head) at the relaxed setting's width
+    W = k + k^2 = 110 (k = 10, plm/rounds.py:26-29), both implementations; the chain is first checked
+    bit for bit against per-linear launches with its tile."""
+    import torch
+
+    from plm_amd import gemm_tables
+    from plm_amd.fast_gemm import hip_linear
+
+    tables = gemm_tables.read_table(args.hidden)
+    wide = Round(110, args.hidden, args.mlp, args.layers, rnd.weights, tables, device, gemms=rnd.gemms)
+    cw = ChainedRound(wide)
+    cw.run()
+    torch.cuda.synchronize()
+    chain_outs = [o.clone() for o in wide.outs]
+    for i, ln in enumerate(cw.chain.links):
+        hip_linear(ln.x, ln.w, dict(cw.chain.cfg, split_k=ln.split_k), wide.outs[i])
+    hip_linear(*cw.head)
+    torch.cuda.synchronize()
+    same = all(torch.equal(a, b) for a, b in zip(chain_outs, wide.outs))
+    cw.chain.check()
+    graph = capture_graph(cw.run)
+    us_chain = time_graph(graph, max(5, args.steps // 2), 2) * 1000.0
+    del graph
+    graph = wide.capture()
+    us_graph = time_graph(graph, max(5, args.steps // 2), 2) * 1000.0
+    del graph
+    line = {"chained": _line(us_chain, wide.bytes, launches=2, chain_matches_per_linear=bool(same)),
+            "per_gemm": _line(us_graph, wide.bytes, launches=len(wide.gemms)),
+            "shape": f"the headline round's {len(wide.gemms)} linears at M=110 (k=10)"}
+    print(f"[bench] W=110 round: chained {us_chain:.1f} us, per-GEMM {us_graph:.1f} us", file=sys.stderr, flush=True)
+    del cw, wide, chain_outs
+    torch.cuda.empty_cache()
+    return line
 
 
 def profile_verify(args, device):

@@ -810,7 +810,7 @@ constexpr bool packed_compiled() {
     return packed_lds_body<MT, NF, KW>() + kFragBytes <= 160 * 1024 &&
            packed_regs<MT, NF, D, KW>() <= (KW == 8 ? 144 : 60);
   }
-  return packed_two_per_cu<MT, NF, D, KW>() || (MT <= 4 && packed_regs<MT, NF, D, KW>() <= 320);
+  return packed_two_per_cu<MT, NF, D, KW>() || packed_regs<MT, NF, D, KW>() <= 320;
 }
 
 template <int MT, int NF, int KW>

@@ -55,13 +55,13 @@ def two_per_cu(M: int, cfg: dict) -> bool:
 def compiled(M: int, cfg: dict) -> bool:
     """Whether the library has a packed-GEMM kernel for this tile at width M (mirrors
     ``packed_compiled`` in csrc/packed_gemm.h: at most 20 accumulator fragments, and two
-    workgroups per CU, or one with the pipeline within 320 registers for M <= 64)."""
+    workgroups per CU, or one with the pipeline within 320 registers)."""
     mt, nf, d, kw = math.ceil(M / 16), cfg["wave_frags"], cfg["unroll"], cfg["k_waves"]
     if not (1 <= mt <= 8 and nf in WAVE_FRAGS and d in DEPTHS and kw in LAYOUTS) or nf * mt > 20:
         return False
     if kw > 4:
         return lds_body(mt, nf, kw) + FRAG <= LDS_LIMIT and _regs(mt, nf, d, kw) <= (144 if kw == 8 else 60)
-    return two_per_cu(M, cfg) or (mt <= 4 and _regs(mt, nf, d, kw) <= 320)
+    return two_per_cu(M, cfg) or _regs(mt, nf, d, kw) <= 320
 
 
 def tile_frags(cfg: dict) -> int:

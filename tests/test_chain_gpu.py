@@ -281,3 +281,26 @@ def test_round_chain_graph_replays_with_new_inputs(device):
                 cols = sample[sample < ws[i].shape[0]]
                 _oracle_columns(links[i].x, ws[i], ys[i], cols)
     chain.check()
+
+
+def test_wide_round_packed_chain_two_blocks(device):
+    """Two 1.3B-shape blocks chained over packed weights at the relaxed setting's width M = 110
+    (k = 10, seven 16-row fragments), with the tile and splits the benchmark's W = 110 round uses:
+    bit for bit the per-linear launches, and the oracle."""
+    from plm_amd import _lib
+    from plm_amd.fast_gemm import _tile
+    from plm_amd.tiles import packed_chain_split, packed_chain_tile
+
+    M = 110
+    cfg = packed_chain_tile(M)
+    G = _lib.lib().plm_gemm_packed_resident_workgroups(_lib.PLM_BF16, M, _tile(cfg))
+    assert G > 0
+    shapes = [(gm.N, gm.K) for gm in workloads.gpt_block(2048, 8192)] * 2
+    ws = _weights(shapes, 70, device)
+    g = torch.Generator(device=device).manual_seed(71)
+    x = torch.randn(M, 2048, generator=g, device=device).bfloat16()
+    links, _ = _chain(x, ws, [packed_chain_split(n, k, cfg, G) for n, k in shapes])
+    chain = LinearChain(links, cfg, packed=True)
+    chain.run()
+    _check_against_single(links, cfg)
+    chain.check()
