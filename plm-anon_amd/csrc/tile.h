@@ -99,6 +99,7 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
 constexpr size_t kCounterBytes = PLM_WORKSPACE_COUNTER_BYTES;
 constexpr int64_t kMaxCounters = static_cast<int64_t>(kCounterBytes / sizeof(int));
 constexpr int kVerifyCounter = 8;
+constexpr int kVerifyOwnDone = 9;  // the fused verify's own-logit workgroups that have counted in
 constexpr int kVerifyGroupBase = 16;
 constexpr int kVerifyGroupSize = 32;
 constexpr int kStreamDoneEnd = 32768 + 16384;

@@ -56,6 +56,12 @@ struct VerifyArgs {
   uint16_t* logits;     // packed verify: rows [0, logit_rows) of the logits in the model dtype, or null
   int64_t ld_logits;
   int logit_rows;
+  // packed verify: the first own_groups workgroups compute the proposals' own logits (four rows
+  // each) and count themselves into *own_done; the others wait for that count before their first
+  // fold (bounded; a wait that gives up sets *error).
+  int own_groups;
+  int* own_done;
+  int* error;
 };
 
 // Online-softmax state of one row: maximum, sum of exp(l - max), sum of exp(l - max) over l > l_own,
@@ -335,16 +341,18 @@ hipError_t verify_dispatch(const VerifyArgs& a, const plm_tile& t, int cu, hipSt
 // The proposal logit of row r is recomputed by one wavefront with exactly that MFMA chain (the
 // packed fragment row holding pending[r] as A, row r's X fragment as B, K steps ascending), which
 // makes it bit-identical to the main pass's value for that column; plm_gemm_packed_f32out with a
-// row-split tile (k_waves = 1, split_k = 1) returns the same logits.
+// row-split tile (k_waves = 1, split_k = 1) returns the same logits. It runs in the same launch:
+// the first ceil(R / 4) workgroups compute four proposals each (one per wavefront) and count
+// themselves in; the main workgroups need the proposals' logits only at their first fold, after
+// streaming their first tile, and wait for that count there.
 
-// One wavefront per row: own[r] = logit[r, pending[r]] (NaN for an id outside [0, V)).
+// One wavefront per row: own[r] = logit[r, pending[r]] (NaN for an id outside [0, V)), `D` K steps of
+// loads in flight. Written device-coherently: in the fused verify the main workgroups read it.
 template <int DT, int D>
-__global__ __launch_bounds__(64) void verify_packed_own_kernel(VerifyArgs a) {
-  const int lane = threadIdx.x;
-  const int r = blockIdx.x;
+__device__ __forceinline__ void own_logit_wave(const VerifyArgs& a, int r, int lane) {
   const int64_t pid64 = r < a.pending_rows ? a.pending[r] : -1;
   if (pid64 < 0 || pid64 >= a.V) {
-    if (lane == 0) a.own[r] = NAN;
+    if (lane == 0) publish(a.own + r, NAN);
     return;
   }
   const int pid = static_cast<int>(pid64);
@@ -384,7 +392,37 @@ __global__ __launch_bounds__(64) void verify_packed_own_kernel(VerifyArgs a) {
   // Element (vocabulary row pid%16, column r%16) of the 16x16 result: lane r%16 + 16*((pid%16)/4),
   // component pid%4.
   const int v = pid & 15;
-  if (lane == (r & 15) + 16 * (v >> 2)) a.own[r] = round_through(acc[v & 3], a.round_mode);
+  if (lane == (r & 15) + 16 * (v >> 2)) publish(a.own + r, round_through(acc[v & 3], a.round_mode));
+}
+
+// K steps in flight in the fused verify's own-logit workgroups (the main kernel's register budget
+// has room for 16 at every compiled tile).
+constexpr int kOwnDepth = 16;
+
+// The fused prologue: workgroup g < own_groups computes rows 4g .. 4g+3, one per wavefront, then
+// counts itself in once its stores have completed.
+template <int DT>
+__device__ __forceinline__ void own_logit_group(const VerifyArgs& a) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = 4 * static_cast<int>(blockIdx.x) + wave;
+  if (r < a.R) own_logit_wave<DT, kOwnDepth>(a, r, lane);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(a.own_done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Polls before a main workgroup gives up waiting for the own logits (several seconds).
+constexpr int kOwnSpinLimit = 1 << 22;
+
+__device__ __forceinline__ void wait_own_logits(const VerifyArgs& a) {
+  for (int i = 0;; ++i) {
+    if (__builtin_amdgcn_readfirstlane(collect(a.own_done)) >= a.own_groups) return;
+    if (i >= kOwnSpinLimit) {
+      if ((threadIdx.x & 63) == 0) publish(a.error, 1);
+      return;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
 }
 
 // The final merges run once per launch, on its critical path, so their code is kept short (rolled
@@ -540,6 +578,11 @@ constexpr bool verify_packed_compiled() {
 template <int DT, int MT, int NF, int D>
 __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D, 1>())) void verify_packed_main_kernel(
     VerifyArgs a) {
+  if (static_cast<int>(blockIdx.x) < a.own_groups) {
+    own_logit_group<DT>(a);
+    return;
+  }
+  const int b = static_cast<int>(blockIdx.x) - a.own_groups;  // this workgroup among the main ones
   constexpr int KW = 1;
   constexpr int XN = x_per_wave<MT, KW>();
   __shared__ float st_mx[kPackedWaves][64], st_se[kPackedWaves][64], st_ab[kPackedWaves][64];
@@ -569,15 +612,18 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D
   // Row states of the rows this lane's accumulators hold: row 16t + lane%16.
   RowState rs[MT];
   float own_l[MT];
+  // Own logits: already there when a separate pass ran first, else read at the first fold, after
+  // the own-logit workgroups have counted in (they run while this workgroup streams its first tile).
+  bool own_ready = a.own_groups == 0;
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
     rs[t] = empty_state();
     const int m = 16 * t + (lane & 15);
-    own_l[t] = m < a.R ? a.own[m] : 0.f;
+    own_l[t] = (own_ready && m < a.R) ? a.own[m] : 0.f;
   }
 
   u32x4 wb[D][NF], xb[D][XN];
-  PCursor ld{static_cast<int>(blockIdx.x), 0, 0, 0, 0};
+  PCursor ld{b, 0, 0, 0, 0};
   pc_enter<NF, D, KW>(L, wave, ld);
   PCursor cp = ld;
   if (ld.item < L.items) {
@@ -619,6 +665,15 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D
       // Fold this wavefront's 16*NF columns into the row states (rounding mode resolved once per
       // item, not per element).
       const int n0 = (cp.item * kPackedWaves + wave) * NF * 16 + 4 * (lane >> 4);
+      if (!own_ready) {
+        wait_own_logits(a);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const int m = 16 * t + (lane & 15);
+          own_l[t] = m < a.R ? collect(a.own + m) : 0.f;
+        }
+        own_ready = true;
+      }
       if (a.logit_rows > 0) store_logits<DT, MT, NF>(acc, n0, a);
       if (a.round_mode == PLM_ROUND_BF16)
         fold_columns<MT, NF, PLM_ROUND_BF16>(acc, n0, a.V, own_l, rs);
@@ -650,7 +705,7 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D
     RowState s0 = RowState{st_mx[0][m], st_se[0][m], st_ab[0][m], st_ai[0][m]};
 #pragma unroll
     for (int w = 1; w < kPackedWaves; ++w) s0 = merge(s0, RowState{st_mx[w][m], st_se[w][m], st_ab[w][m], st_ai[w][m]});
-    const int64_t slot = static_cast<int64_t>(blockIdx.x) * a.R + m;
+    const int64_t slot = static_cast<int64_t>(b) * a.R + m;
     publish(a.state + slot * 3 + 0, s0.mx);
     publish(a.state + slot * 3 + 1, s0.se);
     publish(a.state + slot * 3 + 2, s0.ab);
@@ -659,7 +714,7 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D
   // Two-level merge: the last workgroup of each group of kVerifyGroupSize merges the group's
   // states, the last group to finish merges the group states. Each level is one batch of
   // device-coherent loads into LDS and a fixed-order merge with one lane per row.
-  const int group = blockIdx.x / kVerifyGroupSize;
+  const int group = b / kVerifyGroupSize;
   const int gsize = min(kVerifyGroupSize, a.G - group * kVerifyGroupSize);
   if (!arrive_last(a.group_counter + group, gsize)) return;
   gather_states(a.state, a.state_idx, group * kVerifyGroupSize, gsize, a.R, grid);
@@ -678,7 +733,8 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D
   gather_states(a.gstate, a.gstate_idx, 0, groups, a.R, grid);
   const RowState t = merge_rows(grid, groups, wave, lane, st_mx, st_se, st_ab, st_ai);
   if (wave == 0) {
-    const bool acc = lane < a.R && accept_proposal(a, a.own[lane], t);
+    if (lane == 0 && a.own_groups > 0) publish(a.own_done, 0);  // every workgroup has counted in and read it
+    const bool acc = lane < a.R && accept_proposal(a, collect(a.own + lane), t);
     if (lane < a.R) {
       if (a.accept != nullptr) a.accept[lane] = acc ? 1 : 0;
       if (a.argmax != nullptr) a.argmax[lane] = t.ai;
@@ -707,11 +763,11 @@ hipError_t launch_verify_packed(VerifyArgs a, int cu_count, hipStream_t stream, 
       if (per_cu < 1) return hipErrorInvalidConfiguration;
     }
     const int tiles = ((a.V + 15) / 16 + kPackedWaves * NF - 1) / (kPackedWaves * NF);
-    a.G = min(tiles, min(kMaxVerifyGroups, cu_count * per_cu));
-    hipLaunchKernelGGL((verify_packed_own_kernel<DT, 16>), dim3(a.R), dim3(64), 0, stream, a);
-    hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(main_kern, dim3(a.G), dim3(64 * kPackedWaves), lds, stream, a);
+    // The own-logit workgroups first (lowest indices: dispatched first, and they wait for nothing),
+    // then the main ones, all resident together when the GPU is otherwise idle.
+    a.own_groups = (a.R + kPackedWaves - 1) / kPackedWaves;
+    a.G = min(tiles, min(kMaxVerifyGroups, max(1, cu_count * per_cu - a.own_groups)));
+    hipLaunchKernelGGL(main_kern, dim3(a.own_groups + a.G), dim3(64 * kPackedWaves), lds, stream, a);
     return hipGetLastError();
   }
 }
@@ -743,7 +799,8 @@ hipError_t verify_packed_dispatch(const VerifyArgs& a, const plm_tile& t, int cu
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
-// Workspace layout: counter area (ints kVerifyCounter and [kVerifyGroupBase, +groups) used) |
+// Workspace layout: counter area (ints kVerifyCounter, kVerifyOwnDone, kPkErrorSlot and
+// [kVerifyGroupBase, +groups) used) |
 // own[R] | state[kMaxVerifyGroups][R][3] | state_idx[kMaxVerifyGroups][R] | gstate[groups][R][3] |
 // gstate_idx[groups][R], groups = kMaxVerifyGroups / kVerifyGroupSize.
 constexpr int kMaxVerifyGroupSets = kMaxVerifyGroups / kVerifyGroupSize;
@@ -896,6 +953,8 @@ int packed_verify_entry(int32_t dtype, const void* x, int64_t ldx, const void* p
   a.group_counter = reinterpret_cast<int*>(ws) + plm::kVerifyGroupBase;
   a.gstate = reinterpret_cast<float*>(ws + gstate_off);
   a.gstate_idx = reinterpret_cast<int*>(ws + gidx_off);
+  a.own_done = reinterpret_cast<int*>(ws) + plm::kVerifyOwnDone;
+  a.error = reinterpret_cast<int*>(ws) + plm::kPkErrorSlot;
 
   const hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t err = dtype == PLM_BF16 ? plm::verify_packed_dispatch<plm::DT_BF16>(a, *tile, 1, s, true)

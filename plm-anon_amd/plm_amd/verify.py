@@ -20,7 +20,7 @@ ROUND_MODES = {"fp32": _lib.PLM_ROUND_F32, "bf16": _lib.PLM_ROUND_BF16, "fp16": 
 RULES = {"nucleus": _lib.PLM_RULE_NUCLEUS, "floor": _lib.PLM_RULE_FLOOR}
 
 # Verify tile over packed weights (plm_lm_head_verify_packed): the row-split layout, 128-row tiles.
-VERIFY_CONFIG: Config = {"wave_frags": 2, "k_waves": 1, "split_k": 1, "unroll": 2}
+VERIFY_CONFIG: Config = {"wave_frags": 4, "k_waves": 1, "split_k": 1, "unroll": 4}
 
 # A GEMM tile with the packed verify's accumulation order (every logit one MFMA chain over the K
 # steps in order): ``hip_linear_f32`` with it (or any row-split tile with split_k 1) returns, bit for
