@@ -848,7 +848,10 @@ def time_verify(w_lm, hidden, device, steps):
             rv(x, w, verify_tokens, *state)
     ms_round = time_graph(graph, max(5, steps // 2), 2) / len(copies)
     del graph, copies
-    mfma = mfma_for("verify_packed_main_kernel<bf16, MT=4, NF=2, D=2>") or {}
+    from plm_amd.verify import VERIFY_CONFIG
+
+    mfma = mfma_for("verify_packed_main_kernel<bf16, MT=4, NF=%d, D=%d>" % (
+        VERIFY_CONFIG["wave_frags"], VERIFY_CONFIG["unroll"])) or {}
     head = mfma_for("packed_gemm_kernel<bf16, MT=4, NF=4, D=8, KW=1>") or {}
     return {"us": round(ms * 1000.0, 2), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "pct_of_hbm_peak": round(100.0 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 2),
