@@ -667,7 +667,7 @@ def time_llama_rounds(args, device):
 
 def time_gated_lora(args, device):
     """Gated LoRA on the Llama-style 1.3B fused QKV (2048 -> 2048+512+512, rank 16, gate at k = 7):
-    the fused two-launch form (plm_gemm_packed_lora) against the same GEMMs as the reference composes
+    the fused one-launch form (plm_gemm_packed_lora) against the same GEMMs as the reference composes
     them (base GEMM, hidden GEMM, one addmm per shard; the GEMMs on this build's kernel), graphs
     rotating enough weight copies that each call streams its weight from HBM."""
     import torch

@@ -321,9 +321,13 @@ int plm_round_verify_packed(int32_t dtype, const void* x, int64_t ldx, const voi
  * with A the shards' down-projections stacked ([shards*rank, K], packed by plm_pack_weight), B the
  * shards' up-projections stacked by output column (lora_b: [N, rank] row-major), and shard s owning
  * the next shard_sizes[s] output columns (1 <= shards <= 3: a fused q/k/v or gate/up projection;
- * rank a multiple of 8; lora_b 16-byte aligned). Three launches: h into the workspace, the base GEMM
- * (`tile`), then the gated rows' correction in place. gated_from >= M is plm_gemm_packed. Workspace:
- * plm_gemm_packed_lora_workspace_bytes.
+ * rank a multiple of 8, 8 <= rank <= 1024; lora_b 16-byte aligned). One launch on `tile`: its first
+ * workgroups form h (every row, into the workspace), the others run the base GEMM and, once every h
+ * tile is written, add the correction to their gated rows before storing them. The workgroups wait
+ * on each other (bounded: a wait that gives up sets the int at PLM_WORKSPACE_ERROR_INDEX, and the
+ * launch's results are then invalid and the workspace's counter area must be zeroed again before
+ * its next use); two such launches must not run at once on one workspace. gated_from >= M is
+ * plm_gemm_packed. Workspace: plm_gemm_packed_lora_workspace_bytes.
  */
 int plm_gemm_packed_lora(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy,
                          int64_t M, int64_t N, int64_t K, int64_t gated_from, const void* packed_a, const void* lora_b,

@@ -5,7 +5,6 @@
 #include <algorithm>
 #include <vector>
 
-#include "lora.h"
 #include "packed_gemm.h"
 #include "plm_amd.h"
 
@@ -58,8 +57,27 @@ bool packed_tile_valid(const plm_tile* t) {
          (t->unroll == 2 || t->unroll == 4 || t->unroll == 6 || t->unroll == 8);
 }
 
-hipError_t packed_dispatch_dt(int32_t dtype, PackedArgs& a, const plm_tile& t, int cus, hipStream_t s, bool dry) {
+hipError_t packed_dispatch_dt(int32_t dtype, PackedArgs& a, const plm_tile& t, int cus, hipStream_t s, bool dry,
+                              bool lora = false) {
   const int nf = t.wave_frags, d = t.unroll;
+  if (lora) {
+    if (dtype == PLM_BF16) {
+      switch (t.k_waves) {
+        case 1: return packed_dispatch_lora_bf16_k1(a, nf, d, cus, s, dry);
+        case 4: return packed_dispatch_lora_bf16_k4(a, nf, d, cus, s, dry);
+        case 8: return packed_dispatch_lora_bf16_k8(a, nf, d, cus, s, dry);
+        case 16: return packed_dispatch_lora_bf16_k16(a, nf, d, cus, s, dry);
+      }
+    } else if (dtype == PLM_F16) {
+      switch (t.k_waves) {
+        case 1: return packed_dispatch_lora_f16_k1(a, nf, d, cus, s, dry);
+        case 4: return packed_dispatch_lora_f16_k4(a, nf, d, cus, s, dry);
+        case 8: return packed_dispatch_lora_f16_k8(a, nf, d, cus, s, dry);
+        case 16: return packed_dispatch_lora_f16_k16(a, nf, d, cus, s, dry);
+      }
+    }
+    return hipErrorInvalidConfiguration;
+  }
   if (dtype == PLM_BF16) {
     switch (t.k_waves) {
       case 1: return packed_dispatch_bf16_k1(a, nf, d, cus, s, dry);
@@ -90,16 +108,27 @@ int64_t packed_workspace(int64_t M, int64_t N, const plm_tile& t) {
   return static_cast<int64_t>(kCounterBytes) + packed_tiles(N, t) * t.split_k * tile_fragments(t) * mt * kFragBytes;
 }
 
-// The small GEMM that forms h: 16-row tiles of eight wavefronts splitting K, four K splits (a few
-// dozen workgroups for a fused projection's shards*rank rows), two stages.
-constexpr plm_tile kLoraDownTile{1, 8, 4, 2};
+// Gated-LoRA launch (one launch: the h linear's items, then the base linear's). The h linear runs
+// on the base linear's tile with its own K split, so that each wavefront of an h item keeps at
+// least one pipeline's depth of K steps (at most 8 splits); its few items then end early.
+// Workspace: the counter area, the base linear's split partials, the h linear's, then h in the
+// model dtype for every row ([M][shards*rank], 256-aligned).
+struct LoraLayout {
+  int64_t h_split, h_tiles, h_partial, h_offset, bytes;  // h_partial: float offset of h's partials
+};
 
-// Gated-LoRA launch: the larger of the two GEMMs' workspaces (they run one after the other), then
-// the model-dtype h = X[gated_from:] A^T (256-aligned).
-int64_t lora_h_offset(int64_t M, int64_t N, int64_t rows, int64_t width, const plm_tile& t) {
-  const int64_t w = std::max<int64_t>(std::max(packed_workspace(M, N, t), packed_workspace(rows, width, kLoraDownTile)),
-                                      kCounterBytes);
-  return (w + 255) / 256 * 256;
+LoraLayout lora_layout(int64_t M, int64_t N, int64_t K, int64_t width, const plm_tile& t) {
+  LoraLayout l{};
+  const int64_t waves = t.k_waves == 1 ? 1 : t.k_waves;
+  l.h_split = std::min<int64_t>(8, std::max<int64_t>(1, ksteps(K) / (waves * t.unroll)));
+  l.h_tiles = packed_tiles(width, t);
+  const int64_t mt = (M + 15) / 16, per_tile = tile_fragments(t) * mt * (kFragBytes / 4);
+  const int64_t base = t.split_k > 1 ? packed_tiles(N, t) * t.split_k * per_tile : 0;
+  const int64_t h = l.h_split > 1 ? l.h_tiles * l.h_split * per_tile : 0;
+  l.h_partial = base;
+  l.h_offset = (static_cast<int64_t>(kCounterBytes) + (base + h) * 4 + 255) / 256 * 256;
+  l.bytes = l.h_offset + M * width * 2;
+  return l;
 }
 
 constexpr int kPackedSpinLimit = 1 << 20;  // polls (each one device round trip) before a wait gives up
@@ -122,7 +151,7 @@ int packed_check_linear(int32_t dtype, const plm_chain_gemm& g, int64_t M) {
 }
 
 int packed_launch_args(int32_t dtype, PackedArgs& a, const plm_tile& t, void* workspace, size_t workspace_bytes,
-                       int64_t need, hipStream_t s) {
+                       int64_t need, hipStream_t s, bool lora = false) {
   if (need > 0 && (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < need ||
                    (reinterpret_cast<uintptr_t>(workspace) & 15) != 0))
     return PLM_ERR_WORKSPACE;
@@ -131,8 +160,8 @@ int packed_launch_args(int32_t dtype, PackedArgs& a, const plm_tile& t, void* wo
   a.counters = need > 0 ? static_cast<int*>(workspace) : nullptr;
   a.partial = need > 0 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes) : nullptr;
   a.spin_limit = kPackedSpinLimit;
-  if (packed_dispatch_dt(dtype, a, t, cus, s, true) != hipSuccess) return PLM_ERR_TILE;
-  return packed_dispatch_dt(dtype, a, t, cus, s, false) == hipSuccess ? PLM_OK : PLM_ERR_LAUNCH;
+  if (packed_dispatch_dt(dtype, a, t, cus, s, true, lora) != hipSuccess) return PLM_ERR_TILE;
+  return packed_dispatch_dt(dtype, a, t, cus, s, false, lora) == hipSuccess ? PLM_OK : PLM_ERR_LAUNCH;
 }
 
 int packed_entry(int32_t dtype, const void* x, int64_t ldx, const void* wp, void* y, int64_t ldy, int64_t M, int64_t N,
@@ -379,10 +408,9 @@ int plm_gemm_chain_packed(int32_t dtype, const plm_chain_gemm* host_gemms, const
 
 size_t plm_gemm_packed_lora_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t gated_from, int64_t rank,
                                             int32_t shards, const plm_tile* tile) {
-  (void)K;
-  if (!plm::packed_tile_valid(tile) || M < 1 || N < 1 || rank < 1 || shards < 1) return 0;
-  const int64_t rows = gated_from < M ? M - std::max<int64_t>(gated_from, 0) : 0;
-  return static_cast<size_t>(plm::lora_h_offset(M, N, rows, shards * rank, *tile) + rows * shards * rank * 2);
+  if (!plm::packed_tile_valid(tile) || M < 1 || N < 1 || K < 1 || rank < 1 || shards < 1) return 0;
+  if (gated_from >= M) return static_cast<size_t>(plm::packed_workspace(M, N, *tile));
+  return static_cast<size_t>(plm::lora_layout(M, N, K, shards * rank, *tile).bytes);
 }
 
 int plm_gemm_packed_lora(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy, int64_t M,
@@ -393,9 +421,12 @@ int plm_gemm_packed_lora(int32_t dtype, const void* x, int64_t ldx, const void* 
     return PLM_ERR_ARGUMENT;
   if (gated_from >= M)  // no gated row: the base linear alone (plm/gated_lora.py:47-48)
     return plm::packed_entry(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, 0);
-  if (packed_a == nullptr || lora_b == nullptr || !plm::packed_tile_valid(tile)) return PLM_ERR_ARGUMENT;
+  if (packed_a == nullptr || lora_b == nullptr) return PLM_ERR_ARGUMENT;
+  if (!plm::packed_tile_valid(tile)) return PLM_ERR_TILE;
+  if (N < 1 || N > (int64_t(1) << 30) || K > (int64_t(1) << 30)) return PLM_ERR_ARGUMENT;
+  const plm_tile& t = *tile;
   const int64_t width = shards * rank;  // h columns
-  plm::LoraArgs z{};
+  plm::PackedLora z{};
   int64_t end = 0;
   for (int i = 0; i < 3; ++i) z.shard_end[i] = static_cast<int>(N);
   for (int32_t i = 0; i < shards; ++i) {
@@ -405,32 +436,57 @@ int plm_gemm_packed_lora(int32_t dtype, const void* x, int64_t ldx, const void* 
   }
   if (end != N) return PLM_ERR_ARGUMENT;
   if ((reinterpret_cast<uintptr_t>(lora_b) & 15) != 0) return PLM_ERR_ALIGNMENT;
-  const int64_t rows = M - gated_from;
-  const int64_t h_off = plm::lora_h_offset(M, N, rows, width, *tile);
-  if (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < h_off + rows * width * 2 ||
+  if (N * rank * 2 >= (int64_t(1) << 31)) return PLM_ERR_ARGUMENT;  // B is read through a 32-bit buffer offset
+  const plm::LoraLayout l = plm::lora_layout(M, N, K, width, t);
+  if (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < l.bytes ||
       (reinterpret_cast<uintptr_t>(workspace) & 15) != 0)
     return PLM_ERR_WORKSPACE;
-  void* h = static_cast<char*>(workspace) + h_off;
-  // h = X[gated_from:] A^T in the model dtype, as the reference's second GEMM returns it (54).
-  const plm_tile down = plm::kLoraDownTile;
-  const void* xg = static_cast<const char*>(x) + gated_from * ldx * 2;
-  int status = plm::packed_entry(dtype, xg, ldx, packed_a, h, width, rows, width, K, &down, workspace, workspace_bytes,
-                                 stream, 0);
+  // The base linear: Y = X W^T for every row (the reference's base output, plm/gated_lora.py:52).
+  plm_chain_gemm g{};
+  g.x = x;
+  g.w = packed_w;
+  g.y = y;
+  g.ldx = ldx;
+  g.ldw = K;
+  g.ldy = ldy;
+  g.N = static_cast<int32_t>(N);
+  g.K = static_cast<int32_t>(K);
+  g.split_k = t.split_k;
+  g.dep = -1;
+  g.arrive_base = plm::kPackedArriveBase;
+  int status = plm::packed_check_linear(dtype, g, M);
   if (status != PLM_OK) return status;
-  // Y = X W^T for every row (the reference's base output, in the model dtype), then the gated rows'
-  // correction in place.
-  status = plm::packed_entry(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, 0);
+  // The h linear: h = X A^T in the model dtype (the reference's second GEMM, 54), every row; its
+  // stores are written through to the device-coherent level for the base tiles to read.
+  plm_chain_gemm gh = g;
+  gh.w = packed_a;
+  gh.y = static_cast<char*>(workspace) + l.h_offset;
+  gh.ldy = width;
+  gh.N = static_cast<int32_t>(width);
+  gh.split_k = static_cast<int32_t>(l.h_split);
+  gh.consumed = 1;
+  const int64_t base_tiles = plm::packed_tiles(N, t);
+  gh.arrive_base = static_cast<int32_t>(plm::kPackedArriveBase + base_tiles);
+  gh.partial_offset = l.h_partial;
+  status = plm::packed_check_linear(dtype, gh, M);
   if (status != PLM_OK) return status;
-  z.y = static_cast<uint16_t*>(y);
-  z.ldy = ldy;
-  z.h = static_cast<const uint16_t*>(h);
+  if (base_tiles + l.h_tiles > plm::kPackedBarrierBase - plm::kPackedArriveBase) return PLM_ERR_ARGUMENT;
+  z.pre = gh;
   z.b = static_cast<const uint16_t*>(lora_b);
-  z.ldh = static_cast<int>(width);
   z.rank = static_cast<int>(rank);
   z.gated_from = static_cast<int>(gated_from);
-  z.M = static_cast<int>(M);
-  z.N = static_cast<int>(N);
-  return plm::lora_apply(dtype, z, static_cast<hipStream_t>(stream)) == hipSuccess ? PLM_OK : PLM_ERR_LAUNCH;
+  z.h_tiles = static_cast<int>(l.h_tiles);
+  z.base_tiles = static_cast<int>(base_tiles);
+  z.h_items = static_cast<int>(l.h_tiles * l.h_split);
+  plm::PackedArgs a{};
+  a.single = g;
+  a.count = 2;
+  a.M = static_cast<int>(M);
+  a.G = static_cast<int>(z.h_items + base_tiles * t.split_k);
+  a.sync = 0;
+  a.lora = z;
+  return plm::packed_launch_args(dtype, a, t, workspace, workspace_bytes, l.bytes, static_cast<hipStream_t>(stream),
+                                 true);
 }
 
 }  // extern "C"

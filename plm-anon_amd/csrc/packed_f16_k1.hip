@@ -1,11 +1,16 @@
 // f16 instantiations of the packed-weight GEMM with workgroup layout KW = 1
-// (rows split across the four wavefronts); one translation unit per (dtype, layout) so that they build in parallel.
+// (rows split across the four wavefronts); one translation unit per (dtype, layout) so that they build in
+// parallel. Each also holds the layout's gated-LoRA launches.
 #include "packed_gemm.h"
 
 namespace plm {
 
 hipError_t packed_dispatch_f16_k1(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry) {
   return packed_dispatch_kw<DT_F16, 1>(a, nf, d, cus, s, dry);
+}
+
+hipError_t packed_dispatch_lora_f16_k1(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry) {
+  return packed_dispatch_kw<DT_F16, 1, true>(a, nf, d, cus, s, dry);
 }
 
 }  // namespace plm

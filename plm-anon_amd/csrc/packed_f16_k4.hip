@@ -1,11 +1,16 @@
 // f16 instantiations of the packed-weight GEMM with workgroup layout KW = 4
-// (K split across four wavefronts); one translation unit per (dtype, layout) so that they build in parallel.
+// (K split across four wavefronts); one translation unit per (dtype, layout) so that they build in
+// parallel. Each also holds the layout's gated-LoRA launches.
 #include "packed_gemm.h"
 
 namespace plm {
 
 hipError_t packed_dispatch_f16_k4(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry) {
   return packed_dispatch_kw<DT_F16, 4>(a, nf, d, cus, s, dry);
+}
+
+hipError_t packed_dispatch_lora_f16_k4(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry) {
+  return packed_dispatch_kw<DT_F16, 4, true>(a, nf, d, cus, s, dry);
 }
 
 }  // namespace plm

@@ -65,6 +65,23 @@ constexpr int kPkMaxWorkgroups = 2048;  // progress flags: int64 per workgroup a
 // rewritten (by linear q + 2) after every tile of linear q that a later linear reads is done,
 // and values only grow, so no flag needs clearing.
 constexpr int kPkTileFlags = 1024;
+constexpr int kPkLoraHDone = 12;   // gated-LoRA launch: tiles of h written
+constexpr int kPkLoraPast = 13;    // gated-LoRA launch: base tiles past their wait for h
+
+// Gated low-rank correction inside one launch (plm_gemm_packed_lora, plm/gated_lora.py:45-57):
+// linear 0 forms h = X A^T in the model dtype for every row (each tile counts itself in once
+// written), linear 1 is the base linear, whose tiles wait for every h tile and then store rows
+// m >= gated_from as round(round(acc) + sum_j h[m, s*rank + j] * B[n, j]), s the shard of column
+// n: the reference's base output and one addmm_ per shard. The last base tile to pass its wait
+// resets both counters for the next launch.
+struct PackedLora {
+  plm_chain_gemm pre;   // the h linear (y = h, ldy = its row stride)
+  const uint16_t* b;    // [N][rank], the shards' up-projections stacked by output column
+  int rank, gated_from;
+  int shard_end[3];     // exclusive column ends of the first three shards (N past the last)
+  int h_tiles, base_tiles;
+  int h_items;          // the base linear's items start at workgroup h_items (mod the grid)
+};
 
 struct PackedArgs {
   const plm_chain_gemm* chain;  // device array of `count` linears, or nullptr: use `single`
@@ -78,6 +95,7 @@ struct PackedArgs {
   int spin_limit;  // polls before a wait gives up
   int* counters;
   float* partial;
+  PackedLora lora;  // packed_gemm_kernel<..., LORA = true> only
 };
 
 __device__ __forceinline__ int sgpr(int v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -104,6 +122,7 @@ struct PLinear {
   float* partial;  // split partials
   int64_t* flag;   // sync == 2 and consumed: this linear's tile-done flags (else nullptr)
   int64_t flag_value;  // the value they get: ((epoch + 1) << 16) + seq
+  int role;        // gated-LoRA launch: 1 the h linear, 2 the corrected base linear; else 0
 };
 
 // Wavefronts per workgroup: KW for the K-split layouts, four for the row-split one.
@@ -125,11 +144,14 @@ __device__ __forceinline__ T const_load(const T* p) {
   return *((const __attribute__((address_space(4))) T*)p);
 }
 
-// A linear's descriptor: a chain's from its table, a single linear's from the kernel arguments.
-template <int NF, int KW>
+// A linear's descriptor: a chain's from its table, a single linear's from the kernel arguments
+// (a gated-LoRA launch: linear 0 is the h linear, linear 1 the base).
+template <int NF, int KW, bool LORA = false>
 __device__ __forceinline__ PLinear load_linear(const PackedArgs& a, int gi, int64_t epoch = 0) {
   plm_chain_gemm g = a.single;
-  if (a.chain != nullptr) {
+  if constexpr (LORA) {
+    if (gi == 0) g = a.lora.pre;
+  } else if (a.chain != nullptr) {
     const plm_chain_gemm* c = a.chain + gi;
     g.x = const_load(&c->x);
     g.w = const_load(&c->w);
@@ -167,7 +189,26 @@ __device__ __forceinline__ PLinear load_linear(const PackedArgs& a, int gi, int6
                ? reinterpret_cast<int64_t*>(a.counters + kPackedBarrierBase) + (L.seq & 1) * kPkTileFlags
                : nullptr;
   L.flag_value = ((epoch + 1) << 16) + L.seq;
+  L.role = LORA ? (gi == 0 ? 1 : 2) : 0;
   return L;
+}
+
+// The first item of linear gi this workgroup takes (then every G-th): the gated-LoRA launch gives
+// the h linear's items to workgroups 0, 1, ... and starts the base linear's after them.
+template <bool LORA>
+__device__ __forceinline__ int first_item(const PackedArgs& a, int gi) {
+  if constexpr (LORA) {
+    if (gi == 1) return sgpr((static_cast<int>(blockIdx.x) + a.G - a.lora.h_items % a.G) % a.G);
+  }
+  return static_cast<int>(blockIdx.x);
+}
+
+// Whether an earlier bounded wait of this launch (or of an earlier launch whose flag nobody
+// cleared) gave up. Every wait checks it on entry and every kErrorCheckPolls polls, so once one wait
+// times out the rest of the chain drains at once instead of each link spinning its own limit.
+constexpr int kErrorCheckPolls = 256;
+__device__ __forceinline__ bool chain_failed(const PackedArgs& a) {
+  return __builtin_amdgcn_readfirstlane(collect(a.counters + kPkErrorSlot)) != 0;
 }
 
 // sync == 2: raises the tile-done flag of `tile` once every wavefront's stores of it have
@@ -337,24 +378,118 @@ __device__ __forceinline__ void packed_store4(const PLinear& L, int m, int n, f3
   }
 }
 
+// Gated LoRA, base tile: a first read of the h counter, issued when the tile's K steps end so that
+// it arrives while the tile's sums are formed (and, with split > 1, exchanged).
+__device__ __forceinline__ int lora_probe(const PackedArgs& a) { return collect(a.counters + kPkLoraHDone); }
+
+// Gated LoRA, base tile: every wavefront waits (bounded) until every h tile is written, polling
+// only if the early read was short.
+__device__ __forceinline__ void lora_wait_h(const PackedArgs& a, int lane, int probe) {
+  if (__builtin_amdgcn_readfirstlane(probe) >= a.lora.h_tiles || chain_failed(a)) return;
+  for (int i = 0;; ++i) {
+    if (__builtin_amdgcn_readfirstlane(collect(a.counters + kPkLoraHDone)) >= a.lora.h_tiles) return;
+    if (i >= a.spin_limit) {
+      if (lane == 0) publish(a.counters + kPkErrorSlot, 1);
+      return;
+    }
+    if (i % kErrorCheckPolls == kErrorCheckPolls - 1 && chain_failed(a)) return;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// Eight products of 16-bit pairs added to acc in order.
+template <int DT>
+__device__ __forceinline__ float lora_dot8(u32x4 a, u32x4 b, float acc) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    acc += from_bits16<DT>(static_cast<uint16_t>(a[w] & 0xffffu)) * from_bits16<DT>(static_cast<uint16_t>(b[w] & 0xffffu));
+    acc += from_bits16<DT>(static_cast<uint16_t>(a[w] >> 16)) * from_bits16<DT>(static_cast<uint16_t>(b[w] >> 16));
+  }
+  return acc;
+}
+
+// Gated LoRA: rows n..n+3 of gated column m, the base values rounded to the model dtype plus their
+// correction (h read device-coherently: other workgroups wrote it). Per group of eight rank
+// elements, the four rows' h and B loads are all issued before any is used; rows at or past N load
+// zeros and are not stored.
+template <int DT>
+__device__ __forceinline__ f32x4 lora_correct(const PackedLora& z, int N, int M, int m, int n, f32x4 v) {
+  const auto hr = make_rsrc(z.pre.y, static_cast<uint32_t>(M * z.pre.ldy * 2));
+  const auto brs = make_rsrc(z.b, static_cast<uint32_t>(N * z.rank * 2));
+  const uint32_t hrow = static_cast<uint32_t>(m * z.pre.ldy * 2);
+  uint32_t ho[4], bo[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int c = n + r;
+    const int s = (c >= z.shard_end[0]) + (c >= z.shard_end[1]) + (c >= z.shard_end[2]);
+    ho[r] = c < N ? hrow + static_cast<uint32_t>(s * z.rank * 2) : kOutOfRange;
+    bo[r] = c < N ? static_cast<uint32_t>(c * z.rank * 2) : kOutOfRange;
+  }
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < z.rank / 8; ++j) {
+    u32x4 hv[4], bv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      hv[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(hr, static_cast<int>(ho[r] + 16u * j), 0, kCoherent));
+      bv[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(brs, static_cast<int>(bo[r] + 16u * j), 0, 0));
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = lora_dot8<DT>(hv[r], bv[r], acc[r]);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) v[r] = from_bits16<DT>(to_bits16<DT>(v[r])) + acc[r];
+  return v;
+}
+
 // Fragment q = f*MT + t of a tile, as lane `lane` holds it: rows n0 + 16f + 4*(lane/16) + r
 // (r = 0..3) of column m = 16t + lane%16.
-template <int DT, int MT>
-__device__ __forceinline__ void packed_store_frag(const PLinear& L, int M, int n0, int q, int lane, f32x4 v) {
+template <int DT, int MT, bool LORA>
+__device__ __forceinline__ void packed_store_frag(const PackedArgs& a, const PLinear& L, int M, int n0, int q, int lane,
+                                                  f32x4 v) {
   const int f = q / MT, t = q - f * MT;
   const int m = 16 * t + (lane & 15);
   const int n = n0 + 16 * f + 4 * (lane >> 4);
-  if (m < M && n < L.N) packed_store4<DT>(L, m, n, v);
+  if (m >= M || n >= L.N) return;
+  if constexpr (LORA) {
+    if (L.role == 2 && m >= a.lora.gated_from) v = lora_correct<DT>(a.lora, L.N, M, m, n, v);
+  }
+  packed_store4<DT>(L, m, n, v);
+}
+
+// A tile's Y is stored: raises its tile-done flag (sync == 2), or in a gated-LoRA launch counts an
+// h tile in (once every wavefront's stores of it have completed), or counts a base tile past its
+// wait for h; the last base tile of the launch resets both counters for the next launch.
+template <bool LORA>
+__device__ __forceinline__ void tile_done(const PackedArgs& a, const PLinear& L, int tile) {
+  if constexpr (LORA) {
+    if (L.role == 1) __builtin_amdgcn_s_waitcnt(0);
+    asm volatile("s_barrier" ::: "memory");
+    if (threadIdx.x == 0) {
+      if (L.role == 1) {
+        __hip_atomic_fetch_add(a.counters + kPkLoraHDone, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else if (__hip_atomic_fetch_add(a.counters + kPkLoraPast, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 a.lora.base_tiles - 1) {
+        publish(a.counters + kPkLoraHDone, 0);
+        publish(a.counters + kPkLoraPast, 0);
+      }
+    }
+  } else {
+    publish_tile(L, tile);
+  }
 }
 
 // End of an item for a K-split workgroup: sums the KW wavefronts' tiles (LDS, wavefront order)
 // and writes Y, or with split > 1 the fp32 partial, then the last split to arrive writes Y. With
 // KW > 4 the tiles overlay the wavefronts' X transpose tiles, so the workgroup first waits until
 // every wavefront is past its last K step.
-template <int DT, int MT, int NF, int KW>
-__device__ __forceinline__ void packed_finish(const PLinear& L, int M, int item, int wave, int lane,
+template <int DT, int MT, int NF, int KW, bool LORA>
+__device__ __forceinline__ void packed_finish(const PackedArgs& a, const PLinear& L, int M, int item, int wave, int lane,
                                               f32x4 (&acc)[NF][MT], f32x4* red, int* last_flag) {
   constexpr int Q = NF * MT;
+  int probe = 0;
+  if constexpr (LORA) {
+    if (L.role == 2) probe = lora_probe(a);
+  }
   if constexpr (KW > 4) lds_sync();
 #pragma unroll
   for (int f = 0; f < NF; ++f)
@@ -377,12 +512,15 @@ __device__ __forceinline__ void packed_finish(const PLinear& L, int M, int item,
   }
   lds_sync();  // every wavefront has read the tiles; LDS is free for the next item
   if (L.split == 1) {
+    if constexpr (LORA) {
+      if (L.role == 2) lora_wait_h(a, lane, probe);
+    }
 #pragma unroll
     for (int i = 0; i * KW < Q; ++i) {
       const int q = wave + KW * i;
-      if (q < Q) packed_store_frag<DT, MT>(L, M, n0, q, lane, sum[i]);
+      if (q < Q) packed_store_frag<DT, MT, LORA>(a, L, M, n0, q, lane, sum[i]);
     }
-    publish_tile(L, tile);
+    tile_done<LORA>(a, L, tile);
     return;
   }
   // Split partial: one KiB block per fragment (an fp32 fragment is 64 lanes x 16 bytes), written
@@ -407,6 +545,9 @@ __device__ __forceinline__ void packed_finish(const PLinear& L, int M, int item,
   }
   lds_sync();
   if (*last_flag == 0) return;
+  if constexpr (LORA) {
+    if (L.role == 2) lora_wait_h(a, lane, probe);
+  }
 #pragma unroll
   for (int i = 0; i * KW < Q; ++i) {
     const int q = wave + KW * i;
@@ -424,29 +565,36 @@ __device__ __forceinline__ void packed_finish(const PLinear& L, int M, int item,
         for (int j = 0; j < 8; ++j)
           if (s0 + j < L.split) v += __builtin_bit_cast(f32x4, part[j]);
       }
-      packed_store_frag<DT, MT>(L, M, n0, q, lane, v);
+      packed_store_frag<DT, MT, LORA>(a, L, M, n0, q, lane, v);
     }
   }
-  publish_tile(L, tile);
+  tile_done<LORA>(a, L, tile);
 }
 
 // End of an item for a row-split workgroup (KW = 1): each wavefront owns its NF fragments of the
 // tile outright and writes them (Y, or with split > 1 its fp32 partials; the last split of the
 // tile to arrive sums each wavefront's partials in split order and writes Y).
-template <int DT, int MT, int NF>
-__device__ __forceinline__ void packed_finish_rows(const PLinear& L, int M, int item, int wave, int lane,
-                                                   f32x4 (&acc)[NF][MT], int* last_flag) {
+template <int DT, int MT, int NF, bool LORA>
+__device__ __forceinline__ void packed_finish_rows(const PackedArgs& a, const PLinear& L, int M, int item, int wave,
+                                                   int lane, f32x4 (&acc)[NF][MT], int* last_flag) {
   constexpr int QW = NF * MT;               // fragments of one wavefront
   constexpr int Q = kPackedWaves * QW;      // fragments of the tile
   int tile, s;
   item_tile(item, L.split, tile, s);
   const int n0 = (tile * 4 + wave) * NF * 16;
+  int probe = 0;
+  if constexpr (LORA) {
+    if (L.role == 2) probe = lora_probe(a);
+  }
   if (L.split == 1) {
+    if constexpr (LORA) {
+      if (L.role == 2) lora_wait_h(a, lane, probe);
+    }
 #pragma unroll
     for (int f = 0; f < NF; ++f)
 #pragma unroll
-      for (int t = 0; t < MT; ++t) packed_store_frag<DT, MT>(L, M, n0, f * MT + t, lane, acc[f][t]);
-    publish_tile(L, tile);
+      for (int t = 0; t < MT; ++t) packed_store_frag<DT, MT, LORA>(a, L, M, n0, f * MT + t, lane, acc[f][t]);
+    tile_done<LORA>(a, L, tile);
     return;
   }
   const uint32_t tile_bytes = static_cast<uint32_t>(L.split) * Q * kFragBytes;
@@ -470,6 +618,9 @@ __device__ __forceinline__ void packed_finish_rows(const PLinear& L, int M, int 
   }
   lds_sync();
   if (*last_flag == 0) return;
+  if constexpr (LORA) {
+    if (L.role == 2) lora_wait_h(a, lane, probe);
+  }
   // A rolled loop over the wavefront's fragments: unrolled, the compiler would keep every
   // fragment's partial loads in flight at once and run out of registers.
 #pragma unroll 1
@@ -488,20 +639,12 @@ __device__ __forceinline__ void packed_finish_rows(const PLinear& L, int M, int 
       for (int j = 0; j < 8; ++j)
         if (s0 + j < L.split) v += __builtin_bit_cast(f32x4, part[j]);
     }
-    packed_store_frag<DT, MT>(L, M, n0, qw, lane, v);
+    packed_store_frag<DT, MT, LORA>(a, L, M, n0, qw, lane, v);
   }
-  publish_tile(L, tile);
+  tile_done<LORA>(a, L, tile);
 }
 
 extern __shared__ __attribute__((aligned(16))) f32x4 packed_lds[];
-
-// Whether an earlier bounded wait of this launch (or of an earlier launch whose flag nobody
-// cleared) gave up. Every wait checks it on entry and every kErrorCheckPolls polls, so once one wait
-// times out the rest of the chain drains at once instead of each link spinning its own limit.
-constexpr int kErrorCheckPolls = 256;
-__device__ __forceinline__ bool chain_failed(const PackedArgs& a) {
-  return __builtin_amdgcn_readfirstlane(collect(a.counters + kPkErrorSlot)) != 0;
-}
 
 // Grid barrier after the consumed linear with sequence number `seq`, in two halves so that the
 // wait can overlap weight traffic: barrier_arrive raises this workgroup's progress flag (its
@@ -659,7 +802,7 @@ constexpr size_t packed_lds_body() {
   return red > xts ? red : xts;
 }
 
-template <int DT, int MT, int NF, int D, int KW>
+template <int DT, int MT, int NF, int D, int KW, bool LORA>
 __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT, NF, D, KW>())) void packed_gemm_kernel(PackedArgs a) {
   constexpr int XN = x_per_wave<MT, KW>();
   __shared__ int last_flag;
@@ -680,12 +823,12 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
   // grid barrier): then only X is still to be loaded for them.
   bool w_ready = false;
   for (int gi = 0; gi < a.count; ++gi) {
-    const PLinear L = load_linear<NF, KW>(a, gi, epoch);
+    const PLinear L = load_linear<NF, KW, LORA>(a, gi, epoch);
     POffsets<MT, NF, XN> o;
     packed_offsets<MT, NF, KW>(L, a.M, lane, wave, o);
     const auto wr = make_rsrc(L.wp, static_cast<uint32_t>((L.N + 15) >> 4) * L.Ks * kFragBytes);
     const auto xr = make_rsrc(L.x, static_cast<uint32_t>(a.M * L.ldx * 2));
-    PCursor ld{static_cast<int>(blockIdx.x), 0, 0, 0, 0};
+    PCursor ld{first_item<LORA>(a, gi), 0, 0, 0, 0};
     pc_enter<NF, D, KW>(L, wave, ld);
     PCursor cp = ld;
     if (ld.item < L.items) {
@@ -761,9 +904,9 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
           }
         }
         if constexpr (KW != 1)
-          packed_finish<DT, MT, NF, KW>(L, a.M, cp.item, wave, lane, acc, red, &last_flag);
+          packed_finish<DT, MT, NF, KW, LORA>(a, L, a.M, cp.item, wave, lane, acc, red, &last_flag);
         else
-          packed_finish_rows<DT, MT, NF>(L, a.M, cp.item, wave, lane, acc, &last_flag);
+          packed_finish_rows<DT, MT, NF, LORA>(a, L, a.M, cp.item, wave, lane, acc, &last_flag);
         cp.item += a.G;
         if (cp.item >= L.items) break;
         pc_enter<NF, D, KW>(L, wave, cp);
@@ -776,8 +919,8 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
       // workgroup's part of this Y.
       __builtin_amdgcn_s_waitcnt(0);
       barrier_arrive(a, epoch, L.seq);
-      const PLinear Ln = load_linear<NF, KW>(a, gi + 1);
-      PCursor nx{static_cast<int>(blockIdx.x), 0, 0, 0, 0};
+      const PLinear Ln = load_linear<NF, KW, LORA>(a, gi + 1);
+      PCursor nx{first_item<LORA>(a, gi + 1), 0, 0, 0, 0};
       pc_enter<NF, D, KW>(Ln, wave, nx);
       if (nx.item < Ln.items) {
         POffsets<MT, NF, XN> on;
@@ -821,13 +964,13 @@ constexpr size_t packed_lds_bytes() {
 // Launches with G = min(a.G, resident workgroups), where a.G arrives as the most items of any
 // linear; a chained launch with grid barriers (a.sync) uses every resident workgroup. `dry` only
 // checks that the kernel exists.
-template <int DT, int MT, int NF, int D, int KW>
+template <int DT, int MT, int NF, int D, int KW, bool LORA>
 hipError_t packed_launch(PackedArgs& a, int cus, hipStream_t stream, bool dry) {
   if constexpr (!packed_compiled<MT, NF, D, KW>()) {
     return hipErrorInvalidConfiguration;
   } else {
     if (dry) return hipSuccess;
-    auto kern = packed_gemm_kernel<DT, MT, NF, D, KW>;
+    auto kern = packed_gemm_kernel<DT, MT, NF, D, KW, LORA>;
     constexpr size_t lds = packed_lds_bytes<MT, NF, KW>();
     static int per_cu = 0;
     if (per_cu == 0) {
@@ -853,34 +996,35 @@ hipError_t packed_launch(PackedArgs& a, int cus, hipStream_t stream, bool dry) {
   }
 }
 
-template <int DT, int MT, int NF, int KW>
+template <int DT, int MT, int NF, int KW, bool LORA>
 hipError_t packed_pick_d(PackedArgs& a, int d, int cus, hipStream_t s, bool dry) {
-  if (d == 2) return packed_launch<DT, MT, NF, 2, KW>(a, cus, s, dry);
-  if (d == 4) return packed_launch<DT, MT, NF, 4, KW>(a, cus, s, dry);
-  if (d == 6) return packed_launch<DT, MT, NF, 6, KW>(a, cus, s, dry);
-  if (d == 8) return packed_launch<DT, MT, NF, 8, KW>(a, cus, s, dry);
+  if (d == 2) return packed_launch<DT, MT, NF, 2, KW, LORA>(a, cus, s, dry);
+  if (d == 4) return packed_launch<DT, MT, NF, 4, KW, LORA>(a, cus, s, dry);
+  if (d == 6) return packed_launch<DT, MT, NF, 6, KW, LORA>(a, cus, s, dry);
+  if (d == 8) return packed_launch<DT, MT, NF, 8, KW, LORA>(a, cus, s, dry);
   return hipErrorInvalidConfiguration;
 }
 
-template <int DT, int MT, int KW>
+template <int DT, int MT, int KW, bool LORA>
 hipError_t packed_pick(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry) {
-  if (nf == 1) return packed_pick_d<DT, MT, 1, KW>(a, d, cus, s, dry);
-  if (nf == 2) return packed_pick_d<DT, MT, 2, KW>(a, d, cus, s, dry);
-  if (nf == 4) return packed_pick_d<DT, MT, 4, KW>(a, d, cus, s, dry);
+  if (nf == 1) return packed_pick_d<DT, MT, 1, KW, LORA>(a, d, cus, s, dry);
+  if (nf == 2) return packed_pick_d<DT, MT, 2, KW, LORA>(a, d, cus, s, dry);
+  if (nf == 4) return packed_pick_d<DT, MT, 4, KW, LORA>(a, d, cus, s, dry);
   return hipErrorInvalidConfiguration;
 }
 
-template <int DT, int KW>
+// LORA: the gated-LoRA launch (PackedArgs::lora: two linears, the base tiles corrected).
+template <int DT, int KW, bool LORA = false>
 hipError_t packed_dispatch_kw(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry) {
   switch ((a.M + 15) / 16) {
-    case 1: return packed_pick<DT, 1, KW>(a, nf, d, cus, s, dry);
-    case 2: return packed_pick<DT, 2, KW>(a, nf, d, cus, s, dry);
-    case 3: return packed_pick<DT, 3, KW>(a, nf, d, cus, s, dry);
-    case 4: return packed_pick<DT, 4, KW>(a, nf, d, cus, s, dry);
-    case 5: return packed_pick<DT, 5, KW>(a, nf, d, cus, s, dry);
-    case 6: return packed_pick<DT, 6, KW>(a, nf, d, cus, s, dry);
-    case 7: return packed_pick<DT, 7, KW>(a, nf, d, cus, s, dry);
-    case 8: return packed_pick<DT, 8, KW>(a, nf, d, cus, s, dry);
+    case 1: return packed_pick<DT, 1, KW, LORA>(a, nf, d, cus, s, dry);
+    case 2: return packed_pick<DT, 2, KW, LORA>(a, nf, d, cus, s, dry);
+    case 3: return packed_pick<DT, 3, KW, LORA>(a, nf, d, cus, s, dry);
+    case 4: return packed_pick<DT, 4, KW, LORA>(a, nf, d, cus, s, dry);
+    case 5: return packed_pick<DT, 5, KW, LORA>(a, nf, d, cus, s, dry);
+    case 6: return packed_pick<DT, 6, KW, LORA>(a, nf, d, cus, s, dry);
+    case 7: return packed_pick<DT, 7, KW, LORA>(a, nf, d, cus, s, dry);
+    case 8: return packed_pick<DT, 8, KW, LORA>(a, nf, d, cus, s, dry);
   }
   return hipErrorInvalidConfiguration;
 }
@@ -902,5 +1046,14 @@ hipError_t packed_dispatch_f16_k1(PackedArgs& a, int nf, int d, int cus, hipStre
 hipError_t packed_dispatch_f16_k4(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
 hipError_t packed_dispatch_f16_k8(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
 hipError_t packed_dispatch_f16_k16(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+// The same translation units' gated-LoRA launches.
+hipError_t packed_dispatch_lora_bf16_k1(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_lora_bf16_k4(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_lora_bf16_k8(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_lora_bf16_k16(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_lora_f16_k1(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_lora_f16_k4(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_lora_f16_k8(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_lora_f16_k16(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
 
 }  // namespace plm

@@ -2,9 +2,11 @@
 
 The reference's ``GatedLoraMethod.apply`` runs the base linear over every row, a second GEMM
 ``h = x[g:] A^T`` and one ``addmm_`` per shard of a fused projection (plm/gated_lora.py:45-57). Here a
-tuned, eligible call is one ``plm_gemm_packed_lora``: ``h`` into the workspace, the base GEMM, then
-one small kernel that adds every shard's rank-r correction to the gated rows in place. Calls the reference itself would not route to its fast GEMM (a bias, an untuned shape, a
-non-half dtype) take the reference's unfused composition through ``fast_gemm``'s dispatch slot.
+tuned, eligible call is one launch of ``plm_gemm_packed_lora``: its first workgroups form ``h`` into
+the workspace, the rest run the base GEMM on its tuned tile and add every shard's rank-r correction
+to the gated rows before they store them. Calls the reference itself would not route to its fast
+GEMM (a bias, an untuned shape, a non-half dtype) take the reference's unfused composition through
+``fast_gemm``'s dispatch slot.
 
 ``rows_from(g)`` sets the first gated row for the calls inside it, as the reference's context manager
 does; ``install(model, tensors)`` attaches stacked ``lora_a`` buffers and wraps each adapted layer's
@@ -40,9 +42,6 @@ def rows_from(first_gated_row: int | None) -> Iterator[None]:
         _rows_from = saved
 
 
-# The small GEMM that forms h = x[g:] A^T inside plm_gemm_packed_lora (kLoraDownTile in
-# csrc/packed_api.hip): one 16-row fragment per wavefront, eight wavefronts splitting K, four K splits.
-LORA_DOWN_TILE = {"wave_frags": 1, "k_waves": 8, "split_k": 4, "unroll": 2}
 MAX_RANK = 1024
 
 
@@ -71,7 +70,7 @@ def _eligible(x, weight, lora_a, lora_bs, first_gated_row, bias, cfg) -> bool:
     M, K = x.shape
     if sum(b.shape[0] for b in lora_bs) != weight.shape[0] or K % 8:
         return False
-    return tile_supported(M, K, cfg, x.dtype) and tile_supported(M - first_gated_row, K, LORA_DOWN_TILE, x.dtype)
+    return tile_supported(M, K, cfg, x.dtype)
 
 
 def gated_linear(x: torch.Tensor, weight: torch.Tensor, lora_a: torch.Tensor, lora_bs: list[torch.Tensor],

@@ -48,6 +48,10 @@ CASES = {
     "gate_up": ((5632, 5632), 2048, 16, {"wave_frags": 4, "k_waves": 8, "split_k": 1, "unroll": 2}),
     "o": ((2048,), 2048, 32, {"wave_frags": 2, "k_waves": 8, "split_k": 4, "unroll": 2}),
     "down_rowsplit": ((2048,), 5632, 16, {"wave_frags": 2, "k_waves": 1, "split_k": 2, "unroll": 4}),
+    # 384 base items: more than one workgroup per CU holds, so workgroups take several items and the
+    # ones that form h go on to base items.
+    "qkv_many_items": ((2048, 512, 512), 2048, 16, {"wave_frags": 1, "k_waves": 8, "split_k": 2, "unroll": 2}),
+    "qkv_rank64": ((2048, 512, 512), 2048, 64, {"wave_frags": 2, "k_waves": 4, "split_k": 1, "unroll": 4}),
 }
 
 
@@ -112,3 +116,49 @@ def test_method_wrapper_routes_through_rows_from(device):
     assert torch.equal(plain, hip_linear(xg, wg, cfg))
     _check(gated, oracle.gated_lora(x, w, a, bs, 7))
     assert torch.equal(gated[:7], plain[:7])
+
+
+def _error_flag(device) -> int:
+    """The workspace's error flag: set when a launch's bounded wait gave up."""
+    from plm_amd import _lib, fast_gemm
+
+    ws = fast_gemm.workspace(device, 1 << 20)
+    return int(ws[: 4 * (_lib.ERROR_INDEX + 1)].view(torch.int32)[_lib.ERROR_INDEX].item())
+
+
+def test_graph_replays_with_new_inputs(device):
+    """One launch per call: h formed by the launch's first workgroups, the base tiles waiting for it.
+    Replays of a captured call with X rewritten in place before each must each match an eager call
+    on the same X bit for bit (h and the counters are fresh every launch), and no wait gives up."""
+    shards, K, rank, cfg = CASES["qkv"]
+    _, _, _, _, (xg, wg, ag, bsg) = _operands(56, shards, K, rank, 31, device)
+    from plm_amd.gated_lora import stack_b
+
+    b = stack_b(bsg)
+    x_static = xg.clone()
+    gated_linear(x_static, wg, ag, bsg, 7, cfg=cfg, lora_b=b)   # packs the weights, sizes the workspace
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        out = gated_linear(x_static, wg, ag, bsg, 7, cfg=cfg, lora_b=b)
+    g = torch.Generator().manual_seed(5)
+    for _ in range(4):
+        x_new = torch.randn(56, K, generator=g).bfloat16().to(device)
+        x_static.copy_(x_new)
+        graph.replay()
+        torch.cuda.synchronize()
+        want = gated_linear(x_new, wg, ag, bsg, 7, cfg=cfg, lora_b=b)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want)
+    assert _error_flag(device) == 0
+
+
+def test_back_to_back_calls_and_smaller_width(device):
+    """Consecutive launches on one workspace (each leaves its counters at zero), then a narrower
+    round: every result matches the oracle's composition."""
+    shards, K, rank, cfg = CASES["o"]
+    for M, gate, seed in ((56, 7, 41), (56, 7, 42), (42, 6, 43), (56, 20, 44)):
+        x, w, a, bs, (xg, wg, ag, bsg) = _operands(M, shards, K, rank, seed, device)
+        _check(gated_linear(xg, wg, ag, bsg, gate, cfg=cfg), oracle.gated_lora(x, w, a, bs, gate))
+    assert _error_flag(device) == 0
