@@ -50,6 +50,7 @@ def parse_args():
                     help="skip the per-config lines (single GEMM, one block, the 32 x H2560 round)")
     ap.add_argument("--only-round", action="store_true", help="time the round only (for profiling runs)")
     ap.add_argument("--no-voronoi", action="store_true", help="skip the verify rows' auxiliary decode timing")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-width timing")
     ap.add_argument("--profile", choices=("eager", "copy", "verify", "voronoi"),
                     help="no JSON: 'eager' launches the round and the fused verify step --steps times without a "
                          "graph (for rocprofv3 counter runs); 'copy' runs a 1 GiB device copy, the reference "
@@ -415,6 +416,8 @@ def main():
         if not args.no_llama:
             result["llama_rounds"] = time_llama_rounds(args, device)
             result["gated_lora"] = time_gated_lora(args, device)
+        if not args.no_prefill:
+            result["prefill"] = time_prefill(args, device, weights[:-1])
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_baseline(args.hidden, args.mlp, args.M, args.cpu_seconds)
     print(json.dumps(result), flush=True)
@@ -713,6 +716,51 @@ def time_gated_lora(args, device):
         del graph
     print(f"[bench] gated LoRA qkv: {res}", file=sys.stderr, flush=True)
     return dict(res, shape=f"M={M} N={N} K={K} rank={rank} shards={list(shards)} gate={gate}")
+
+
+def time_prefill(args, device, block_weights):
+    """Prefill widths (M = 64 ... 640, plm/rounds.py:16; the reference hands them to F.linear) over
+    the round's 96 block linears: the packed kernel on the packed copies (fast_gemm's path for a
+    released weight: the tuned tile or default_config, 128-row slices above 128 rows) against
+    F.linear (hipBLASLt) on the row-major weights, each a graph of the 96 launches; per block."""
+    import torch
+    import torch.nn.functional as F
+
+    from plm_amd.fast_gemm import CONFIGS, default_config, hip_linear, packed_weight, unpack_weight
+
+    out = {}
+    for M in (64, 128, 256, 640):
+        gen = torch.Generator(device=device).manual_seed(900 + M)
+        xs = {K: torch.randn(M, K, generator=gen, device=device).bfloat16()
+              for K in sorted({w.shape[1] for w in block_weights})}
+        cfgs = [CONFIGS.get((M, w.shape[0], w.shape[1])) or default_config(M, w.shape[0], w.shape[1])
+                for w in block_weights]
+        flops = sum(2 * M * w.shape[0] * w.shape[1] for w in block_weights)
+        line = {}
+        packs = [packed_weight(w) for w in block_weights]
+        unpack = {id(w): p for w, p in zip(block_weights, packs)}
+        for name, fn in (("packed", lambda w, c: hip_linear(xs[w.shape[1]], w, c)),
+                         ("unpacked_f_linear", lambda w, c: F.linear(
+                             xs[w.shape[1]], unpack_weight(unpack[id(w)], w.shape[0], w.shape[1], w.dtype))),
+                         ("f_linear", lambda w, c: F.linear(xs[w.shape[1]], w))):
+            for w, c in zip(block_weights, cfgs):
+                fn(w, c)
+            torch.cuda.synchronize()
+            stream = torch.cuda.Stream()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                for w, c in zip(block_weights, cfgs):
+                    fn(w, c)
+            us = time_graph(graph, max(5, args.steps // 5), 2) * 1000.0
+            del graph
+            line[name] = {"us_per_block": round(us / (len(block_weights) / 4), 2),
+                          "tflops": round(flops / (us * 1e-6) / 1e12, 1)}
+        out[str(M)] = line
+        print(f"[bench] prefill M={M}: {line}", file=sys.stderr, flush=True)
+    return dict(out, note="96 block linears of the headline round per graph; packed = plm_gemm_packed "
+                          "(128-row slices above 128 rows), unpacked_f_linear = plm_unpack_weight into a "
+                          "transient buffer + F.linear (a released weight's path above 128 rows), f_linear = "
+                          "torch F.linear on a kept row-major weight")
 
 
 # The auxiliary decode's workload: the k = 7 verify rows of a width-56 round, the GPT-2 vocabulary,

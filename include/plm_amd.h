@@ -93,6 +93,16 @@ int plm_pack_weight(int32_t dtype, const void* w, int64_t ldw, int64_t N, int64_
                     void* stream);
 
 /*
+ * The inverse of plm_pack_weight: writes the row-major W[N,K] (row stride ldw, 16-byte aligned,
+ * ldw % 8 == 0) back from its packed copy, bit for bit. No counterpart in the reference, which
+ * keeps only the row-major weight and hands the widths it does not tune (prefill chunks,
+ * plm/rounds.py:16) to F.linear (plm/fast_gemm.py:108-111): a caller that keeps only the packed
+ * copy unpacks a weight into a transient buffer for such a call.
+ */
+int plm_unpack_weight(int32_t dtype, const void* packed, size_t packed_bytes, int64_t N, int64_t K, void* w, int64_t ldw,
+                      void* stream);
+
+/*
  * Y[M,N] = X[M,K] · W[N,K]^T over a packed W, fp32 accumulation, Y in the input dtype: the fast
  * path behind triton_linear (plm/fast_gemm.py:82-97, with gemm_kernel 17-48 and
  * splitk_reduce_kernel 51-61). Tile fields for this kernel: wave_frags = 16-row fragments per
@@ -101,8 +111,11 @@ int plm_pack_weight(int32_t dtype, const void* w, int64_t ldw, int64_t N, int64_
  * workgroup tile is 64*wave_frags rows, each wavefront owns 16*wave_frags of them over the whole
  * K range, and the four share one copy of X through LDS; split_k = workgroups splitting K (1..64,
  * partials summed in split order); unroll = K steps of loads in flight per wavefront (2, 4, 6,
- * 8). Requirements as plm_gemm (1 <= M <= 128, K % 8 == 0, K <= 2^24, ldx % 8 == 0, x 16-byte
- * aligned).
+ * 8). Requirements as plm_gemm (K % 8 == 0, K <= 2^24, ldx % 8 == 0, x 16-byte aligned) except
+ * that M may exceed 128: wider calls (prefill chunks, plm/rounds.py:16, which the reference hands to
+ * F.linear) run as consecutive 128-row slices of X and Y, one launch each, so the tile must have a
+ * kernel at 128 rows and at the last slice's width (plm_gemm_packed_tile_supported checks both).
+ * Workspace: plm_gemm_packed_workspace_bytes (one slice's; the slices share it).
  */
 int plm_gemm_packed(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy, int64_t M,
                     int64_t N, int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream);

@@ -25,6 +25,19 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(const uint16_t* __rest
   }
 }
 
+// The inverse of pack_weight_kernel: thread i writes lane (i % 64) of fragment i / 64 back to its 16
+// bytes of the row-major W (fragments' padding past N or K is dropped).
+__global__ __launch_bounds__(256) void unpack_weight_kernel(const u32x4* __restrict__ packed, int N, int K, int Ks,
+                                                           int64_t lanes, uint16_t* __restrict__ w, int64_t ldw) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < lanes;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int lane = static_cast<int>(i & 63);
+    const int64_t frag = i >> 6;
+    const int f = static_cast<int>(frag / Ks), s = static_cast<int>(frag - static_cast<int64_t>(f) * Ks);
+    const int n = 16 * f + (lane & 15), k = 32 * s + 8 * (lane >> 4);
+    if (n < N && k < K) *reinterpret_cast<u32x4*>(w + static_cast<int64_t>(n) * ldw + k) = packed[i];
+  }
+}
 
 namespace {
 
@@ -195,6 +208,33 @@ int packed_entry(int32_t dtype, const void* x, int64_t ldx, const void* wp, void
                             static_cast<hipStream_t>(stream));
 }
 
+// Widths past one launch's 128 rows (prefill chunks, plm/rounds.py:16): consecutive 128-row slices
+// of X and Y, one launch each on the same stream (each leaves the workspace's counters at zero, so
+// the slices share it). The tile must have a kernel at both slice widths; that and every argument
+// are checked before the first launch, so an invalid call writes nothing.
+int packed_rows(int32_t dtype, const void* x, int64_t ldx, const void* wp, void* y, int64_t ldy, int64_t M, int64_t N,
+                int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream, int out_f32) {
+  if (M <= kPackedMaxM) return packed_entry(dtype, x, ldx, wp, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, out_f32);
+  if (!packed_tile_valid(tile)) return PLM_ERR_TILE;
+  const int64_t rest = M % kPackedMaxM;
+  for (const int64_t rows : {kPackedMaxM, rest}) {
+    if (rows == 0) continue;
+    PackedArgs a{};
+    a.M = static_cast<int>(rows);
+    if (packed_dispatch_dt(dtype, a, *tile, 1, nullptr, true) != hipSuccess) return PLM_ERR_TILE;
+  }
+  if (ldy < N || (M - 1) * ldx + K > (int64_t(1) << 40)) return PLM_ERR_ARGUMENT;
+  const int64_t esize = out_f32 ? 4 : 2;
+  for (int64_t m0 = 0; m0 < M; m0 += kPackedMaxM) {
+    const int64_t rows = std::min(kPackedMaxM, M - m0);
+    const int status = packed_entry(dtype, static_cast<const char*>(x) + m0 * ldx * 2, ldx, wp,
+                                    static_cast<char*>(y) + m0 * ldy * esize, ldy, rows, N, K, tile, workspace,
+                                    workspace_bytes, stream, out_f32);
+    if (status != PLM_OK) return status;
+  }
+  return PLM_OK;
+}
+
 // How the linears of a chain wait for the ones they read: 0 (none reads another), 2 (every linear
 // after the first reads the one before it, none that is read has more tiles than a parity set of
 // tile flags holds, and every Y that is read starts on a 128-byte boundary with rows a multiple of
@@ -272,12 +312,12 @@ PSpan pspan(const void* p, int64_t rows, int64_t ld, int64_t cols, int64_t elem)
 int packed_gemm_call(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy, int64_t M,
                      int64_t N, int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream,
                      int out_f32) {
-  return packed_entry(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, out_f32);
+  return packed_rows(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, out_f32);
 }
 
 int64_t packed_gemm_workspace(int64_t M, int64_t N, const plm_tile* tile) {
   if (!packed_tile_valid(tile) || M < 1 || N < 1) return -1;
-  return packed_workspace(M, N, *tile);
+  return packed_workspace(std::min(M, kPackedMaxM), N, *tile);
 }
 
 }  // namespace plm
@@ -306,28 +346,49 @@ int plm_pack_weight(int32_t dtype, const void* w, int64_t ldw, int64_t N, int64_
   return hipGetLastError() == hipSuccess ? PLM_OK : PLM_ERR_LAUNCH;
 }
 
+int plm_unpack_weight(int32_t dtype, const void* packed, size_t packed_bytes, int64_t N, int64_t K, void* w, int64_t ldw,
+                      void* stream) {
+  if (w == nullptr || packed == nullptr || (dtype != PLM_BF16 && dtype != PLM_F16)) return PLM_ERR_ARGUMENT;
+  if (N < 1 || K < 8 || K % 8 != 0 || ldw < K || N > (int64_t(1) << 30) || K > (int64_t(1) << 30))
+    return PLM_ERR_ARGUMENT;
+  if (ldw % 8 != 0 || (reinterpret_cast<uintptr_t>(w) & 15) != 0 || (reinterpret_cast<uintptr_t>(packed) & 15) != 0)
+    return PLM_ERR_ALIGNMENT;
+  const int64_t bytes = plm::packed_bytes(N, K);
+  if (static_cast<int64_t>(packed_bytes) < bytes) return PLM_ERR_ARGUMENT;
+  const int64_t lanes = bytes / 16;
+  const int64_t blocks = std::min<int64_t>((lanes + 255) / 256, 65536);
+  hipLaunchKernelGGL(plm::unpack_weight_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const plm::u32x4*>(packed), static_cast<int>(N),
+                     static_cast<int>(K), static_cast<int>(plm::ksteps(K)), lanes, static_cast<uint16_t*>(w), ldw);
+  return hipGetLastError() == hipSuccess ? PLM_OK : PLM_ERR_LAUNCH;
+}
+
 size_t plm_gemm_packed_workspace_bytes(int64_t M, int64_t N, int64_t K, const plm_tile* tile) {
   (void)K;
   if (!plm::packed_tile_valid(tile) || M < 1 || N < 1) return 0;
-  return static_cast<size_t>(plm::packed_workspace(M, N, *tile));
+  return static_cast<size_t>(plm::packed_workspace(std::min(M, plm::kPackedMaxM), N, *tile));
 }
 
 int plm_gemm_packed_tile_supported(int32_t dtype, int64_t M, int64_t K, const plm_tile* tile) {
-  if (!plm::packed_tile_valid(tile) || M < 1 || M > plm::kPackedMaxM || K < 8) return 0;
-  plm::PackedArgs a{};
-  a.M = static_cast<int>(M);
-  return plm::packed_dispatch_dt(dtype, a, *tile, 1, nullptr, true) == hipSuccess ? 1 : 0;
+  if (!plm::packed_tile_valid(tile) || M < 1 || K < 8) return 0;
+  for (const int64_t rows : {std::min(M, plm::kPackedMaxM), M > plm::kPackedMaxM ? M % plm::kPackedMaxM : 0}) {
+    if (rows == 0) continue;
+    plm::PackedArgs a{};
+    a.M = static_cast<int>(rows);
+    if (plm::packed_dispatch_dt(dtype, a, *tile, 1, nullptr, true) != hipSuccess) return 0;
+  }
+  return 1;
 }
 
 int plm_gemm_packed(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy, int64_t M,
                     int64_t N, int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream) {
-  return plm::packed_entry(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, 0);
+  return plm::packed_rows(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, 0);
 }
 
 int plm_gemm_packed_f32out(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, float* y, int64_t ldy,
                            int64_t M, int64_t N, int64_t K, const plm_tile* tile, void* workspace,
                            size_t workspace_bytes, void* stream) {
-  return plm::packed_entry(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, 1);
+  return plm::packed_rows(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, 1);
 }
 
 int plm_gemm_packed_resident_workgroups(int32_t dtype, int64_t M, const plm_tile* tile) {

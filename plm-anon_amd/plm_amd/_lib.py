@@ -37,6 +37,7 @@ EXPORTS = (
     "plm_gemm_tile_supported",
     "plm_packed_weight_bytes",
     "plm_pack_weight",
+    "plm_unpack_weight",
     "plm_gemm_packed",
     "plm_gemm_packed_f32out",
     "plm_gemm_packed_noalloc",
@@ -111,6 +112,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.plm_packed_weight_bytes.restype = c_sz
     lib.plm_pack_weight.argtypes = [c_i32, c_p, c_i64, c_i64, c_i64, c_p, c_sz, c_p]
     lib.plm_pack_weight.restype = ctypes.c_int
+    lib.plm_unpack_weight.argtypes = [c_i32, c_p, c_sz, c_i64, c_i64, c_p, c_i64, c_p]
+    lib.plm_unpack_weight.restype = ctypes.c_int
     lib.plm_gemm_packed.argtypes = [c_i32, c_p, c_i64, c_p, c_p, c_i64, c_i64, c_i64, c_i64, tile_p, c_p, c_sz, c_p]
     lib.plm_gemm_packed.restype = ctypes.c_int
     lib.plm_gemm_packed_f32out.argtypes = lib.plm_gemm_packed.argtypes

@@ -18,7 +18,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .fast_gemm import Config, HALF_DTYPES, _tile, packed_weight, workspace
+from .fast_gemm import Config, HALF_DTYPES, _tile, packed_weight, row_major_weight, workspace
 
 
 @dataclass
@@ -61,7 +61,7 @@ class LinearChain:
             if ln.y.dtype not in (self.dtype, torch.float32):
                 raise TypeError(f"link {i}: y must be {self.dtype} or float32")
             g = arr[i]
-            g.x, g.w, g.y = ln.x.data_ptr(), (packed_weight(ln.w) if packed else ln.w).data_ptr(), ln.y.data_ptr()
+            g.x, g.w, g.y = ln.x.data_ptr(), (packed_weight(ln.w) if packed else row_major_weight(ln.w)).data_ptr(), ln.y.data_ptr()
             g.ldx, g.ldw, g.ldy = ln.x.stride(0), ln.w.stride(0), ln.y.stride(0)
             g.N, g.K = ln.w.shape[0], ln.w.shape[1]
             g.split_k, g.dep = ln.split_k, ln.dep

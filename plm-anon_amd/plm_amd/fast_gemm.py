@@ -9,6 +9,12 @@ reproducible run to run (plm/fast_gemm.py:3-4). ``install`` routes eligible call
 kernel: the build's own dispatch slot always, and vLLM's ``default_unquantized_gemm`` when vLLM is
 importable (plm/fast_gemm.py:100-113). Tile configs are keyed on ``(M, N, K)``; shapes without a
 config go to ``F.linear``, exactly as in the reference.
+
+``release(weight)`` keeps one copy of a weight: its row-major storage is freed and every product with
+it runs on the packed copy: widths up to 128 rows (the round widths, on their tuned tiles, or
+``default_config``'s) on the packed kernel; wider calls (prefill chunks, plm/rounds.py:16, which the
+reference hands to ``F.linear``) as ``F.linear`` on the weight unpacked into a transient buffer
+(``unpacked``), so they are the reference's own prefill products bit for bit.
 """
 
 from __future__ import annotations
@@ -33,6 +39,8 @@ _tiles: dict[tuple[int, int, int, int], _lib.Tile] = {}
 # weight tensor -> ((data_ptr, shape, row stride, version counter), packed copy); entries go with
 # the tensor
 _packed = WeakTensorKeyDictionary()
+# released weight tensor -> its packed copy (the tensor itself then holds no data)
+_released = WeakTensorKeyDictionary()
 _pack_lock = threading.Lock()
 _workspaces: dict[int, torch.Tensor] = {}
 _ws_lock = threading.Lock()
@@ -94,7 +102,10 @@ def pack_weight(w: torch.Tensor) -> torch.Tensor:
 
 def packed_weight(w: torch.Tensor) -> torch.Tensor:
     """The packed copy of ``w``, made on first use and reused while ``w`` lives unchanged (same
-    storage, shape, stride and version counter)."""
+    storage, shape, stride and version counter); for a released weight, the copy it keeps."""
+    released = _released.get(w)
+    if released is not None:
+        return released
     key = (w.data_ptr(), tuple(w.shape), w.stride(0), w._version)
     hit = _packed.get(w)
     if hit is not None and hit[0] == key:
@@ -106,6 +117,71 @@ def packed_weight(w: torch.Tensor) -> torch.Tensor:
         p = pack_weight(w)
         _packed[w] = (key, p)
         return p
+
+
+def release(w: torch.Tensor) -> torch.Tensor:
+    """Keep one copy of ``w``: pack it (if not yet) and free its row-major storage. ``w`` keeps its
+    shape, dtype and device, but holds no data any more (a one-element view expanded to its shape):
+    afterwards only the packed kernels may read it (``hip_linear``, ``fast_gemm`` at every width,
+    the packed verify and chain); the row-major paths raise. The storage is returned to the caching
+    allocator once nothing else refers to it. Returns ``w``."""
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("release() packs and frees memory, which cannot happen during graph capture")
+    if w in _released:
+        return w
+    p = packed_weight(w)
+    with _pack_lock:
+        N, K = w.shape
+        w.data = torch.empty(1, dtype=w.dtype, device=w.device).expand(N, K)
+        _released[w] = p
+        _packed.pop(w, None)
+    return w
+
+
+def is_released(w: torch.Tensor) -> bool:
+    """Whether ``w``'s row-major data was freed by ``release``."""
+    return w in _released
+
+
+def unpack_weight(p: torch.Tensor, N: int, K: int, dtype: torch.dtype) -> torch.Tensor:
+    """The row-major ``[N, K]`` weight rebuilt from its packed copy ``p`` (``plm_unpack_weight``), bit
+    for bit: a new tensor on ``p``'s device."""
+    out = torch.empty(N, K, dtype=dtype, device=p.device)
+    status = _lib.lib().plm_unpack_weight(_lib.DTYPE_CODES[dtype], p.data_ptr(), p.numel(), N, K, out.data_ptr(), K,
+                                          _lib.stream_handle(p.device))
+    _lib.check(status, f"plm_unpack_weight(N={N}, K={K})")
+    return out
+
+
+def unpacked(w: torch.Tensor) -> torch.Tensor:
+    """A transient row-major copy of a released weight, rebuilt from the packed copy it keeps."""
+    p = _released.get(w)
+    if p is None:
+        raise ValueError("unpacked() takes a released weight")
+    return unpack_weight(p, w.shape[0], w.shape[1], w.dtype)
+
+
+def row_major_weight(w: torch.Tensor) -> torch.Tensor:
+    """``w`` for a kernel that reads it row-major; raises for a released weight."""
+    if w in _released:
+        raise RuntimeError(f"weight {tuple(w.shape)} was released (only its packed copy exists); "
+                           "use the packed kernels")
+    return w
+
+
+def default_config(M: int, N: int, K: int) -> Config:
+    """The tile for a width the tables do not tune: round widths (M <= 128) take
+    ``tiles.heuristic_tile``; wider calls (prefill chunks) run as 128-row slices on the row-split
+    layout, whose workgroup shares each X fragment among its four wavefronts (the K-split layouts
+    load all eight X fragments per weight fragment pair), with K split until about every compute
+    unit has an item (at least 256 of K per split)."""
+    from .tiles import CU_COUNT, heuristic_tile
+
+    if M <= 128:
+        return heuristic_tile(M, N, K, supported=lambda cfg: tile_supported(M, K, cfg))
+    tiles_ = -(-N // 128)  # 64 * wave_frags rows per tile
+    split = max(1, min(16, round(CU_COUNT / tiles_), K // 256))
+    return {"wave_frags": 2, "k_waves": 1, "split_k": split, "unroll": 4}
 
 
 def reserve_workspace(device: torch.device, shapes: dict[tuple[int, int, int], Config] | None = None) -> None:
@@ -151,6 +227,7 @@ def hip_linear_rowmajor(a: torch.Tensor, w: torch.Tensor, cfg: Config, out: torc
     """``a @ w.T`` on the streaming kernel that reads W row-major (``plm_gemm``; no packed copy).
     Its tiles: ``64*wave_frags`` rows, ``unroll`` = 2 (``tiles.stream_compiled``)."""
     _check_operands(a, w)
+    row_major_weight(w)
     M, K = a.shape
     N = w.shape[0]
     if out is None:
@@ -202,9 +279,40 @@ def hip_linear_f32(a: torch.Tensor, w: torch.Tensor, cfg: Config, out: torch.Ten
     return _launch(a, w, cfg, out, True)
 
 
+# Widths above this run as F.linear on the unpacked weight rather than as 128-row slices of the
+# packed kernel (faster from 256 rows on, measured on MI355X over the 1.3B block's linears).
+WIDE_ROWS = 128
+
+
+def released_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """``F.linear(x, weight, bias)`` for a released weight, any leading shape of ``x``: up to
+    ``WIDE_ROWS`` rows on the packed kernel (the tuned tile where the tables have one for
+    ``(M, N, K)``, else ``default_config``; a bias added after), wider as ``F.linear`` on the weight
+    unpacked into a transient buffer."""
+    if x.dtype != weight.dtype:
+        raise TypeError(f"released weight is {weight.dtype}, input is {x.dtype}")
+    N, K = weight.shape
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, K)
+    M = x2.shape[0]
+    if M > WIDE_ROWS:
+        return F.linear(x, unpacked(weight), bias)
+    if M == 0:
+        out = x2.new_empty(0, N)
+    else:
+        cfg = CONFIGS.get((M, N, K)) or default_config(M, N, K)
+        out = hip_linear(x2, weight, cfg)
+    if bias is not None:
+        out += bias
+    return out.reshape(*lead, N)
+
+
 def fast_gemm(layer, x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
     """vLLM ``default_unquantized_gemm`` signature; tuned 2-D half-precision calls without bias go to
-    the HIP kernel, everything else to ``F.linear`` (plm/fast_gemm.py:106-111)."""
+    the HIP kernel, everything else to ``F.linear`` (plm/fast_gemm.py:106-111). A released weight
+    has no row-major data: every call with it runs on its packed copy (``released_linear``)."""
+    if weight in _released:
+        return released_linear(x, weight, bias)
     if bias is None and x.dim() == 2 and x.dtype in HALF_DTYPES:
         cfg = CONFIGS.get((x.shape[0], weight.shape[0], weight.shape[1]))
         if cfg is not None:
@@ -213,6 +321,8 @@ def fast_gemm(layer, x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor |
 
 
 def _default_gemm(layer, x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    if weight in _released:
+        return released_linear(x, weight, bias)
     return F.linear(x, weight, bias)
 
 

@@ -14,7 +14,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .fast_gemm import HALF_DTYPES, Config, packed_weight, workspace
+from .fast_gemm import HALF_DTYPES, Config, packed_weight, row_major_weight, workspace
 
 ROUND_MODES = {"fp32": _lib.PLM_ROUND_F32, "bf16": _lib.PLM_ROUND_BF16, "fp16": _lib.PLM_ROUND_F16}
 RULES = {"nucleus": _lib.PLM_RULE_NUCLEUS, "floor": _lib.PLM_RULE_FLOOR}
@@ -67,7 +67,9 @@ def lm_head_verify(x: torch.Tensor, w: torch.Tensor, pending: torch.Tensor, p: f
     cfg = (VERIFY_CONFIG if packed else ROWMAJOR_VERIFY_CONFIG) if cfg is None else cfg
     tile = _lib.Tile.from_config(cfg)
     x = x if (x.stride(1) == 1 and x.stride(0) % 8 == 0) else x.contiguous()
-    w = w if (w.stride(1) == 1 and w.stride(0) % 8 == 0) else w.contiguous()
+    if not packed:  # the packed path reads packed_weight(w), which handles any layout of w itself
+        w = row_major_weight(w)
+        w = w if (w.stride(1) == 1 and w.stride(0) % 8 == 0) else w.contiguous()
     pending = pending.contiguous()
     # The kernel writes one byte 0/1 per row: a bool tensor's storage directly.
     direct = accept is not None and accept.dtype == torch.bool and accept.is_contiguous() and accept.shape == (R,)

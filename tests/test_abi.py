@@ -124,7 +124,16 @@ def test_packed_argument_validation_happens_before_launch():
     fake = 1 << 20
     # K not a multiple of 8; M out of range; misaligned X; unknown dtype.
     assert lib.plm_gemm_packed(0, fake, 1024, fake, fake, 4096, 42, 4096, 1020, tile, None, 0, None) == -1
-    assert lib.plm_gemm_packed(0, fake, 1024, fake, fake, 4096, 129, 4096, 1024, tile, None, 0, None) == -1
+    assert lib.plm_gemm_packed(0, fake, 1024, fake, fake, 4096, 0, 4096, 1024, tile, None, 0, None) == -1
+    # Wider than one launch: 128-row slices; a tile must have a kernel at both slice widths
+    # (eight fragments of X rows with four of weight rows is past the accumulator budget).
+    assert lib.plm_gemm_packed(0, fake, 1024, fake, fake, 4096, 640, 4096, 1024, _lib.Tile(4, 4, 1, 2), None, 0,
+                               None) == -3
+    assert lib.plm_gemm_packed_tile_supported(0, 129, 1024, _lib.Tile(2, 1, 1, 4)) == 1
+    assert lib.plm_gemm_packed_tile_supported(0, 129, 1024, _lib.Tile(4, 1, 1, 4)) == 0
+    assert lib.plm_gemm_packed_tile_supported(0, 16, 1024, _lib.Tile(4, 1, 1, 4)) == 1
+    assert lib.plm_gemm_packed_workspace_bytes(640, 4096, 1024, _lib.Tile(2, 1, 4, 4)) == \
+        lib.plm_gemm_packed_workspace_bytes(128, 4096, 1024, _lib.Tile(2, 1, 4, 4))
     assert lib.plm_gemm_packed(0, fake + 2, 1024, fake, fake, 4096, 42, 4096, 1024, tile, None, 0, None) == -2
     assert lib.plm_gemm_packed(7, fake, 1024, fake, fake, 4096, 42, 4096, 1024, tile, None, 0, None) == -1
     # Split-K without a workspace; a pipeline depth with no kernel.
@@ -188,6 +197,14 @@ def test_workspace_sizes():
     # Partial planes pad N to a multiple of 4 floats.
     assert lib.plm_gemm_workspace_bytes(42, 50257, 1024, _lib.Tile(2, 4, 2, 2)) == _lib.COUNTER_BYTES + (2 * 42 * 50260 + 63) // 64 * 64 * 4
     assert lib.plm_lm_head_verify_workspace_bytes(56, 50257, 2048, _lib.Tile(2, 4, 1, 4)) > 56 * 4
+
+
+def test_default_config_has_a_kernel_at_every_width():
+    for M in (1, 7, 33, 56, 64, 110, 128, 129, 200, 256, 640, 1000):
+        for N, K in ((2048, 2048), (6144, 2048), (8192, 2048), (2048, 8192), (50257, 2048), (1000, 1416)):
+            cfg = fast_gemm.default_config(M, N, K)
+            assert fast_gemm.tile_supported(M, K, cfg), (M, N, K, cfg)
+            assert cfg["split_k"] >= 1 and math.ceil(K / 32) // cfg["split_k"] >= 2
 
 
 def test_tile_support_matches_register_budget():
