@@ -51,7 +51,7 @@ def parse_args():
     ap.add_argument("--only-round", action="store_true", help="time the round only (for profiling runs)")
     ap.add_argument("--no-voronoi", action="store_true", help="skip the verify rows' auxiliary decode timing")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-width timing")
-    ap.add_argument("--profile", choices=("eager", "copy", "verify", "voronoi"),
+    ap.add_argument("--profile", choices=("eager", "copy", "verify", "voronoi", "lora"),
                     help="no JSON: 'eager' launches the round and the fused verify step --steps times without a "
                          "graph (for rocprofv3 counter runs); 'copy' runs a 1 GiB device copy, the reference "
                          "kernel that scales the HBM byte counters; 'verify' runs the fused verify step and the "
@@ -285,6 +285,9 @@ def main():
         return
     if args.profile == "voronoi":
         profile_voronoi(args, device)
+        return
+    if args.profile == "lora":
+        profile_lora(args, device)
         return
     tables = gemm_tables.read_table(args.hidden)
     gemms = [g for _ in range(args.layers) for g in gpt_block(args.hidden, args.mlp)]
@@ -618,6 +621,35 @@ def profile_verify(args, device):
         hip_linear(x, copies[i % 6], cfg)
     torch.cuda.synchronize()
     print(f"[bench] verify x {max(1, args.steps)}, LM-head GEMM {cfg} x {max(1, args.steps)}", file=sys.stderr)
+
+
+def profile_lora(args, device):
+    """The gated-LoRA linear on the Llama-style 1.3B fused QKV (one launch: h and the corrected base
+    GEMM) and the base GEMM alone, eager, rotating over 20 weight sets (252 MB)."""
+    import torch
+
+    from plm_amd import gemm_tables
+    from plm_amd.fast_gemm import hip_linear
+    from plm_amd.gated_lora import gated_linear, stack_b
+
+    M, K, shards, rank, gate = args.M, 2048, (2048, 512, 512), 16, 7
+    N = sum(shards)
+    cfg = gemm_tables.read_table(K)[(M, N, K)]
+    gen = torch.Generator(device=device).manual_seed(77)
+    x = torch.randn(M, K, generator=gen, device=device).bfloat16()
+    sets = []
+    for _ in range(20):
+        w = (0.02 * torch.randn(N, K, generator=gen, device=device)).bfloat16()
+        a = (0.05 * torch.randn(len(shards) * rank, K, generator=gen, device=device)).bfloat16()
+        bs = [(0.5 * torch.randn(n, rank, generator=gen, device=device)).bfloat16() for n in shards]
+        sets.append((w, a, bs, stack_b(bs)))
+    for i in range(max(1, args.steps)):
+        w, a, bs, b = sets[i % len(sets)]
+        gated_linear(x, w, a, bs, gate, cfg=cfg, lora_b=b)
+    for i in range(max(1, args.steps)):
+        hip_linear(x, sets[i % len(sets)][0], cfg)
+    torch.cuda.synchronize()
+    print(f"[bench] gated LoRA x {max(1, args.steps)}, base GEMM {cfg} x {max(1, args.steps)}", file=sys.stderr)
 
 
 def time_llama_rounds(args, device):

@@ -73,6 +73,23 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return buf
 
 
+def check_workspace(device: torch.device) -> None:
+    """Raises if a launch on ``device``'s workspace reported a bounded wait that gave up (the int at
+    ``PLM_WORKSPACE_ERROR_INDEX``: chained launches, the gated-LoRA launch, the fused verify), whose
+    results are then invalid; the counter area is zeroed first, so the workspace is usable again.
+    Synchronizes with the device: call it where the serving loop syncs anyway, with no launch on
+    the workspace in flight."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    buf = _workspaces.get(index)
+    if buf is None:
+        return
+    flag = int(buf[: 4 * (_lib.ERROR_INDEX + 1)].view(torch.int32)[_lib.ERROR_INDEX].item())
+    if flag:
+        buf[: _lib.COUNTER_BYTES].zero_()
+        raise RuntimeError(f"a launch on cuda:{index}'s workspace gave up a bounded wait (another process "
+                           "holding CUs?): its results are invalid; the counter area was reset")
+
+
 def gemm_workspace_bytes(M: int, N: int, K: int, cfg: Config) -> int:
     return int(_lib.lib().plm_gemm_packed_workspace_bytes(M, N, K, _tile(cfg)))
 

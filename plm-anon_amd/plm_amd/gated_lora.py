@@ -81,7 +81,9 @@ def gated_linear(x: torch.Tensor, weight: torch.Tensor, lora_a: torch.Tensor, lo
     ``lora_a`` is ``[shards*rank, K]``, ``lora_bs[s]`` is ``[N_s, rank]`` with ``sum N_s = N``;
     ``lora_b`` may carry them already stacked (``stack_b``). The HIP path runs when the call is
     eligible for the tuned GEMM (no bias, 2-D half-precision operands, a tile in ``cfg`` or
-    installed for ``(M, N, K)``, a rank the kernel takes); otherwise the reference's composition."""
+    installed for ``(M, N, K)``, a rank the kernel takes); otherwise the reference's composition.
+    The HIP path's workgroups wait on each other within the launch (bounded):
+    ``fast_gemm.check_workspace`` reports a wait that gave up."""
     M = x.shape[0]
     if first_gated_row is None or first_gated_row >= M:
         return dispatch_unquantized_gemm()(None, x, weight, bias)

@@ -162,3 +162,22 @@ def test_back_to_back_calls_and_smaller_width(device):
         x, w, a, bs, (xg, wg, ag, bsg) = _operands(M, shards, K, rank, seed, device)
         _check(gated_linear(xg, wg, ag, bsg, gate, cfg=cfg), oracle.gated_lora(x, w, a, bs, gate))
     assert _error_flag(device) == 0
+
+
+def test_check_workspace_reports_and_resets_the_error_flag(device):
+    """The error flag a timed-out wait sets, forced from the host (no kernel waits or faults):
+    check_workspace raises once and leaves a zeroed counter area, after which launches run clean."""
+    from plm_amd import _lib, fast_gemm
+
+    shards, K, rank, cfg = CASES["qkv"]
+    x, w, a, bs, (xg, wg, ag, bsg) = _operands(56, shards, K, rank, 51, device)
+    gated_linear(xg, wg, ag, bsg, 7, cfg=cfg)
+    torch.cuda.synchronize()
+    fast_gemm.check_workspace(device)   # clean
+    ws = fast_gemm.workspace(device, 1 << 20)
+    ws[4 * _lib.ERROR_INDEX: 4 * (_lib.ERROR_INDEX + 1)].view(torch.int32).fill_(1)
+    with pytest.raises(RuntimeError, match="gave up"):
+        fast_gemm.check_workspace(device)
+    assert int(ws[: _lib.COUNTER_BYTES].count_nonzero().item()) == 0
+    _check(gated_linear(xg, wg, ag, bsg, 7, cfg=cfg), oracle.gated_lora(x, w, a, bs, 7))
+    fast_gemm.check_workspace(device)
