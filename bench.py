@@ -790,7 +790,7 @@ def time_prefill(args, device, block_weights):
         out[str(M)] = line
         print(f"[bench] prefill M={M}: {line}", file=sys.stderr, flush=True)
     return dict(out, note="96 block linears of the headline round per graph; packed = plm_gemm_packed "
-                          "(128-row slices above 128 rows), unpacked_f_linear = plm_unpack_weight into a "
+                          "(its wide kernel above 128 rows), unpacked_f_linear = plm_unpack_weight into a "
                           "transient buffer + F.linear (a released weight's path above 128 rows), f_linear = "
                           "torch F.linear on a kept row-major weight")
 

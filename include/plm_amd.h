@@ -113,9 +113,9 @@ int plm_unpack_weight(int32_t dtype, const void* packed, size_t packed_bytes, in
  * partials summed in split order); unroll = K steps of loads in flight per wavefront (2, 4, 6,
  * 8). Requirements as plm_gemm (K % 8 == 0, K <= 2^24, ldx % 8 == 0, x 16-byte aligned) except
  * that M may exceed 128: wider calls (prefill chunks, plm/rounds.py:16, which the reference hands to
- * F.linear) run as consecutive 128-row slices of X and Y, one launch each, so the tile must have a
- * kernel at 128 rows and at the last slice's width (plm_gemm_packed_tile_supported checks both).
- * Workspace: plm_gemm_packed_workspace_bytes (one slice's; the slices share it).
+ * F.linear) run on a compute-oriented wide kernel (128 x 128 tiles staged through LDS, K split in
+ * fixed order for shapes with few tiles) whose tiling is its own: `tile` must be valid but is not
+ * used. Workspace: plm_gemm_packed_workspace_bytes.
  */
 int plm_gemm_packed(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy, int64_t M,
                     int64_t N, int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream);

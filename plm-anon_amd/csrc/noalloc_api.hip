@@ -59,7 +59,7 @@ extern "C" {
 
 int plm_gemm_packed_noalloc(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy,
                             int64_t M, int64_t N, int64_t K, const plm_tile* tile, void* stream) {
-  const int64_t need = plm::packed_gemm_workspace(M, N, tile);
+  const int64_t need = plm::packed_gemm_workspace(M, N, K, tile);
   if (need < 0)  // an invalid tile or size: the regular checks name it
     return plm::packed_gemm_call(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, nullptr, 0, stream, 0);
   if (static_cast<uint64_t>(need) > plm::kScratchBytes) return PLM_ERR_WORKSPACE;

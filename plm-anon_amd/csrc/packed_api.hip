@@ -7,6 +7,7 @@
 
 #include "packed_gemm.h"
 #include "plm_amd.h"
+#include "wide_gemm.h"
 
 namespace plm {
 
@@ -208,31 +209,31 @@ int packed_entry(int32_t dtype, const void* x, int64_t ldx, const void* wp, void
                             static_cast<hipStream_t>(stream));
 }
 
-// Widths past one launch's 128 rows (prefill chunks, plm/rounds.py:16): consecutive 128-row slices
-// of X and Y, one launch each on the same stream (each leaves the workspace's counters at zero, so
-// the slices share it). The tile must have a kernel at both slice widths; that and every argument
-// are checked before the first launch, so an invalid call writes nothing.
+// Widths past 128 rows (prefill chunks, plm/rounds.py:16, which the reference hands to F.linear)
+// run on the wide kernel (csrc/wide_gemm.hip: 128 x 128 tiles staged through LDS, K split for thin
+// shapes); the tile configuration applies to the skinny kernel only and is checked for validity.
+// Every argument is checked before the launch.
 int packed_rows(int32_t dtype, const void* x, int64_t ldx, const void* wp, void* y, int64_t ldy, int64_t M, int64_t N,
                 int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream, int out_f32) {
   if (M <= kPackedMaxM) return packed_entry(dtype, x, ldx, wp, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, out_f32);
   if (!packed_tile_valid(tile)) return PLM_ERR_TILE;
-  const int64_t rest = M % kPackedMaxM;
-  for (const int64_t rows : {kPackedMaxM, rest}) {
-    if (rows == 0) continue;
-    PackedArgs a{};
-    a.M = static_cast<int>(rows);
-    if (packed_dispatch_dt(dtype, a, *tile, 1, nullptr, true) != hipSuccess) return PLM_ERR_TILE;
-  }
-  if (ldy < N || (M - 1) * ldx + K > (int64_t(1) << 40)) return PLM_ERR_ARGUMENT;
-  const int64_t esize = out_f32 ? 4 : 2;
-  for (int64_t m0 = 0; m0 < M; m0 += kPackedMaxM) {
-    const int64_t rows = std::min(kPackedMaxM, M - m0);
-    const int status = packed_entry(dtype, static_cast<const char*>(x) + m0 * ldx * 2, ldx, wp,
-                                    static_cast<char*>(y) + m0 * ldy * esize, ldy, rows, N, K, tile, workspace,
-                                    workspace_bytes, stream, out_f32);
-    if (status != PLM_OK) return status;
-  }
-  return PLM_OK;
+  if (N < 1 || N > (int64_t(1) << 30) || K > (int64_t(1) << 30)) return PLM_ERR_ARGUMENT;
+  plm_chain_gemm g{};
+  g.x = x;
+  g.w = wp;
+  g.y = y;
+  g.ldx = ldx;
+  g.ldw = K;
+  g.ldy = ldy;
+  g.N = static_cast<int32_t>(N);
+  g.K = static_cast<int32_t>(K);
+  g.split_k = 1;
+  g.out_f32 = out_f32;
+  const int status = packed_check_linear(dtype, g, kPackedMaxM);  // the checks but the width's
+  if (status != PLM_OK) return status;
+  if (M > (int64_t(1) << 24) || M * ldx * 2 >= (int64_t(1) << 31)) return PLM_ERR_ARGUMENT;
+  return wide_gemm(dtype, x, ldx, wp, y, ldy, M, N, K, workspace, workspace_bytes, static_cast<hipStream_t>(stream),
+                   out_f32);
 }
 
 // How the linears of a chain wait for the ones they read: 0 (none reads another), 2 (every linear
@@ -315,9 +316,9 @@ int packed_gemm_call(int32_t dtype, const void* x, int64_t ldx, const void* pack
   return packed_rows(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, out_f32);
 }
 
-int64_t packed_gemm_workspace(int64_t M, int64_t N, const plm_tile* tile) {
-  if (!packed_tile_valid(tile) || M < 1 || N < 1) return -1;
-  return packed_workspace(std::min(M, kPackedMaxM), N, *tile);
+int64_t packed_gemm_workspace(int64_t M, int64_t N, int64_t K, const plm_tile* tile) {
+  if (!packed_tile_valid(tile) || M < 1 || N < 1 || K < 1) return -1;
+  return M > kPackedMaxM ? wide_workspace(M, N, K) : packed_workspace(M, N, *tile);
 }
 
 }  // namespace plm
@@ -364,20 +365,16 @@ int plm_unpack_weight(int32_t dtype, const void* packed, size_t packed_bytes, in
 }
 
 size_t plm_gemm_packed_workspace_bytes(int64_t M, int64_t N, int64_t K, const plm_tile* tile) {
-  (void)K;
-  if (!plm::packed_tile_valid(tile) || M < 1 || N < 1) return 0;
-  return static_cast<size_t>(plm::packed_workspace(std::min(M, plm::kPackedMaxM), N, *tile));
+  const int64_t n = plm::packed_gemm_workspace(M, N, K, tile);
+  return n < 0 ? 0 : static_cast<size_t>(n);
 }
 
 int plm_gemm_packed_tile_supported(int32_t dtype, int64_t M, int64_t K, const plm_tile* tile) {
   if (!plm::packed_tile_valid(tile) || M < 1 || K < 8) return 0;
-  for (const int64_t rows : {std::min(M, plm::kPackedMaxM), M > plm::kPackedMaxM ? M % plm::kPackedMaxM : 0}) {
-    if (rows == 0) continue;
-    plm::PackedArgs a{};
-    a.M = static_cast<int>(rows);
-    if (plm::packed_dispatch_dt(dtype, a, *tile, 1, nullptr, true) != hipSuccess) return 0;
-  }
-  return 1;
+  if (M > plm::kPackedMaxM) return dtype == PLM_BF16 || dtype == PLM_F16 ? 1 : 0;  // the wide kernel
+  plm::PackedArgs a{};
+  a.M = static_cast<int>(M);
+  return plm::packed_dispatch_dt(dtype, a, *tile, 1, nullptr, true) == hipSuccess ? 1 : 0;
 }
 
 int plm_gemm_packed(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy, int64_t M,

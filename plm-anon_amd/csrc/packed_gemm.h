@@ -1035,7 +1035,7 @@ hipError_t packed_dispatch_kw(PackedArgs& a, int nf, int d, int cus, hipStream_t
 int packed_gemm_call(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy, int64_t M,
                      int64_t N, int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream,
                      int out_f32);
-int64_t packed_gemm_workspace(int64_t M, int64_t N, const plm_tile* tile);
+int64_t packed_gemm_workspace(int64_t M, int64_t N, int64_t K, const plm_tile* tile);
 
 // One translation unit per (dtype, workgroup layout) so that they build in parallel.
 hipError_t packed_dispatch_bf16_k1(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);

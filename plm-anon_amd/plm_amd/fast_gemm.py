@@ -11,10 +11,11 @@ importable (plm/fast_gemm.py:100-113). Tile configs are keyed on ``(M, N, K)``; 
 config go to ``F.linear``, exactly as in the reference.
 
 ``release(weight)`` keeps one copy of a weight: its row-major storage is freed and every product with
-it runs on the packed copy: widths up to 128 rows (the round widths, on their tuned tiles, or
-``default_config``'s) on the packed kernel; wider calls (prefill chunks, plm/rounds.py:16, which the
+it runs from the packed copy: widths up to 128 rows (the round widths) on the packed kernel with
+their tuned tiles or ``default_config``'s; wider calls (prefill chunks, plm/rounds.py:16, which the
 reference hands to ``F.linear``) as ``F.linear`` on the weight unpacked into a transient buffer
-(``unpacked``), so they are the reference's own prefill products bit for bit.
+(``unpacked``, bit for bit), which measured faster than ``plm_gemm_packed``'s own wide kernel
+(1.3B block at M = 640: 134.5 against 190.7 µs), so they are the reference's own products.
 """
 
 from __future__ import annotations
@@ -188,17 +189,13 @@ def row_major_weight(w: torch.Tensor) -> torch.Tensor:
 
 def default_config(M: int, N: int, K: int) -> Config:
     """The tile for a width the tables do not tune: round widths (M <= 128) take
-    ``tiles.heuristic_tile``; wider calls (prefill chunks) run as 128-row slices on the row-split
-    layout, whose workgroup shares each X fragment among its four wavefronts (the K-split layouts
-    load all eight X fragments per weight fragment pair), with K split until about every compute
-    unit has an item (at least 256 of K per split)."""
-    from .tiles import CU_COUNT, heuristic_tile
+    ``tiles.heuristic_tile``; wider calls run on the wide kernel, which has its own fixed tiling
+    (any valid tile is accepted and not used)."""
+    from .tiles import heuristic_tile
 
     if M <= 128:
         return heuristic_tile(M, N, K, supported=lambda cfg: tile_supported(M, K, cfg))
-    tiles_ = -(-N // 128)  # 64 * wave_frags rows per tile
-    split = max(1, min(16, round(CU_COUNT / tiles_), K // 256))
-    return {"wave_frags": 2, "k_waves": 1, "split_k": split, "unroll": 4}
+    return {"wave_frags": 2, "k_waves": 8, "split_k": 1, "unroll": 2}  # unused: the wide kernel runs
 
 
 def reserve_workspace(device: torch.device, shapes: dict[tuple[int, int, int], Config] | None = None) -> None:
@@ -296,8 +293,8 @@ def hip_linear_f32(a: torch.Tensor, w: torch.Tensor, cfg: Config, out: torch.Ten
     return _launch(a, w, cfg, out, True)
 
 
-# Widths above this run as F.linear on the unpacked weight rather than as 128-row slices of the
-# packed kernel (faster from 256 rows on, measured on MI355X over the 1.3B block's linears).
+# Widths above this run as F.linear on the unpacked weight (plm_gemm_packed's wide kernel, which
+# takes them too, measured slower over the 1.3B block's linears from 256 rows on).
 WIDE_ROWS = 128
 
 

@@ -125,15 +125,16 @@ def test_packed_argument_validation_happens_before_launch():
     # K not a multiple of 8; M out of range; misaligned X; unknown dtype.
     assert lib.plm_gemm_packed(0, fake, 1024, fake, fake, 4096, 42, 4096, 1020, tile, None, 0, None) == -1
     assert lib.plm_gemm_packed(0, fake, 1024, fake, fake, 4096, 0, 4096, 1024, tile, None, 0, None) == -1
-    # Wider than one launch: 128-row slices; a tile must have a kernel at both slice widths
-    # (eight fragments of X rows with four of weight rows is past the accumulator budget).
-    assert lib.plm_gemm_packed(0, fake, 1024, fake, fake, 4096, 640, 4096, 1024, _lib.Tile(4, 4, 1, 2), None, 0,
+    # Wider than 128 rows: the wide kernel (its own tiling; the tile must still be a valid one).
+    # 4096 x 640 at K = 1024 is 160 tiles of 128 x 128, split twice in K: a workspace is needed.
+    assert lib.plm_gemm_packed(0, fake, 1024, fake, fake, 4096, 640, 4096, 1024, _lib.Tile(2, 4, 1, 3), None, 0,
                                None) == -3
-    assert lib.plm_gemm_packed_tile_supported(0, 129, 1024, _lib.Tile(2, 1, 1, 4)) == 1
-    assert lib.plm_gemm_packed_tile_supported(0, 129, 1024, _lib.Tile(4, 1, 1, 4)) == 0
+    assert lib.plm_gemm_packed(0, fake, 1024, fake, fake, 4096, 640, 4096, 1024, tile, None, 0, None) == -4
+    assert lib.plm_gemm_packed(0, fake + 2, 1024, fake, fake, 4096, 640, 4096, 1024, tile, None, 0, None) == -2
+    assert lib.plm_gemm_packed_tile_supported(0, 129, 1024, _lib.Tile(4, 1, 1, 4)) == 1
     assert lib.plm_gemm_packed_tile_supported(0, 16, 1024, _lib.Tile(4, 1, 1, 4)) == 1
-    assert lib.plm_gemm_packed_workspace_bytes(640, 4096, 1024, _lib.Tile(2, 1, 4, 4)) == \
-        lib.plm_gemm_packed_workspace_bytes(128, 4096, 1024, _lib.Tile(2, 1, 4, 4))
+    assert lib.plm_gemm_packed_workspace_bytes(640, 4096, 1024, tile) == _lib.COUNTER_BYTES + 160 * 2 * 64 * 1024
+    assert lib.plm_gemm_packed_workspace_bytes(640, 6144, 2048, tile) == 0   # 240 tiles: no split
     assert lib.plm_gemm_packed(0, fake + 2, 1024, fake, fake, 4096, 42, 4096, 1024, tile, None, 0, None) == -2
     assert lib.plm_gemm_packed(7, fake, 1024, fake, fake, 4096, 42, 4096, 1024, tile, None, 0, None) == -1
     # Split-K without a workspace; a pipeline depth with no kernel.

@@ -77,18 +77,19 @@ def test_unpack_restores_the_weight_bit_for_bit(device, N, K):
     assert torch.equal(fast_gemm.unpacked(w), original)
 
 
-def test_wide_calls_on_the_packed_kernel_in_slices(device):
-    """plm_gemm_packed above 128 rows (128-row slices, one launch each): the sampled columns match
-    the oracle and each slice equals the same rows computed alone."""
-    N, K = 2048, 2048
-    for M in (129, 300):
-        x, w = _inputs_on_gpu(M, N, K, 400 + M, device)
-        cfg = fast_gemm.default_config(M, N, K)
-        y = hip_linear(x, w, cfg)
-        check_cols(y, x, w, torch.randperm(N, generator=torch.Generator().manual_seed(M))[:256])
-        for m0 in range(0, M, 128):
-            rows = min(128, M - m0)
-            assert torch.equal(y[m0:m0 + rows], hip_linear(x[m0:m0 + rows].contiguous(), w, cfg))
+@pytest.mark.parametrize("M,N,K", [(129, 2048, 2048), (300, 6144, 2048), (640, 2048, 8192), (200, 1000, 1416),
+                                   (777, 50257, 512)])
+def test_wide_kernel(device, M, N, K):
+    """plm_gemm_packed above 128 rows (the wide kernel; K split where the shape has few tiles):
+    sampled columns match the oracle, the fp32 output rounds to the 16-bit one, and a second call
+    is bit-identical (splits are summed in a fixed order)."""
+    x, w = _inputs_on_gpu(M, N, K, 400 + M, device)
+    cfg = fast_gemm.default_config(M, N, K)
+    y = hip_linear(x, w, cfg)
+    check_cols(y, x, w, torch.randperm(N, generator=torch.Generator().manual_seed(M))[:256])
+    assert torch.equal(y, hip_linear(x, w, cfg))
+    y32 = fast_gemm.hip_linear_f32(x, w, cfg)
+    assert torch.equal(y32.bfloat16(), y)
 
 
 def test_released_linear_shapes_bias_and_routing(device):
