@@ -419,6 +419,7 @@ def main():
         if not args.no_llama:
             result["llama_rounds"] = time_llama_rounds(args, device)
             result["gated_lora"] = time_gated_lora(args, device)
+            result["gate_up_silu"] = time_gate_up_silu(args, device)
         if not args.no_prefill:
             result["prefill"] = time_prefill(args, device, weights[:-1])
     if args.cpu_seconds > 0:
@@ -748,6 +749,45 @@ def time_gated_lora(args, device):
         del graph
     print(f"[bench] gated LoRA qkv: {res}", file=sys.stderr, flush=True)
     return dict(res, shape=f"M={M} N={N} K={K} rank={rank} shards={list(shards)} gate={gate}")
+
+
+def time_gate_up_silu(args, device):
+    """The Llama-style 1.3B MLP's gate_up_proj (2048 -> 2 x 5632) and its SiLU-and-multiply: the
+    fused launch (gate_up_silu) against the projection alone and the projection followed by the
+    activation as separate launches (torch's silu and mul), graphs rotating enough weight copies
+    that each call streams its weight from HBM."""
+    import torch
+    import torch.nn.functional as F
+
+    from plm_amd import gemm_tables
+    from plm_amd.fast_gemm import gate_up_silu, hip_linear
+
+    M, K, I = args.M, 2048, 5632
+    N = 2 * I
+    cfg = gemm_tables.read_table(K)[(M, N, K)]
+    gen = torch.Generator(device=device).manual_seed(78)
+    x = torch.randn(M, K, generator=gen, device=device).bfloat16()
+    ws = [(0.02 * torch.randn(N, K, generator=gen, device=device)).bfloat16() for _ in range(8)]  # 8 x 46 MB
+
+    def separate(w):
+        y = hip_linear(x, w, cfg)
+        return F.silu(y[:, :I]) * y[:, I:]
+
+    res = {}
+    for name, fn in (("fused_us", lambda w: gate_up_silu(x, w, cfg)), ("gemm_then_act_us", separate),
+                     ("gemm_alone_us", lambda w: hip_linear(x, w, cfg))):
+        for w in ws:
+            fn(w)
+        torch.cuda.synchronize()
+        stream = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for w in ws:
+                fn(w)
+        res[name] = round(time_graph(graph, max(5, args.steps // 4), 2) * 1000.0 / len(ws), 2)
+        del graph
+    print(f"[bench] gate_up + SiLU-and-multiply: {res}", file=sys.stderr, flush=True)
+    return dict(res, shape=f"M={M} N={N} K={K}")
 
 
 def time_prefill(args, device, block_weights):

@@ -350,6 +350,23 @@ size_t plm_gemm_packed_lora_workspace_bytes(int64_t M, int64_t N, int64_t K, int
                                             int32_t shards, const plm_tile* tile);
 
 /*
+ * A fused gate/up projection followed by its activation, in one launch. Replaces two launches of
+ * the reference's Llama-style rounds: the gate_up_proj GEMM (plm/fast_gemm.py:104-110, or F.linear)
+ * and vLLM 0.26.0's SiluAndMul on its output (uv.lock:3123-3125; the rounds run with
+ * enforce_eager, plm/decoder.py:37, so its silu_and_mul kernel), with the same roundings:
+ *   Y[m, n] = round(round(silu(g)) * u),  g = round((X W^T)[m, n]),  u = round((X W^T)[m, N/2 + n])
+ * for 0 <= n < N/2, silu(g) = g / (1 + e^-g) in fp32, round() to the model dtype. `packed_w` is
+ * W[N, K] (gate rows 0..N/2-1, up rows N/2..N-1) packed with the two halves interleaved by 16-row
+ * fragment — fragment 2j = gate rows [16j, 16j+16), fragment 2j+1 = up rows [16j, 16j+16) — i.e.
+ * plm_pack_weight of the rows in that order. N a multiple of 32, tile.wave_frags 2 or 4, Y [M, N/2]
+ * with ldy % 4 == 0 and y 8-byte aligned; otherwise as plm_gemm_packed (M <= 128). Workspace as
+ * plm_gemm_packed_workspace_bytes(M, N, K, tile).
+ */
+int plm_gemm_packed_silu_mul(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy,
+                             int64_t M, int64_t N, int64_t K, const plm_tile* tile, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/*
  * The verify rows' auxiliary decode, logit-Voronoi scheme with the `iterate` engine
  * (LogitVoronoiAuxiliary.decode_unmasked, plm/auxiliary.py:67-75, over Voronoi.assign,
  * plm/iterate.py:322-342). A problem is one row of logits[n_problems, n_vocab] (bf16 or fp16,

@@ -39,5 +39,7 @@ from .plm_oracle import (  # noqa: F401
     linear_fp64,
     nucleus_acceptance,
     nucleus_margin,
+    silu_mul,
+    silu_mul_fp64,
     verify,
 )

@@ -55,6 +55,31 @@ def gated_lora(x: torch.Tensor, w: torch.Tensor, lora_a: torch.Tensor, lora_bs: 
     return output
 
 
+def silu_mul(y: torch.Tensor) -> torch.Tensor:
+    """The Llama-style MLP's activation on a fused gate/up projection's output ``y[..., 2I]``.
+
+    The rounds run the model through vLLM 0.26.0 (uv.lock:3123-3125) with ``enforce_eager=True``
+    (plm/decoder.py:37), so its ``SiluAndMul`` runs the ``silu_and_mul`` custom kernel: per element,
+    ``silu(g) = g / (1 + e^-g)`` computed in fp32 from the model-dtype gate ``g = y[..., :I]`` and
+    rounded to the model dtype, then multiplied by ``u = y[..., I:]`` in the model dtype (exact in
+    fp32, rounded once). Eager torch's ``F.silu(g) * u`` on model-dtype tensors rounds the same two
+    times, which is what this computes (on the CPU)."""
+    half = y.shape[-1] // 2
+    g, u = y[..., :half].cpu(), y[..., half:].cpu()
+    return (F.silu(g.float()).to(y.dtype).float() * u.float()).to(y.dtype)
+
+
+def silu_mul_fp64(y: torch.Tensor) -> np.ndarray:
+    """Independent numpy version of ``silu_mul``: ``g / (1 + e^-g)`` in fp64 rounded to the model
+    dtype, times ``u`` in fp64, rounded to the model dtype (the pin for ``silu_mul``: the two agree
+    except where the fp32 and fp64 silu round to neighbouring values)."""
+    half = y.shape[-1] // 2
+    yd = y.cpu().double().numpy()
+    g, u = yd[..., :half], yd[..., half:]
+    s = torch.from_numpy(g / (1.0 + np.exp(-g))).to(y.dtype).double().numpy()
+    return torch.from_numpy(s * u).to(y.dtype).double().numpy()
+
+
 def gated_lora_fp64(x: torch.Tensor, w: torch.Tensor, lora_a: torch.Tensor, lora_bs: list[torch.Tensor],
                     first_gated_row: int) -> np.ndarray:
     """Independent numpy version: the base and hidden products exact in fp64 and rounded to the model

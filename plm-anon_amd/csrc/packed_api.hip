@@ -71,43 +71,26 @@ bool packed_tile_valid(const plm_tile* t) {
          (t->unroll == 2 || t->unroll == 4 || t->unroll == 6 || t->unroll == 8);
 }
 
+// The compiled kernels of one (epilogue, dtype, workgroup layout), per translation unit.
+using PackedDispatch = hipError_t (*)(PackedArgs&, int, int, int, hipStream_t, bool);
+
 hipError_t packed_dispatch_dt(int32_t dtype, PackedArgs& a, const plm_tile& t, int cus, hipStream_t s, bool dry,
-                              bool lora = false) {
-  const int nf = t.wave_frags, d = t.unroll;
-  if (lora) {
-    if (dtype == PLM_BF16) {
-      switch (t.k_waves) {
-        case 1: return packed_dispatch_lora_bf16_k1(a, nf, d, cus, s, dry);
-        case 4: return packed_dispatch_lora_bf16_k4(a, nf, d, cus, s, dry);
-        case 8: return packed_dispatch_lora_bf16_k8(a, nf, d, cus, s, dry);
-        case 16: return packed_dispatch_lora_bf16_k16(a, nf, d, cus, s, dry);
-      }
-    } else if (dtype == PLM_F16) {
-      switch (t.k_waves) {
-        case 1: return packed_dispatch_lora_f16_k1(a, nf, d, cus, s, dry);
-        case 4: return packed_dispatch_lora_f16_k4(a, nf, d, cus, s, dry);
-        case 8: return packed_dispatch_lora_f16_k8(a, nf, d, cus, s, dry);
-        case 16: return packed_dispatch_lora_f16_k16(a, nf, d, cus, s, dry);
-      }
-    }
-    return hipErrorInvalidConfiguration;
-  }
-  if (dtype == PLM_BF16) {
-    switch (t.k_waves) {
-      case 1: return packed_dispatch_bf16_k1(a, nf, d, cus, s, dry);
-      case 4: return packed_dispatch_bf16_k4(a, nf, d, cus, s, dry);
-      case 8: return packed_dispatch_bf16_k8(a, nf, d, cus, s, dry);
-      case 16: return packed_dispatch_bf16_k16(a, nf, d, cus, s, dry);
-    }
-  } else if (dtype == PLM_F16) {
-    switch (t.k_waves) {
-      case 1: return packed_dispatch_f16_k1(a, nf, d, cus, s, dry);
-      case 4: return packed_dispatch_f16_k4(a, nf, d, cus, s, dry);
-      case 8: return packed_dispatch_f16_k8(a, nf, d, cus, s, dry);
-      case 16: return packed_dispatch_f16_k16(a, nf, d, cus, s, dry);
-    }
-  }
-  return hipErrorInvalidConfiguration;
+                              int epi = kEpiPlain) {
+  static const PackedDispatch table[3][2][4] = {
+      {{packed_dispatch_bf16_k1, packed_dispatch_bf16_k4, packed_dispatch_bf16_k8, packed_dispatch_bf16_k16},
+       {packed_dispatch_f16_k1, packed_dispatch_f16_k4, packed_dispatch_f16_k8, packed_dispatch_f16_k16}},
+      {{packed_dispatch_lora_bf16_k1, packed_dispatch_lora_bf16_k4, packed_dispatch_lora_bf16_k8,
+        packed_dispatch_lora_bf16_k16},
+       {packed_dispatch_lora_f16_k1, packed_dispatch_lora_f16_k4, packed_dispatch_lora_f16_k8,
+        packed_dispatch_lora_f16_k16}},
+      {{packed_dispatch_act_bf16_k1, packed_dispatch_act_bf16_k4, packed_dispatch_act_bf16_k8,
+        packed_dispatch_act_bf16_k16},
+       {packed_dispatch_act_f16_k1, packed_dispatch_act_f16_k4, packed_dispatch_act_f16_k8,
+        packed_dispatch_act_f16_k16}}};
+  const int di = dtype == PLM_BF16 ? 0 : (dtype == PLM_F16 ? 1 : -1);
+  const int ki = t.k_waves == 1 ? 0 : t.k_waves == 4 ? 1 : t.k_waves == 8 ? 2 : t.k_waves == 16 ? 3 : -1;
+  if (di < 0 || ki < 0 || epi < kEpiPlain || epi > kEpiAct) return hipErrorInvalidConfiguration;
+  return table[epi][di][ki](a, t.wave_frags, t.unroll, cus, s, dry);
 }
 
 // Weight fragments (16 rows each) of one workgroup tile.
@@ -165,7 +148,7 @@ int packed_check_linear(int32_t dtype, const plm_chain_gemm& g, int64_t M) {
 }
 
 int packed_launch_args(int32_t dtype, PackedArgs& a, const plm_tile& t, void* workspace, size_t workspace_bytes,
-                       int64_t need, hipStream_t s, bool lora = false) {
+                       int64_t need, hipStream_t s, int epi = kEpiPlain) {
   if (need > 0 && (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < need ||
                    (reinterpret_cast<uintptr_t>(workspace) & 15) != 0))
     return PLM_ERR_WORKSPACE;
@@ -174,8 +157,8 @@ int packed_launch_args(int32_t dtype, PackedArgs& a, const plm_tile& t, void* wo
   a.counters = need > 0 ? static_cast<int*>(workspace) : nullptr;
   a.partial = need > 0 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes) : nullptr;
   a.spin_limit = kPackedSpinLimit;
-  if (packed_dispatch_dt(dtype, a, t, cus, s, true, lora) != hipSuccess) return PLM_ERR_TILE;
-  return packed_dispatch_dt(dtype, a, t, cus, s, false, lora) == hipSuccess ? PLM_OK : PLM_ERR_LAUNCH;
+  if (packed_dispatch_dt(dtype, a, t, cus, s, true, epi) != hipSuccess) return PLM_ERR_TILE;
+  return packed_dispatch_dt(dtype, a, t, cus, s, false, epi) == hipSuccess ? PLM_OK : PLM_ERR_LAUNCH;
 }
 
 int packed_entry(int32_t dtype, const void* x, int64_t ldx, const void* wp, void* y, int64_t ldy, int64_t M, int64_t N,
@@ -544,7 +527,44 @@ int plm_gemm_packed_lora(int32_t dtype, const void* x, int64_t ldx, const void* 
   a.sync = 0;
   a.lora = z;
   return plm::packed_launch_args(dtype, a, t, workspace, workspace_bytes, l.bytes, static_cast<hipStream_t>(stream),
-                                 true);
+                                 plm::kEpiLora);
+}
+
+int plm_gemm_packed_silu_mul(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy,
+                             int64_t M, int64_t N, int64_t K, const plm_tile* tile, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  if (!plm::packed_tile_valid(tile)) return PLM_ERR_TILE;
+  const plm_tile& t = *tile;
+  // Gate and up fragments pair up inside a wavefront's or a tile's fragments, and the output's
+  // 16-column blocks are whole.
+  if (t.wave_frags % 2 != 0 || N < 32 || N % 32 != 0 || N > (int64_t(1) << 30) || K > (int64_t(1) << 30))
+    return PLM_ERR_ARGUMENT;
+  if (ldy < N / 2 || ldy % 4 != 0) return PLM_ERR_ARGUMENT;
+  if ((reinterpret_cast<uintptr_t>(y) & 7) != 0) return PLM_ERR_ALIGNMENT;
+  plm_chain_gemm g{};
+  g.x = x;
+  g.w = packed_w;
+  g.y = y;
+  g.ldx = ldx;
+  g.ldw = K;
+  g.ldy = N;  // the checks below see the projection's N; the output's row stride is ldy
+  g.N = static_cast<int32_t>(N);
+  g.K = static_cast<int32_t>(K);
+  g.split_k = t.split_k;
+  g.dep = -1;
+  int status = plm::packed_check_linear(dtype, g, M);
+  if (status != PLM_OK) return status;
+  g.ldy = ldy;
+  const int64_t tiles = plm::packed_tiles(N, t);
+  if (t.split_k > 1 && tiles > plm::kPackedBarrierBase - plm::kPackedArriveBase) return PLM_ERR_ARGUMENT;
+  g.arrive_base = plm::kPackedArriveBase;
+  plm::PackedArgs a{};
+  a.single = g;
+  a.count = 1;
+  a.M = static_cast<int>(M);
+  a.G = static_cast<int>(tiles * t.split_k);
+  return plm::packed_launch_args(dtype, a, t, workspace, workspace_bytes, plm::packed_workspace(M, N, t),
+                                 static_cast<hipStream_t>(stream), plm::kEpiAct);
 }
 
 }  // extern "C"

@@ -1,6 +1,6 @@
 // f16 instantiations of the packed-weight GEMM with workgroup layout KW = 16
 // (K split across 16 wavefronts); one translation unit per (dtype, layout) so that they build in
-// parallel. Each also holds the layout's gated-LoRA launches.
+// parallel. Each also holds the layout's gated-LoRA and SiLU-and-multiply launches.
 #include "packed_gemm.h"
 
 namespace plm {
@@ -10,7 +10,11 @@ hipError_t packed_dispatch_f16_k16(PackedArgs& a, int nf, int d, int cus, hipStr
 }
 
 hipError_t packed_dispatch_lora_f16_k16(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry) {
-  return packed_dispatch_kw<DT_F16, 16, true>(a, nf, d, cus, s, dry);
+  return packed_dispatch_kw<DT_F16, 16, kEpiLora>(a, nf, d, cus, s, dry);
+}
+
+hipError_t packed_dispatch_act_f16_k16(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry) {
+  return packed_dispatch_kw<DT_F16, 16, kEpiAct>(a, nf, d, cus, s, dry);
 }
 
 }  // namespace plm

@@ -74,6 +74,11 @@ constexpr int kPkLoraPast = 13;    // gated-LoRA launch: base tiles past their w
 // m >= gated_from as round(round(acc) + sum_j h[m, s*rank + j] * B[n, j]), s the shard of column
 // n: the reference's base output and one addmm_ per shard. The last base tile to pass its wait
 // resets both counters for the next launch.
+// Store epilogues of packed_gemm_kernel (its EPI template parameter).
+constexpr int kEpiPlain = 0;  // Y = X W^T
+constexpr int kEpiLora = 1;   // the gated-LoRA launch (PackedLora)
+constexpr int kEpiAct = 2;    // a fused gate/up projection's SiLU-and-multiply (act_store)
+
 struct PackedLora {
   plm_chain_gemm pre;   // the h linear (y = h, ldy = its row stride)
   const uint16_t* b;    // [N][rank], the shards' up-projections stacked by output column
@@ -95,7 +100,7 @@ struct PackedArgs {
   int spin_limit;  // polls before a wait gives up
   int* counters;
   float* partial;
-  PackedLora lora;  // packed_gemm_kernel<..., LORA = true> only
+  PackedLora lora;  // packed_gemm_kernel<..., EPI = kEpiLora> only
 };
 
 __device__ __forceinline__ int sgpr(int v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -146,10 +151,10 @@ __device__ __forceinline__ T const_load(const T* p) {
 
 // A linear's descriptor: a chain's from its table, a single linear's from the kernel arguments
 // (a gated-LoRA launch: linear 0 is the h linear, linear 1 the base).
-template <int NF, int KW, bool LORA = false>
+template <int NF, int KW, int EPI = kEpiPlain>
 __device__ __forceinline__ PLinear load_linear(const PackedArgs& a, int gi, int64_t epoch = 0) {
   plm_chain_gemm g = a.single;
-  if constexpr (LORA) {
+  if constexpr (EPI == kEpiLora) {
     if (gi == 0) g = a.lora.pre;
   } else if (a.chain != nullptr) {
     const plm_chain_gemm* c = a.chain + gi;
@@ -189,15 +194,15 @@ __device__ __forceinline__ PLinear load_linear(const PackedArgs& a, int gi, int6
                ? reinterpret_cast<int64_t*>(a.counters + kPackedBarrierBase) + (L.seq & 1) * kPkTileFlags
                : nullptr;
   L.flag_value = ((epoch + 1) << 16) + L.seq;
-  L.role = LORA ? (gi == 0 ? 1 : 2) : 0;
+  L.role = EPI == kEpiLora ? (gi == 0 ? 1 : 2) : 0;
   return L;
 }
 
 // The first item of linear gi this workgroup takes (then every G-th): the gated-LoRA launch gives
 // the h linear's items to workgroups 0, 1, ... and starts the base linear's after them.
-template <bool LORA>
+template <int EPI>
 __device__ __forceinline__ int first_item(const PackedArgs& a, int gi) {
-  if constexpr (LORA) {
+  if constexpr (EPI == kEpiLora) {
     if (gi == 1) return sgpr((static_cast<int>(blockIdx.x) + a.G - a.lora.h_items % a.G) % a.G);
   }
   return static_cast<int>(blockIdx.x);
@@ -443,14 +448,14 @@ __device__ __forceinline__ f32x4 lora_correct(const PackedLora& z, int N, int M,
 
 // Fragment q = f*MT + t of a tile, as lane `lane` holds it: rows n0 + 16f + 4*(lane/16) + r
 // (r = 0..3) of column m = 16t + lane%16.
-template <int DT, int MT, bool LORA>
+template <int DT, int MT, int EPI>
 __device__ __forceinline__ void packed_store_frag(const PackedArgs& a, const PLinear& L, int M, int n0, int q, int lane,
                                                   f32x4 v) {
   const int f = q / MT, t = q - f * MT;
   const int m = 16 * t + (lane & 15);
   const int n = n0 + 16 * f + 4 * (lane >> 4);
   if (m >= M || n >= L.N) return;
-  if constexpr (LORA) {
+  if constexpr (EPI == kEpiLora) {
     if (L.role == 2 && m >= a.lora.gated_from) v = lora_correct<DT>(a.lora, L.N, M, m, n, v);
   }
   packed_store4<DT>(L, m, n, v);
@@ -459,9 +464,9 @@ __device__ __forceinline__ void packed_store_frag(const PackedArgs& a, const PLi
 // A tile's Y is stored: raises its tile-done flag (sync == 2), or in a gated-LoRA launch counts an
 // h tile in (once every wavefront's stores of it have completed), or counts a base tile past its
 // wait for h; the last base tile of the launch resets both counters for the next launch.
-template <bool LORA>
+template <int EPI>
 __device__ __forceinline__ void tile_done(const PackedArgs& a, const PLinear& L, int tile) {
-  if constexpr (LORA) {
+  if constexpr (EPI == kEpiLora) {
     if (L.role == 1) __builtin_amdgcn_s_waitcnt(0);
     asm volatile("s_barrier" ::: "memory");
     if (threadIdx.x == 0) {
@@ -478,16 +483,118 @@ __device__ __forceinline__ void tile_done(const PackedArgs& a, const PLinear& L,
   }
 }
 
+// SiLU-and-multiply epilogue (kEpiAct) of a fused gate/up projection packed with its gate and up
+// rows interleaved by fragment: fragment 2j holds gate rows [16j, 16j+16) and fragment 2j+1 the
+// up rows [16j, 16j+16) of the same output columns. Column block `cblk` (16 columns of the [M, N/2]
+// output) of X row 16t + lane%16, columns 16*cblk + 4*(lane/16) + r: the gate and up values rounded
+// to the model dtype (the projection's output), then vLLM's SiluAndMul on them (its silu_and_mul
+// kernel, which the rounds run with enforce_eager): silu(g) = g / (1 + e^-g) in fp32 rounded to the
+// model dtype, times u, rounded again (the product of two 16-bit values is exact in fp32).
+template <int DT, int MT>
+__device__ __forceinline__ void act_store(const PLinear& L, int M, int cblk, int t, int lane, f32x4 g, f32x4 u) {
+  const int m = 16 * t + (lane & 15);
+  const int n = 16 * cblk + 4 * (lane >> 4);
+  if (m >= M || n >= (L.N >> 1)) return;  // N/2 is a multiple of 16: all four columns are in range
+  uint16_t h[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float gr = from_bits16<DT>(to_bits16<DT>(g[r])), ur = from_bits16<DT>(to_bits16<DT>(u[r]));
+    h[r] = to_bits16<DT>(from_bits16<DT>(to_bits16<DT>(gr / (1.0f + expf(-gr)))) * ur);
+  }
+  uint16_t* y = static_cast<uint16_t*>(L.y) + static_cast<int64_t>(m) * L.ldy + n;
+  *reinterpret_cast<uint64_t*>(y) = (static_cast<uint64_t>(h[0]) | (static_cast<uint64_t>(h[1]) << 16)) |
+                                    ((static_cast<uint64_t>(h[2]) | (static_cast<uint64_t>(h[3]) << 16)) << 32);
+}
+
+// kEpiAct end of an item for a K-split workgroup (the wavefronts' tiles already in LDS): each
+// wavefront takes fragment pairs (gate, up) of the tile, sums both over the KW wavefronts, and
+// stores the activation, or with split > 1 writes the two partials; the last split to arrive sums
+// each pair's partials in split order and stores the activation.
+template <int DT, int MT, int NF, int KW>
+__device__ __forceinline__ void packed_finish_act(const PackedArgs& a, const PLinear& L, int M, int tile, int s,
+                                                  int wave, int lane, const f32x4* red, int* last_flag) {
+  constexpr int Q = NF * MT, QP = Q / 2, I = (QP + KW - 1) / KW;
+  f32x4 g[I], u[I];
+#pragma unroll
+  for (int i = 0; i < I; ++i) {
+    const int p = wave + KW * i;
+    if (p < QP) {
+      const int j = p / MT, t = p - j * MT, qg = 2 * j * MT + t, qu = qg + MT;
+      f32x4 vg = red[qg * 64 + lane], vu = red[qu * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < KW; ++w) {
+        vg += red[(w * Q + qg) * 64 + lane];
+        vu += red[(w * Q + qu) * 64 + lane];
+      }
+      g[i] = vg;
+      u[i] = vu;
+    }
+  }
+  lds_sync();  // every wavefront has read the tiles; LDS is free for the next item
+  if (L.split == 1) {
+#pragma unroll
+    for (int i = 0; i < I; ++i) {
+      const int p = wave + KW * i;
+      if (p < QP) {
+        const int j = p / MT, t = p - j * MT;
+        act_store<DT, MT>(L, M, tile * (NF / 2) + j, t, lane, g[i], u[i]);
+      }
+    }
+    tile_done<kEpiAct>(a, L, tile);
+    return;
+  }
+  const uint32_t tile_bytes = static_cast<uint32_t>(L.split) * Q * kFragBytes;
+  const auto prs = make_rsrc(L.partial + static_cast<int64_t>(tile) * L.split * Q * 256, tile_bytes);
+#pragma unroll
+  for (int i = 0; i < I; ++i) {
+    const int p = wave + KW * i;
+    if (p < QP) {
+      const int j = p / MT, t = p - j * MT, qg = 2 * j * MT + t, qu = qg + MT;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, g[i]), prs,
+                                             static_cast<uint32_t>((s * Q + qg) * kFragBytes + lane * 16), 0, kCoherent);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, u[i]), prs,
+                                             static_cast<uint32_t>((s * Q + qu) * kFragBytes + lane * 16), 0, kCoherent);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this wavefront's partials are written through
+  lds_sync();
+  if (threadIdx.x == 0) {
+    int* counter = L.arrive + tile;
+    const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = before == L.split - 1;
+    if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *last_flag = last;
+  }
+  lds_sync();
+  if (*last_flag == 0) return;
+#pragma unroll 1
+  for (int i = 0; i < I; ++i) {
+    const int p = wave + KW * i;
+    if (p < QP) {
+      const int j = p / MT, t = p - j * MT, qg = 2 * j * MT + t, qu = qg + MT;
+      f32x4 vg = f32x4{0.f, 0.f, 0.f, 0.f}, vu = vg;
+      for (int s0 = 0; s0 < L.split; ++s0) {
+        vg += __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            prs, static_cast<uint32_t>((s0 * Q + qg) * kFragBytes + lane * 16), 0, kCoherent));
+        vu += __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            prs, static_cast<uint32_t>((s0 * Q + qu) * kFragBytes + lane * 16), 0, kCoherent));
+      }
+      act_store<DT, MT>(L, M, tile * (NF / 2) + j, t, lane, vg, vu);
+    }
+  }
+  tile_done<kEpiAct>(a, L, tile);
+}
+
 // End of an item for a K-split workgroup: sums the KW wavefronts' tiles (LDS, wavefront order)
 // and writes Y, or with split > 1 the fp32 partial, then the last split to arrive writes Y. With
 // KW > 4 the tiles overlay the wavefronts' X transpose tiles, so the workgroup first waits until
 // every wavefront is past its last K step.
-template <int DT, int MT, int NF, int KW, bool LORA>
+template <int DT, int MT, int NF, int KW, int EPI>
 __device__ __forceinline__ void packed_finish(const PackedArgs& a, const PLinear& L, int M, int item, int wave, int lane,
                                               f32x4 (&acc)[NF][MT], f32x4* red, int* last_flag) {
   constexpr int Q = NF * MT;
   int probe = 0;
-  if constexpr (LORA) {
+  if constexpr (EPI == kEpiLora) {
     if (L.role == 2) probe = lora_probe(a);
   }
   if constexpr (KW > 4) lds_sync();
@@ -498,6 +605,10 @@ __device__ __forceinline__ void packed_finish(const PackedArgs& a, const PLinear
   lds_sync();
   int tile, s;
   item_tile(item, L.split, tile, s);
+  if constexpr (EPI == kEpiAct) {
+    packed_finish_act<DT, MT, NF, KW>(a, L, M, tile, s, wave, lane, red, last_flag);
+    return;
+  }
   const int n0 = tile * NF * 16;
   f32x4 sum[(Q + KW - 1) / KW];
 #pragma unroll
@@ -512,15 +623,15 @@ __device__ __forceinline__ void packed_finish(const PackedArgs& a, const PLinear
   }
   lds_sync();  // every wavefront has read the tiles; LDS is free for the next item
   if (L.split == 1) {
-    if constexpr (LORA) {
+    if constexpr (EPI == kEpiLora) {
       if (L.role == 2) lora_wait_h(a, lane, probe);
     }
 #pragma unroll
     for (int i = 0; i * KW < Q; ++i) {
       const int q = wave + KW * i;
-      if (q < Q) packed_store_frag<DT, MT, LORA>(a, L, M, n0, q, lane, sum[i]);
+      if (q < Q) packed_store_frag<DT, MT, EPI>(a, L, M, n0, q, lane, sum[i]);
     }
-    tile_done<LORA>(a, L, tile);
+    tile_done<EPI>(a, L, tile);
     return;
   }
   // Split partial: one KiB block per fragment (an fp32 fragment is 64 lanes x 16 bytes), written
@@ -545,7 +656,7 @@ __device__ __forceinline__ void packed_finish(const PackedArgs& a, const PLinear
   }
   lds_sync();
   if (*last_flag == 0) return;
-  if constexpr (LORA) {
+  if constexpr (EPI == kEpiLora) {
     if (L.role == 2) lora_wait_h(a, lane, probe);
   }
 #pragma unroll
@@ -565,16 +676,16 @@ __device__ __forceinline__ void packed_finish(const PackedArgs& a, const PLinear
         for (int j = 0; j < 8; ++j)
           if (s0 + j < L.split) v += __builtin_bit_cast(f32x4, part[j]);
       }
-      packed_store_frag<DT, MT, LORA>(a, L, M, n0, q, lane, v);
+      packed_store_frag<DT, MT, EPI>(a, L, M, n0, q, lane, v);
     }
   }
-  tile_done<LORA>(a, L, tile);
+  tile_done<EPI>(a, L, tile);
 }
 
 // End of an item for a row-split workgroup (KW = 1): each wavefront owns its NF fragments of the
 // tile outright and writes them (Y, or with split > 1 its fp32 partials; the last split of the
 // tile to arrive sums each wavefront's partials in split order and writes Y).
-template <int DT, int MT, int NF, bool LORA>
+template <int DT, int MT, int NF, int EPI>
 __device__ __forceinline__ void packed_finish_rows(const PackedArgs& a, const PLinear& L, int M, int item, int wave,
                                                    int lane, f32x4 (&acc)[NF][MT], int* last_flag) {
   constexpr int QW = NF * MT;               // fragments of one wavefront
@@ -583,18 +694,26 @@ __device__ __forceinline__ void packed_finish_rows(const PackedArgs& a, const PL
   item_tile(item, L.split, tile, s);
   const int n0 = (tile * 4 + wave) * NF * 16;
   int probe = 0;
-  if constexpr (LORA) {
+  if constexpr (EPI == kEpiLora) {
     if (L.role == 2) probe = lora_probe(a);
   }
   if (L.split == 1) {
-    if constexpr (LORA) {
+    if constexpr (EPI == kEpiLora) {
       if (L.role == 2) lora_wait_h(a, lane, probe);
     }
+    if constexpr (EPI == kEpiAct) {
 #pragma unroll
-    for (int f = 0; f < NF; ++f)
+      for (int j = 0; j < NF / 2; ++j)
 #pragma unroll
-      for (int t = 0; t < MT; ++t) packed_store_frag<DT, MT, LORA>(a, L, M, n0, f * MT + t, lane, acc[f][t]);
-    tile_done<LORA>(a, L, tile);
+        for (int t = 0; t < MT; ++t)
+          act_store<DT, MT>(L, M, (tile * 4 + wave) * (NF / 2) + j, t, lane, acc[2 * j][t], acc[2 * j + 1][t]);
+    } else {
+#pragma unroll
+      for (int f = 0; f < NF; ++f)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) packed_store_frag<DT, MT, EPI>(a, L, M, n0, f * MT + t, lane, acc[f][t]);
+    }
+    tile_done<EPI>(a, L, tile);
     return;
   }
   const uint32_t tile_bytes = static_cast<uint32_t>(L.split) * Q * kFragBytes;
@@ -618,8 +737,25 @@ __device__ __forceinline__ void packed_finish_rows(const PackedArgs& a, const PL
   }
   lds_sync();
   if (*last_flag == 0) return;
-  if constexpr (LORA) {
+  if constexpr (EPI == kEpiLora) {
     if (L.role == 2) lora_wait_h(a, lane, probe);
+  }
+  if constexpr (EPI == kEpiAct) {
+    // Each of the wavefront's (gate, up) pairs: both partials summed in split order.
+#pragma unroll 1
+    for (int pw = 0; pw < QW / 2; ++pw) {
+      const int j = pw / MT, t = pw - j * MT, qg = wave * QW + 2 * j * MT + t, qu = qg + MT;
+      f32x4 vg = f32x4{0.f, 0.f, 0.f, 0.f}, vu = vg;
+      for (int s0 = 0; s0 < L.split; ++s0) {
+        vg += __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            prs, static_cast<uint32_t>((s0 * Q + qg) * kFragBytes + lane * 16), 0, kCoherent));
+        vu += __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            prs, static_cast<uint32_t>((s0 * Q + qu) * kFragBytes + lane * 16), 0, kCoherent));
+      }
+      act_store<DT, MT>(L, M, (tile * 4 + wave) * (NF / 2) + j, t, lane, vg, vu);
+    }
+    tile_done<EPI>(a, L, tile);
+    return;
   }
   // A rolled loop over the wavefront's fragments: unrolled, the compiler would keep every
   // fragment's partial loads in flight at once and run out of registers.
@@ -639,9 +775,9 @@ __device__ __forceinline__ void packed_finish_rows(const PackedArgs& a, const PL
       for (int j = 0; j < 8; ++j)
         if (s0 + j < L.split) v += __builtin_bit_cast(f32x4, part[j]);
     }
-    packed_store_frag<DT, MT, LORA>(a, L, M, n0, qw, lane, v);
+    packed_store_frag<DT, MT, EPI>(a, L, M, n0, qw, lane, v);
   }
-  tile_done<LORA>(a, L, tile);
+  tile_done<EPI>(a, L, tile);
 }
 
 extern __shared__ __attribute__((aligned(16))) f32x4 packed_lds[];
@@ -802,7 +938,7 @@ constexpr size_t packed_lds_body() {
   return red > xts ? red : xts;
 }
 
-template <int DT, int MT, int NF, int D, int KW, bool LORA>
+template <int DT, int MT, int NF, int D, int KW, int EPI>
 __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT, NF, D, KW>())) void packed_gemm_kernel(PackedArgs a) {
   constexpr int XN = x_per_wave<MT, KW>();
   __shared__ int last_flag;
@@ -823,12 +959,12 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
   // grid barrier): then only X is still to be loaded for them.
   bool w_ready = false;
   for (int gi = 0; gi < a.count; ++gi) {
-    const PLinear L = load_linear<NF, KW, LORA>(a, gi, epoch);
+    const PLinear L = load_linear<NF, KW, EPI>(a, gi, epoch);
     POffsets<MT, NF, XN> o;
     packed_offsets<MT, NF, KW>(L, a.M, lane, wave, o);
     const auto wr = make_rsrc(L.wp, static_cast<uint32_t>((L.N + 15) >> 4) * L.Ks * kFragBytes);
     const auto xr = make_rsrc(L.x, static_cast<uint32_t>(a.M * L.ldx * 2));
-    PCursor ld{first_item<LORA>(a, gi), 0, 0, 0, 0};
+    PCursor ld{first_item<EPI>(a, gi), 0, 0, 0, 0};
     pc_enter<NF, D, KW>(L, wave, ld);
     PCursor cp = ld;
     if (ld.item < L.items) {
@@ -904,9 +1040,9 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
           }
         }
         if constexpr (KW != 1)
-          packed_finish<DT, MT, NF, KW, LORA>(a, L, a.M, cp.item, wave, lane, acc, red, &last_flag);
+          packed_finish<DT, MT, NF, KW, EPI>(a, L, a.M, cp.item, wave, lane, acc, red, &last_flag);
         else
-          packed_finish_rows<DT, MT, NF, LORA>(a, L, a.M, cp.item, wave, lane, acc, &last_flag);
+          packed_finish_rows<DT, MT, NF, EPI>(a, L, a.M, cp.item, wave, lane, acc, &last_flag);
         cp.item += a.G;
         if (cp.item >= L.items) break;
         pc_enter<NF, D, KW>(L, wave, cp);
@@ -919,8 +1055,8 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
       // workgroup's part of this Y.
       __builtin_amdgcn_s_waitcnt(0);
       barrier_arrive(a, epoch, L.seq);
-      const PLinear Ln = load_linear<NF, KW, LORA>(a, gi + 1);
-      PCursor nx{first_item<LORA>(a, gi + 1), 0, 0, 0, 0};
+      const PLinear Ln = load_linear<NF, KW, EPI>(a, gi + 1);
+      PCursor nx{first_item<EPI>(a, gi + 1), 0, 0, 0, 0};
       pc_enter<NF, D, KW>(Ln, wave, nx);
       if (nx.item < Ln.items) {
         POffsets<MT, NF, XN> on;
@@ -956,6 +1092,21 @@ constexpr bool packed_compiled() {
   return packed_two_per_cu<MT, NF, D, KW>() || packed_regs<MT, NF, D, KW>() <= 320;
 }
 
+// Whether a configuration's epilogue fits the registers its pipeline leaves (measured: no scratch
+// in the compiler's resource report for either element type). KW = 1 configurations are held to
+// 256 VGPRs; the LoRA epilogue keeps the low-rank correction's operands beside the pipeline. A
+// configuration that does not fit runs at a lower pipeline depth D (packed_pick_d): the K steps
+// are summed in the same order at every depth, so the results are the same.
+template <int MT, int NF, int D, int KW, int EPI>
+constexpr bool packed_fits() {
+  constexpr int r = packed_regs<MT, NF, D, KW>();
+  if constexpr (KW == 1) return r <= (EPI == kEpiLora ? 240 : 244) || (EPI == kEpiAct && r <= 292);
+  if constexpr (EPI != kEpiLora) return true;
+  if constexpr (KW == 4) return packed_two_per_cu<MT, NF, D, KW>() || r <= 288;
+  if constexpr (KW == 16) return r <= 48;
+  return true;
+}
+
 template <int MT, int NF, int KW>
 constexpr size_t packed_lds_bytes() {
   return packed_lds_body<MT, NF, KW>() + kFragBytes;  // + the warm-up sink
@@ -964,13 +1115,13 @@ constexpr size_t packed_lds_bytes() {
 // Launches with G = min(a.G, resident workgroups), where a.G arrives as the most items of any
 // linear; a chained launch with grid barriers (a.sync) uses every resident workgroup. `dry` only
 // checks that the kernel exists.
-template <int DT, int MT, int NF, int D, int KW, bool LORA>
+template <int DT, int MT, int NF, int D, int KW, int EPI>
 hipError_t packed_launch(PackedArgs& a, int cus, hipStream_t stream, bool dry) {
-  if constexpr (!packed_compiled<MT, NF, D, KW>()) {
+  if constexpr (!packed_compiled<MT, NF, D, KW>() || (D > 2 && !packed_fits<MT, NF, D, KW, EPI>())) {
     return hipErrorInvalidConfiguration;
   } else {
     if (dry) return hipSuccess;
-    auto kern = packed_gemm_kernel<DT, MT, NF, D, KW, LORA>;
+    auto kern = packed_gemm_kernel<DT, MT, NF, D, KW, EPI>;
     constexpr size_t lds = packed_lds_bytes<MT, NF, KW>();
     static int per_cu = 0;
     if (per_cu == 0) {
@@ -996,35 +1147,43 @@ hipError_t packed_launch(PackedArgs& a, int cus, hipStream_t stream, bool dry) {
   }
 }
 
-template <int DT, int MT, int NF, int KW, bool LORA>
+template <int DT, int MT, int NF, int KW, int EPI>
 hipError_t packed_pick_d(PackedArgs& a, int d, int cus, hipStream_t s, bool dry) {
-  if (d == 2) return packed_launch<DT, MT, NF, 2, KW, LORA>(a, cus, s, dry);
-  if (d == 4) return packed_launch<DT, MT, NF, 4, KW, LORA>(a, cus, s, dry);
-  if (d == 6) return packed_launch<DT, MT, NF, 6, KW, LORA>(a, cus, s, dry);
-  if (d == 8) return packed_launch<DT, MT, NF, 8, KW, LORA>(a, cus, s, dry);
+  // The tile's depth is a cap: lowered to one whose epilogue fits (packed_fits).
+  if (d == 8 && !packed_fits<MT, NF, 8, KW, EPI>()) d = 6;
+  if (d == 6 && !packed_fits<MT, NF, 6, KW, EPI>()) d = 4;
+  if (d == 4 && !packed_fits<MT, NF, 4, KW, EPI>()) d = 2;
+  if (d == 2) return packed_launch<DT, MT, NF, 2, KW, EPI>(a, cus, s, dry);
+  if (d == 4) return packed_launch<DT, MT, NF, 4, KW, EPI>(a, cus, s, dry);
+  if (d == 6) return packed_launch<DT, MT, NF, 6, KW, EPI>(a, cus, s, dry);
+  if (d == 8) return packed_launch<DT, MT, NF, 8, KW, EPI>(a, cus, s, dry);
   return hipErrorInvalidConfiguration;
 }
 
-template <int DT, int MT, int KW, bool LORA>
+template <int DT, int MT, int KW, int EPI>
 hipError_t packed_pick(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry) {
-  if (nf == 1) return packed_pick_d<DT, MT, 1, KW, LORA>(a, d, cus, s, dry);
-  if (nf == 2) return packed_pick_d<DT, MT, 2, KW, LORA>(a, d, cus, s, dry);
-  if (nf == 4) return packed_pick_d<DT, MT, 4, KW, LORA>(a, d, cus, s, dry);
+  if (nf == 1) {
+    if constexpr (EPI == kEpiAct) return hipErrorInvalidConfiguration;  // gate and up fragments come in pairs
+    else return packed_pick_d<DT, MT, 1, KW, EPI>(a, d, cus, s, dry);
+  }
+  if (nf == 2) return packed_pick_d<DT, MT, 2, KW, EPI>(a, d, cus, s, dry);
+  if (nf == 4) return packed_pick_d<DT, MT, 4, KW, EPI>(a, d, cus, s, dry);
   return hipErrorInvalidConfiguration;
 }
 
-// LORA: the gated-LoRA launch (PackedArgs::lora: two linears, the base tiles corrected).
-template <int DT, int KW, bool LORA = false>
+// EPI: the store epilogue (kEpiPlain; kEpiLora: the gated-LoRA launch, PackedArgs::lora: two linears,
+// the base tiles corrected).
+template <int DT, int KW, int EPI = kEpiPlain>
 hipError_t packed_dispatch_kw(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry) {
   switch ((a.M + 15) / 16) {
-    case 1: return packed_pick<DT, 1, KW, LORA>(a, nf, d, cus, s, dry);
-    case 2: return packed_pick<DT, 2, KW, LORA>(a, nf, d, cus, s, dry);
-    case 3: return packed_pick<DT, 3, KW, LORA>(a, nf, d, cus, s, dry);
-    case 4: return packed_pick<DT, 4, KW, LORA>(a, nf, d, cus, s, dry);
-    case 5: return packed_pick<DT, 5, KW, LORA>(a, nf, d, cus, s, dry);
-    case 6: return packed_pick<DT, 6, KW, LORA>(a, nf, d, cus, s, dry);
-    case 7: return packed_pick<DT, 7, KW, LORA>(a, nf, d, cus, s, dry);
-    case 8: return packed_pick<DT, 8, KW, LORA>(a, nf, d, cus, s, dry);
+    case 1: return packed_pick<DT, 1, KW, EPI>(a, nf, d, cus, s, dry);
+    case 2: return packed_pick<DT, 2, KW, EPI>(a, nf, d, cus, s, dry);
+    case 3: return packed_pick<DT, 3, KW, EPI>(a, nf, d, cus, s, dry);
+    case 4: return packed_pick<DT, 4, KW, EPI>(a, nf, d, cus, s, dry);
+    case 5: return packed_pick<DT, 5, KW, EPI>(a, nf, d, cus, s, dry);
+    case 6: return packed_pick<DT, 6, KW, EPI>(a, nf, d, cus, s, dry);
+    case 7: return packed_pick<DT, 7, KW, EPI>(a, nf, d, cus, s, dry);
+    case 8: return packed_pick<DT, 8, KW, EPI>(a, nf, d, cus, s, dry);
   }
   return hipErrorInvalidConfiguration;
 }
@@ -1055,5 +1214,14 @@ hipError_t packed_dispatch_lora_f16_k1(PackedArgs& a, int nf, int d, int cus, hi
 hipError_t packed_dispatch_lora_f16_k4(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
 hipError_t packed_dispatch_lora_f16_k8(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
 hipError_t packed_dispatch_lora_f16_k16(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+// ... and the SiLU-and-multiply launches (wave_frags 2 or 4).
+hipError_t packed_dispatch_act_bf16_k1(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_act_bf16_k4(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_act_bf16_k8(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_act_bf16_k16(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_act_f16_k1(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_act_f16_k4(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_act_f16_k8(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
+hipError_t packed_dispatch_act_f16_k16(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);
 
 }  // namespace plm

@@ -55,6 +55,7 @@ EXPORTS = (
     "plm_round_verify_packed",
     "plm_gemm_packed_lora",
     "plm_gemm_packed_lora_workspace_bytes",
+    "plm_gemm_packed_silu_mul",
     "plm_voronoi_shortlist",
     "plm_voronoi_spread",
     "plm_voronoi_prior",
@@ -152,6 +153,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.plm_gemm_packed_lora.restype = ctypes.c_int
     lib.plm_gemm_packed_lora_workspace_bytes.argtypes = [c_i64, c_i64, c_i64, c_i64, c_i64, c_i32, tile_p]
     lib.plm_gemm_packed_lora_workspace_bytes.restype = c_sz
+    lib.plm_gemm_packed_silu_mul.argtypes = lib.plm_gemm_packed.argtypes
+    lib.plm_gemm_packed_silu_mul.restype = ctypes.c_int
     lib.plm_lm_head_verify_packed_logits.argtypes = [c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_p, c_i64, c_i32,
                                                      ctypes.c_float, c_i32, c_p, c_p, c_p, c_i64, c_i64, tile_p, c_p,
                                                      c_sz, c_p]

@@ -42,6 +42,9 @@ _tiles: dict[tuple[int, int, int, int], _lib.Tile] = {}
 _packed = WeakTensorKeyDictionary()
 # released weight tensor -> its packed copy (the tensor itself then holds no data)
 _released = WeakTensorKeyDictionary()
+# fused gate/up weight tensor -> ((data_ptr, shape, row stride, version counter), packed copy with the
+# gate and up halves interleaved by 16-row fragment)
+_packed_gate_up = WeakTensorKeyDictionary()
 _pack_lock = threading.Lock()
 _workspaces: dict[int, torch.Tensor] = {}
 _ws_lock = threading.Lock()
@@ -196,6 +199,75 @@ def default_config(M: int, N: int, K: int) -> Config:
     if M <= 128:
         return heuristic_tile(M, N, K, supported=lambda cfg: tile_supported(M, K, cfg))
     return {"wave_frags": 2, "k_waves": 8, "split_k": 1, "unroll": 2}  # unused: the wide kernel runs
+
+
+def gate_up_order(w: torch.Tensor) -> torch.Tensor:
+    """A fused gate/up weight ``[2I, K]`` (gate rows first) with its halves interleaved by 16-row
+    fragment — gate rows [16j, 16j+16), then up rows [16j, 16j+16), for j = 0, 1, ... — the row
+    order ``plm_gemm_packed_silu_mul`` reads packed. A new tensor."""
+    N, K = w.shape
+    if N % 32:
+        raise ValueError(f"a fused gate/up weight needs a multiple of 32 rows, got {N}")
+    return w.reshape(2, N // 32, 16, K).transpose(0, 1).reshape(N, K).contiguous()
+
+
+def packed_gate_up(w: torch.Tensor) -> torch.Tensor:
+    """The interleaved packed copy of a fused gate/up weight, made on first use and kept while ``w``
+    lives unchanged (for a released weight, rebuilt from its packed copy)."""
+    key = (w.data_ptr(), tuple(w.shape), w.stride(0), w._version)
+    hit = _packed_gate_up.get(w)
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("a gate/up weight is packed on its first use, which cannot happen during graph capture")
+    with _pack_lock:
+        src = unpack_weight(_released[w], w.shape[0], w.shape[1], w.dtype) if w in _released else w
+        p = pack_weight(gate_up_order(src))
+        _packed_gate_up[w] = (key, p)
+        return p
+
+
+def gate_up_silu(x: torch.Tensor, w: torch.Tensor, cfg: Config | None = None,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """``silu(g) * u`` of the fused gate/up projection ``x @ w^T`` (``w = [gate; up]``, ``[2I, K]``),
+    ``[M, I]`` in x's dtype, in one launch (``plm_gemm_packed_silu_mul``): the Llama-style MLP's
+    gate_up_proj GEMM (routed through plm/fast_gemm.py:104-110) and the ``SiluAndMul`` vLLM runs on
+    its output as a second launch, with the same roundings (the projection's output rounded to the
+    model dtype, silu rounded, then the product). ``cfg``: the tile (wave_frags 2 or 4); by default
+    the projection's tuned tile, with wave_frags 2 where it has 1. Widths above 128 rows run as the
+    projection then the activation, each as its own launch."""
+    _check_operands(x, w)
+    M, K = x.shape
+    N = w.shape[0]
+    half = N // 2
+    if M > 128:
+        y = released_linear(x, w) if w in _released else F.linear(x, w)
+        act = F.silu(y[:, :half]) * y[:, half:]
+        if out is not None:
+            out.copy_(act)
+            return out
+        return act
+    if cfg is None:
+        cfg = CONFIGS.get((M, N, K)) or default_config(M, N, K)
+        if cfg["wave_frags"] % 2:
+            cfg = dict(cfg, wave_frags=2)
+    if out is None:
+        out = torch.empty(M, half, device=x.device, dtype=x.dtype)
+    elif out.shape != (M, half) or out.dtype != x.dtype or out.stride(1) != 1:
+        raise ValueError(f"out must be a row-major [{M},{half}] {x.dtype} tensor")
+    x = _row_major(x)
+    tile = _tile(cfg)
+    lib = _lib.lib()
+    need = int(lib.plm_gemm_packed_workspace_bytes(M, N, K, tile))
+    ws_ptr, ws_bytes = None, 0
+    if need:
+        ws = workspace(x.device, need)
+        ws_ptr, ws_bytes = ws.data_ptr(), ws.numel()
+    status = lib.plm_gemm_packed_silu_mul(_lib.DTYPE_CODES[x.dtype], x.data_ptr(), x.stride(0),
+                                          packed_gate_up(w).data_ptr(), out.data_ptr(), out.stride(0), M, N, K,
+                                          tile, ws_ptr, ws_bytes, _lib.stream_handle(x.device))
+    _lib.check(status, f"plm_gemm_packed_silu_mul(M={M}, N={N}, K={K}, cfg={cfg})")
+    return out
 
 
 def reserve_workspace(device: torch.device, shapes: dict[tuple[int, int, int], Config] | None = None) -> None:

@@ -368,3 +368,28 @@ def test_golden_verify(name):
     exact = torch.from_numpy(z["x"].double().numpy() @ z["w"].double().numpy().T)
     assert np.array_equal(po.nucleus_acceptance_fp64(exact, pending, float(z["p"])), z["accept"])
     assert 0 < int(z["accept"].sum()) < len(z["accept"])
+
+
+def test_silu_mul_is_pinned():
+    """silu_mul against its fp64 restatement (equal but for a rare neighbouring rounding of silu),
+    the intermediate rounding (silu(g) is rounded before the product: a single-rounding version
+    differs on a sizeable share of elements), and the closed forms: g = 0 gives 0, a large positive
+    gate passes u * g, a large negative one gives (about) 0, and the halves are taken in order."""
+    g = torch.Generator().manual_seed(9)
+    for dtype, bits in ((torch.bfloat16, 8), (torch.float16, 11)):
+        y = (3 * torch.randn(64, 256, generator=g)).to(dtype)
+        got = oracle.silu_mul(y).double().numpy()
+        ref = oracle.silu_mul_fp64(y)
+        step = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -14))) - (bits - 1))
+        assert np.all(np.abs(got - ref) <= step * 1.0001) and np.mean(got != ref) < 0.002
+        yd = y.double().numpy()
+        once = torch.from_numpy(yd[:, :128] / (1 + np.exp(-yd[:, :128])) * yd[:, 128:]).to(dtype).double().numpy()
+        assert np.mean(once != got) > 0.02
+    z = torch.zeros(2, 8).bfloat16()
+    z[:, 4:] = 5.0
+    assert torch.equal(oracle.silu_mul(z), torch.zeros(2, 4).bfloat16())
+    big = torch.tensor([[20.0, -20.0, 3.0, 3.0]]).bfloat16()
+    out = oracle.silu_mul(big).float()
+    assert out[0, 0].item() == pytest.approx(60.0, rel=1e-2) and abs(out[0, 1].item()) < 1e-6
+    swapped = oracle.silu_mul(torch.tensor([[3.0, 20.0]]).bfloat16()).float()   # gate 3, up 20
+    assert swapped.item() == pytest.approx(3.0 / (1 + np.exp(-3.0)) * 20.0, rel=1e-2)
