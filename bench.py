@@ -61,9 +61,12 @@ def parse_args():
 
 
 class Round:
-    """The round's weights, activation chain and captured graph at one width M."""
+    """The round's weights, activation chain and captured graph at one width M. ``act``: the
+    Llama-style gate/up projections carry their SiLU-and-multiply (output ``[M, I]``, read whole by
+    down: the MLP's real dataflow); otherwise each linear reads the leading columns of the one
+    before it."""
 
-    def __init__(self, M, hidden, mlp, layers, weights, tables, device, gemms=None):
+    def __init__(self, M, hidden, mlp, layers, weights, tables, device, gemms=None, act=False):
         import torch
 
         from plm_amd.workloads import GPT2_VOCAB, gpt_block
@@ -75,9 +78,14 @@ class Round:
         self.gemms = list(gemms)
         self.weights = weights
         self.cfgs = [tables[(M, g.N, g.K)] for g in self.gemms]
+        self.act = [act and gm.name == "gate_up" for gm in self.gemms]
+        for i, a in enumerate(self.act):
+            if a and self.cfgs[i]["wave_frags"] % 2:
+                self.cfgs[i] = dict(self.cfgs[i], wave_frags=2)   # gate and up fragments in pairs
         g = torch.Generator(device=device).manual_seed(3000 + M)
         self.x0 = torch.randn(M, hidden, generator=g, device=device).bfloat16()
-        self.outs = [torch.empty(M, gm.N, device=device, dtype=torch.bfloat16) for gm in self.gemms]
+        self.outs = [torch.empty(M, gm.N // 2 if a else gm.N, device=device, dtype=torch.bfloat16)
+                     for gm, a in zip(self.gemms, self.act)]
         self.inputs = []
         x = self.x0
         for gm, out in zip(self.gemms, self.outs):
@@ -86,10 +94,11 @@ class Round:
         self.graph = None
 
     def launch(self, indices=None):
-        from plm_amd.fast_gemm import hip_linear
+        from plm_amd.fast_gemm import gate_up_silu, hip_linear
 
         for i in (range(len(self.gemms)) if indices is None else indices):
-            hip_linear(self.inputs[i], self.weights[i], self.cfgs[i], self.outs[i])
+            fn = gate_up_silu if self.act[i] else hip_linear
+            fn(self.inputs[i], self.weights[i], self.cfgs[i], self.outs[i])
 
     def capture(self, indices=None):
         import torch
@@ -245,8 +254,9 @@ class ChainedRound:
         G = _lib.lib().plm_gemm_packed_resident_workgroups(_lib.PLM_BF16, rnd.M, _tile(cfg))
         _lib.check(min(G, 0), "plm_gemm_packed_resident_workgroups")
         n = len(rnd.gemms) - 1
-        links = [Link(x, w, y, i - 1, packed_chain_split(g.N, g.K, cfg, G))
-                 for i, (g, x, w, y) in enumerate(zip(rnd.gemms[:n], rnd.inputs[:n], rnd.weights[:n], rnd.outs[:n]))]
+        links = [Link(x, w, y, i - 1, packed_chain_split(g.N, g.K, cfg, G), a)
+                 for i, (g, x, w, y, a) in enumerate(zip(rnd.gemms[:n], rnd.inputs[:n], rnd.weights[:n], rnd.outs[:n],
+                                                         rnd.act[:n]))]
         self.chain = LinearChain(links, cfg, packed=True)
         self.head = (rnd.inputs[n], rnd.weights[n], rnd.cfgs[n], rnd.outs[n])
         self.chain_bytes = sum(g.bytes(rnd.M) for g in rnd.gemms[:n])
@@ -657,11 +667,13 @@ def time_llama_rounds(args, device):
     """The reference's Llama-style linear sets (hidden 2048 and 3072: GQA QKV, fused gate/up, vocabulary
     50304) as rounds at width M, both ways: the chained launch of the block linears + LM-head launch
     (checked bit for bit against per-linear launches first) and the per-GEMM graph with the tuned
-    table's tile per shape."""
+    table's tile per shape; each once as bare linears (each reading the leading columns of the one
+    before) and once with the gate/up projections carrying their SiLU-and-multiply, read whole by
+    down (``act``: the MLP's dataflow)."""
     import torch
 
     from plm_amd import gemm_tables
-    from plm_amd.fast_gemm import hip_linear
+    from plm_amd.fast_gemm import gate_up_silu, hip_linear
     from plm_amd.workloads import LLAMA_SETS, llama_round
 
     out = {}
@@ -671,32 +683,42 @@ def time_llama_rounds(args, device):
         gen = torch.Generator(device=device)
         weights = []
         for i, g in enumerate(gemms):
+            # std 1/sqrt(K): every linear keeps its input's scale, so 28 layers of products (and of
+            # silu(g) * u) neither overflow nor vanish without the norms a real layer has
             gen.manual_seed(7 + 1000 * 6 + i)
-            weights.append((0.02 * torch.randn(g.N, g.K, generator=gen, device=device)).bfloat16())
-        rnd = Round(args.M, spec["hidden"], None, spec["layers"], weights, tables, device, gemms=gemms)
-        chained = ChainedRound(rnd)
-        chained.run()
-        torch.cuda.synchronize()
-        chain_outs = [o.clone() for o in rnd.outs]
-        for i, ln in enumerate(chained.chain.links):
-            hip_linear(ln.x, ln.w, dict(chained.chain.cfg, split_k=ln.split_k), rnd.outs[i])
-        hip_linear(*chained.head)
-        torch.cuda.synchronize()
-        same = all(torch.equal(a, b) for a, b in zip(chain_outs, rnd.outs)) and not chained.chain.error_flag()
-        graph = capture_graph(chained.run)
-        us_chain = time_graph(graph, max(10, args.steps // 2), 3) * 1000.0
-        del graph
-        graph = rnd.capture()
-        us_graph = time_graph(graph, max(10, args.steps // 2), 3) * 1000.0
-        del graph
-        nbytes = rnd.bytes
-        out[name] = {"layers": spec["layers"], "hidden": spec["hidden"], "bytes": nbytes,
-                     "chained_us": round(us_chain, 1), "chained_gbps": round(nbytes / (us_chain * 1e-6) / 1e9, 1),
-                     "per_gemm_us": round(us_graph, 1), "per_gemm_gbps": round(nbytes / (us_graph * 1e-6) / 1e9, 1),
-                     "chain_matches_per_linear": bool(same)}
-        print(f"[bench] Llama-style {name} round: chained {us_chain:.1f} us, per-GEMM {us_graph:.1f} us", file=sys.stderr,
-              flush=True)
-        del rnd, chained, weights, chain_outs
+            weights.append((torch.randn(g.N, g.K, generator=gen, device=device) / g.K ** 0.5).bfloat16())
+        res = {"layers": spec["layers"], "hidden": spec["hidden"]}
+        for act in (False, True):
+            rnd = Round(args.M, spec["hidden"], None, spec["layers"], weights, tables, device, gemms=gemms, act=act)
+            chained = ChainedRound(rnd)
+            chained.run()
+            torch.cuda.synchronize()
+            chain_outs = [o.clone() for o in rnd.outs]
+            for i, ln in enumerate(chained.chain.links):
+                fn = gate_up_silu if ln.act else hip_linear
+                fn(ln.x, ln.w, dict(chained.chain.cfg, split_k=ln.split_k), rnd.outs[i])
+            hip_linear(*chained.head)
+            torch.cuda.synchronize()
+            same = all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(chain_outs, rnd.outs))
+            same = same and not chained.chain.error_flag()
+            graph = capture_graph(chained.run)
+            us_chain = time_graph(graph, max(10, args.steps // 2), 3) * 1000.0
+            del graph
+            graph = rnd.capture()
+            us_graph = time_graph(graph, max(10, args.steps // 2), 3) * 1000.0
+            del graph
+            nbytes = rnd.bytes
+            key = "mlp_act" if act else "linears"
+            res[key] = {"bytes": nbytes, "chained_us": round(us_chain, 1),
+                        "chained_gbps": round(nbytes / (us_chain * 1e-6) / 1e9, 1), "per_gemm_us": round(us_graph, 1),
+                        "per_gemm_gbps": round(nbytes / (us_graph * 1e-6) / 1e9, 1),
+                        "chain_matches_per_linear": bool(same)}
+            print(f"[bench] Llama-style {name} round ({key}): chained {us_chain:.1f} us, per-GEMM {us_graph:.1f} us, "
+                  f"chain matches {same}", file=sys.stderr, flush=True)
+            del rnd, chained, chain_outs
+            torch.cuda.empty_cache()
+        out[name] = res
+        del weights
         torch.cuda.empty_cache()
     return out
 

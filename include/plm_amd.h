@@ -33,6 +33,11 @@ enum plm_round_mode { PLM_ROUND_F32 = 0, PLM_ROUND_BF16 = 1, PLM_ROUND_F16 = 2 }
  * PLM_RULE_FLOOR is floor_acceptance (plm/decoder.py:78-82) with threshold = epsilon. */
 enum plm_accept_rule { PLM_RULE_NUCLEUS = 0, PLM_RULE_FLOOR = 1 };
 
+/* What a chain linear writes (plm_chain_gemm.out_f32): Y in the input dtype, the fp32
+ * accumulator, or — packed chains only — the SiLU-and-multiply of a fused gate/up projection
+ * (plm_gemm_packed_silu_mul's epilogue: Y[M, N/2], W packed with its halves interleaved). */
+enum plm_out_kind { PLM_OUT_MODEL = 0, PLM_OUT_F32 = 1, PLM_OUT_SILU_MUL = 2 };
+
 /* Every workspace starts with this many bytes of integer arrival counters, which must be zero
  * before the first call and which every kernel leaves zero; the rest of a workspace is scratch
  * that needs no initialisation. One workspace may therefore serve every entry point in turn on
@@ -175,8 +180,10 @@ typedef struct plm_chain_gemm {
   int32_t N, K;
   int32_t split_k;        /* workgroups splitting K (>= 1) */
   int32_t dep;            /* -1, or the index of an earlier linear whose Y this X is (x == that y,
-                             ldx == its ldy, K <= its N): the linear then waits for those tiles */
-  int32_t out_f32;        /* 1: Y is the fp32 accumulator, 0: Y in the input dtype */
+                             ldx == its ldy, K <= its Y's columns): the linear then waits for those tiles */
+  int32_t out_f32;        /* a plm_out_kind: PLM_OUT_F32 (1) the fp32 accumulator, PLM_OUT_MODEL (0) Y in
+                             the input dtype; PLM_OUT_SILU_MUL (2, packed chains, even wave_frags) the
+                             SiLU-and-multiply, Y[M, N/2] with N % 32 == 0, ldy % 4 == 0, y 8-byte aligned */
   /* filled by plm_gemm_chain_prepare */
   int32_t consumed;       /* 1 when a later linear reads this Y */
   int32_t arrive_base;    /* counter-area index of this linear's split-K arrival counters */

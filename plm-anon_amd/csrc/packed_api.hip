@@ -132,14 +132,23 @@ constexpr int kPackedSpinLimit = 1 << 20;  // polls (each one device round trip)
 // Counter area of a packed launch: split arrival counters from kPackedArriveBase, progress flags
 // of a chain (an int64 per workgroup) from kPackedBarrierBase.
 
-// Checks one linear's operands (W packed); returns PLM_OK or the status to report.
-int packed_check_linear(int32_t dtype, const plm_chain_gemm& g, int64_t M) {
+// Y columns of a linear: N, or N/2 for the SiLU-and-multiply epilogue.
+int64_t out_cols(const plm_chain_gemm& g) { return g.out_f32 == PLM_OUT_SILU_MUL ? g.N / 2 : g.N; }
+
+// Checks one linear's operands (W packed); returns PLM_OK or the status to report. `tile` given:
+// the SiLU-and-multiply epilogue is allowed (gate and up fragments pair up inside a wavefront's
+// or a tile's fragments, and the output's 16-column blocks are whole).
+int packed_check_linear(int32_t dtype, const plm_chain_gemm& g, int64_t M, const plm_tile* tile = nullptr) {
   if (g.x == nullptr || g.w == nullptr || g.y == nullptr) return PLM_ERR_ARGUMENT;
   if (dtype != PLM_BF16 && dtype != PLM_F16) return PLM_ERR_ARGUMENT;
+  const bool act = g.out_f32 == PLM_OUT_SILU_MUL;
+  if (g.out_f32 != PLM_OUT_MODEL && g.out_f32 != PLM_OUT_F32 && !(act && tile != nullptr)) return PLM_ERR_ARGUMENT;
+  if (act && (tile->wave_frags % 2 != 0 || g.N % 32 != 0 || g.ldy % 4 != 0)) return PLM_ERR_ARGUMENT;
   if (M < 1 || M > kPackedMaxM || g.N < 1 || g.K < 8 || g.K > (1 << 24) || g.K % 8 != 0 || g.ldx < g.K ||
-      g.ldy < g.N)
+      g.ldy < out_cols(g))
     return PLM_ERR_ARGUMENT;
-  if (g.split_k < 1 || g.split_k > 64 || (g.out_f32 != 0 && g.out_f32 != 1)) return PLM_ERR_ARGUMENT;
+  if (g.split_k < 1 || g.split_k > 64) return PLM_ERR_ARGUMENT;
+  if (act && (reinterpret_cast<uintptr_t>(g.y) & 7) != 0) return PLM_ERR_ALIGNMENT;
   // 32-bit buffer offsets: X and the packed weights must each span less than 2 GiB.
   if (M * g.ldx * 2 >= (int64_t(1) << 31) || packed_bytes(g.N, g.K) >= (int64_t(1) << 31)) return PLM_ERR_ARGUMENT;
   if (g.ldx % 8 != 0 || (reinterpret_cast<uintptr_t>(g.x) & 15) != 0 || (reinterpret_cast<uintptr_t>(g.w) & 15) != 0)
@@ -404,7 +413,7 @@ int plm_gemm_chain_packed(int32_t dtype, const plm_chain_gemm* host_gemms, const
   std::vector<plm_chain_gemm> check(host_gemms, host_gemms + count);
   const int64_t need = plm::packed_prepare(check.data(), count, M, *tile);
   if (need < 0) return static_cast<int>(need);
-  bool sync = false, any_split = false;
+  bool sync = false, any_split = false, any_act = false;
   int64_t most_items = 0;
   std::vector<plm::PSpan> ys(count), xs(count), ws(count);
   for (int32_t i = 0; i < count; ++i) {
@@ -412,20 +421,21 @@ int plm_gemm_chain_packed(int32_t dtype, const plm_chain_gemm* host_gemms, const
     if (g.consumed != check[i].consumed || g.arrive_base != check[i].arrive_base ||
         g.done_base != check[i].done_base || g.partial_offset != check[i].partial_offset)
       return PLM_ERR_ARGUMENT;
-    const int status = plm::packed_check_linear(dtype, g, M);
+    const int status = plm::packed_check_linear(dtype, g, M, tile);
     if (status != PLM_OK) return status;
     plm_tile ti = *tile;
     ti.split_k = g.split_k;
     most_items = std::max(most_items, plm::packed_tiles(g.N, ti) * g.split_k);
     any_split = any_split || g.split_k > 1;
-    ys[i] = plm::pspan(g.y, M, g.ldy, g.N, g.out_f32 ? 4 : 2);
+    any_act = any_act || g.out_f32 == PLM_OUT_SILU_MUL;
+    ys[i] = plm::pspan(g.y, M, g.ldy, plm::out_cols(g), g.out_f32 == PLM_OUT_F32 ? 4 : 2);
     xs[i] = plm::pspan(g.x, M, g.ldx, g.K, 2);
     ws[i] = plm::PSpan{reinterpret_cast<uintptr_t>(g.w),
                        reinterpret_cast<uintptr_t>(g.w) + static_cast<uintptr_t>(plm::packed_bytes(g.N, g.K))};
     if (g.dep >= 0) {
       sync = true;
       const plm_chain_gemm& p = host_gemms[g.dep];
-      if (g.x != p.y || g.ldx != p.ldy || g.K > p.N || p.out_f32) return PLM_ERR_ARGUMENT;
+      if (g.x != p.y || g.ldx != p.ldy || g.K > plm::out_cols(p) || p.out_f32 == PLM_OUT_F32) return PLM_ERR_ARGUMENT;
     }
   }
   // No linear writes what another linear writes, or reads before it is written.
@@ -444,7 +454,7 @@ int plm_gemm_chain_packed(int32_t dtype, const plm_chain_gemm* host_gemms, const
   a.sync = sync ? plm::packed_chain_mode(host_gemms, count, *tile) : 0;
   const int64_t needed = (sync || any_split) ? need : 0;
   return plm::packed_launch_args(dtype, a, *tile, workspace, workspace_bytes, needed,
-                                 static_cast<hipStream_t>(stream));
+                                 static_cast<hipStream_t>(stream), any_act ? plm::kEpiAct : plm::kEpiPlain);
 }
 
 size_t plm_gemm_packed_lora_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t gated_from, int64_t rank,
@@ -535,26 +545,21 @@ int plm_gemm_packed_silu_mul(int32_t dtype, const void* x, int64_t ldx, const vo
                              size_t workspace_bytes, void* stream) {
   if (!plm::packed_tile_valid(tile)) return PLM_ERR_TILE;
   const plm_tile& t = *tile;
-  // Gate and up fragments pair up inside a wavefront's or a tile's fragments, and the output's
-  // 16-column blocks are whole.
-  if (t.wave_frags % 2 != 0 || N < 32 || N % 32 != 0 || N > (int64_t(1) << 30) || K > (int64_t(1) << 30))
-    return PLM_ERR_ARGUMENT;
-  if (ldy < N / 2 || ldy % 4 != 0) return PLM_ERR_ARGUMENT;
-  if ((reinterpret_cast<uintptr_t>(y) & 7) != 0) return PLM_ERR_ALIGNMENT;
+  if (N < 32 || N > (int64_t(1) << 30) || K > (int64_t(1) << 30)) return PLM_ERR_ARGUMENT;
   plm_chain_gemm g{};
   g.x = x;
   g.w = packed_w;
   g.y = y;
   g.ldx = ldx;
   g.ldw = K;
-  g.ldy = N;  // the checks below see the projection's N; the output's row stride is ldy
+  g.ldy = ldy;
   g.N = static_cast<int32_t>(N);
   g.K = static_cast<int32_t>(K);
   g.split_k = t.split_k;
   g.dep = -1;
-  int status = plm::packed_check_linear(dtype, g, M);
+  g.out_f32 = PLM_OUT_SILU_MUL;
+  const int status = plm::packed_check_linear(dtype, g, M, &t);
   if (status != PLM_OK) return status;
-  g.ldy = ldy;
   const int64_t tiles = plm::packed_tiles(N, t);
   if (t.split_k > 1 && tiles > plm::kPackedBarrierBase - plm::kPackedArriveBase) return PLM_ERR_ARGUMENT;
   g.arrive_base = plm::kPackedArriveBase;

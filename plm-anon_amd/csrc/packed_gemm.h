@@ -354,7 +354,7 @@ __device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t xr, const PCursor
 template <int DT>
 __device__ __forceinline__ void packed_store4(const PLinear& L, int m, int n, f32x4 v) {
   const int left = L.N - n;
-  if (L.out_f32) {
+  if (L.out_f32 == PLM_OUT_F32) {
     float* y = static_cast<float*>(L.y) + static_cast<int64_t>(m) * L.ldy + n;
     if (left >= 4 && (reinterpret_cast<uintptr_t>(y) & 15) == 0) {
       *reinterpret_cast<f32x4*>(y) = v;
@@ -501,9 +501,13 @@ __device__ __forceinline__ void act_store(const PLinear& L, int M, int cblk, int
     const float gr = from_bits16<DT>(to_bits16<DT>(g[r])), ur = from_bits16<DT>(to_bits16<DT>(u[r]));
     h[r] = to_bits16<DT>(from_bits16<DT>(to_bits16<DT>(gr / (1.0f + expf(-gr)))) * ur);
   }
-  uint16_t* y = static_cast<uint16_t*>(L.y) + static_cast<int64_t>(m) * L.ldy + n;
-  *reinterpret_cast<uint64_t*>(y) = (static_cast<uint64_t>(h[0]) | (static_cast<uint64_t>(h[1]) << 16)) |
-                                    ((static_cast<uint64_t>(h[2]) | (static_cast<uint64_t>(h[3]) << 16)) << 32);
+  uint64_t* y = reinterpret_cast<uint64_t*>(static_cast<uint16_t*>(L.y) + static_cast<int64_t>(m) * L.ldy + n);
+  const uint64_t bits = (static_cast<uint64_t>(h[0]) | (static_cast<uint64_t>(h[1]) << 16)) |
+                        ((static_cast<uint64_t>(h[2]) | (static_cast<uint64_t>(h[3]) << 16)) << 32);
+  if (L.consumed)
+    publish(y, bits);  // a later linear of the chain reads it
+  else
+    *y = bits;
 }
 
 // kEpiAct end of an item for a K-split workgroup (the wavefronts' tiles already in LDS): each
@@ -606,8 +610,10 @@ __device__ __forceinline__ void packed_finish(const PackedArgs& a, const PLinear
   int tile, s;
   item_tile(item, L.split, tile, s);
   if constexpr (EPI == kEpiAct) {
-    packed_finish_act<DT, MT, NF, KW>(a, L, M, tile, s, wave, lane, red, last_flag);
-    return;
+    if (L.out_f32 == PLM_OUT_SILU_MUL) {
+      packed_finish_act<DT, MT, NF, KW>(a, L, M, tile, s, wave, lane, red, last_flag);
+      return;
+    }
   }
   const int n0 = tile * NF * 16;
   f32x4 sum[(Q + KW - 1) / KW];
@@ -701,7 +707,7 @@ __device__ __forceinline__ void packed_finish_rows(const PackedArgs& a, const PL
     if constexpr (EPI == kEpiLora) {
       if (L.role == 2) lora_wait_h(a, lane, probe);
     }
-    if constexpr (EPI == kEpiAct) {
+    if (EPI == kEpiAct && L.out_f32 == PLM_OUT_SILU_MUL) {
 #pragma unroll
       for (int j = 0; j < NF / 2; ++j)
 #pragma unroll
@@ -740,7 +746,7 @@ __device__ __forceinline__ void packed_finish_rows(const PackedArgs& a, const PL
   if constexpr (EPI == kEpiLora) {
     if (L.role == 2) lora_wait_h(a, lane, probe);
   }
-  if constexpr (EPI == kEpiAct) {
+  if (EPI == kEpiAct && L.out_f32 == PLM_OUT_SILU_MUL) {
     // Each of the wavefront's (gate, up) pairs: both partials summed in split order.
 #pragma unroll 1
     for (int pw = 0; pw < QW / 2; ++pw) {
@@ -869,10 +875,11 @@ __device__ __forceinline__ void wait_producer_tiles(const PackedArgs& a, const P
     }
   }
   if (lo >= hi || chain_failed(a)) return;
-  constexpr int kCols = 16 * tile_frags<NF, KW>();  // Y columns of one producer tile
-  constexpr int kLineCols = 64;                      // bf16 columns of a 128-byte line
-  const int t0 = max(32 * lo - (kLineCols - 1), 0) / kCols;
-  const int t1 = min((32 * hi - 1 + (kLineCols - 1)) / kCols, P.tiles - 1);
+  // Y columns of one producer tile (half its rows when its epilogue is the SiLU-and-multiply)
+  const int cols = P.out_f32 == PLM_OUT_SILU_MUL ? 8 * tile_frags<NF, KW>() : 16 * tile_frags<NF, KW>();
+  constexpr int kLineCols = 64;  // bf16 columns of a 128-byte line
+  const int t0 = max(32 * lo - (kLineCols - 1), 0) / cols;
+  const int t1 = min((32 * hi - 1 + (kLineCols - 1)) / cols, P.tiles - 1);
   const auto frs = make_rsrc(P.flag, static_cast<uint32_t>(P.tiles) * 8u);
   for (int i = 0;; ++i) {
     bool done = true;

@@ -17,6 +17,7 @@ LIBRARY = Path(__file__).resolve().parent / "libplm_amd.so"
 PLM_BF16, PLM_F16 = 0, 1
 PLM_ROUND_F32, PLM_ROUND_BF16, PLM_ROUND_F16 = 0, 1, 2
 PLM_RULE_NUCLEUS, PLM_RULE_FLOOR = 0, 1
+PLM_OUT_MODEL, PLM_OUT_F32, PLM_OUT_SILU_MUL = 0, 1, 2   # plm_chain_gemm.out_f32
 DTYPE_CODES = {torch.bfloat16: PLM_BF16, torch.float16: PLM_F16}
 # PLM_WORKSPACE_COUNTER_BYTES: the zero-between-calls counter area at the start of every workspace.
 COUNTER_BYTES = 1 << 18

@@ -18,19 +18,23 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .fast_gemm import Config, HALF_DTYPES, _tile, packed_weight, row_major_weight, workspace
+from .fast_gemm import Config, HALF_DTYPES, _tile, packed_gate_up, packed_weight, row_major_weight, workspace
 
 
 @dataclass
 class Link:
     """One linear of a chain: ``y = x @ w.T``. ``dep`` is the index of the earlier link whose ``y``
-    this ``x`` is (its leading ``K`` columns), or -1 when ``x`` comes from outside the chain."""
+    this ``x`` is (its leading ``K`` columns), or -1 when ``x`` comes from outside the chain.
+    ``act`` (packed chains): ``w`` is a fused gate/up weight ``[2I, K]`` and ``y`` ``[M, I]`` gets
+    ``silu(gate) * up`` (``fast_gemm.gate_up_silu``'s result); the chain's tile needs an even
+    ``wave_frags``."""
 
     x: torch.Tensor
     w: torch.Tensor
     y: torch.Tensor
     dep: int = -1
     split_k: int = 1
+    act: bool = False
 
 
 class LinearChain:
@@ -56,16 +60,20 @@ class LinearChain:
                     raise ValueError(f"link {i}: {name} must be a row-major {self.dtype} matrix on {self.device}")
             if ln.x.shape[0] != self.M or ln.y.shape[0] != self.M or ln.x.shape[1] != ln.w.shape[1]:
                 raise ValueError(f"link {i}: shapes x{tuple(ln.x.shape)} w{tuple(ln.w.shape)} y{tuple(ln.y.shape)}")
-            if ln.y.shape[1] != ln.w.shape[0] or ln.y.stride(1) != 1 or ln.y.device != self.device:
-                raise ValueError(f"link {i}: y must be a row-major [{self.M},{ln.w.shape[0]}] matrix")
-            if ln.y.dtype not in (self.dtype, torch.float32):
-                raise TypeError(f"link {i}: y must be {self.dtype} or float32")
+            cols = ln.w.shape[0] // 2 if ln.act else ln.w.shape[0]
+            if ln.y.shape[1] != cols or ln.y.stride(1) != 1 or ln.y.device != self.device:
+                raise ValueError(f"link {i}: y must be a row-major [{self.M},{cols}] matrix")
+            if ln.y.dtype not in ((self.dtype,) if ln.act else (self.dtype, torch.float32)):
+                raise TypeError(f"link {i}: y must be {self.dtype}" + ("" if ln.act else " or float32"))
+            if ln.act and not packed:
+                raise ValueError(f"link {i}: the SiLU-and-multiply epilogue needs a packed chain")
             g = arr[i]
-            g.x, g.w, g.y = ln.x.data_ptr(), (packed_weight(ln.w) if packed else row_major_weight(ln.w)).data_ptr(), ln.y.data_ptr()
+            wp = packed_gate_up(ln.w) if ln.act else (packed_weight(ln.w) if packed else row_major_weight(ln.w))
+            g.x, g.w, g.y = ln.x.data_ptr(), wp.data_ptr(), ln.y.data_ptr()
             g.ldx, g.ldw, g.ldy = ln.x.stride(0), ln.w.stride(0), ln.y.stride(0)
             g.N, g.K = ln.w.shape[0], ln.w.shape[1]
             g.split_k, g.dep = ln.split_k, ln.dep
-            g.out_f32 = int(ln.y.dtype == torch.float32)
+            g.out_f32 = _lib.PLM_OUT_SILU_MUL if ln.act else int(ln.y.dtype == torch.float32)
         self._tile = _tile(self.cfg)
         lib = _lib.lib()
         prepare = lib.plm_gemm_chain_packed_prepare if packed else lib.plm_gemm_chain_prepare
