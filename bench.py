@@ -51,7 +51,7 @@ def parse_args():
     ap.add_argument("--only-round", action="store_true", help="time the round only (for profiling runs)")
     ap.add_argument("--no-voronoi", action="store_true", help="skip the verify rows' auxiliary decode timing")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-width timing")
-    ap.add_argument("--profile", choices=("eager", "copy", "verify", "voronoi", "lora"),
+    ap.add_argument("--profile", choices=("eager", "copy", "verify", "voronoi", "lora", "act"),
                     help="no JSON: 'eager' launches the round and the fused verify step --steps times without a "
                          "graph (for rocprofv3 counter runs); 'copy' runs a 1 GiB device copy, the reference "
                          "kernel that scales the HBM byte counters; 'verify' runs the fused verify step and the "
@@ -298,6 +298,9 @@ def main():
         return
     if args.profile == "lora":
         profile_lora(args, device)
+        return
+    if args.profile == "act":
+        profile_act(args, device)
         return
     tables = gemm_tables.read_table(args.hidden)
     gemms = [g for _ in range(args.layers) for g in gpt_block(args.hidden, args.mlp)]
@@ -661,6 +664,42 @@ def profile_lora(args, device):
         hip_linear(x, sets[i % len(sets)][0], cfg)
     torch.cuda.synchronize()
     print(f"[bench] gated LoRA x {max(1, args.steps)}, base GEMM {cfg} x {max(1, args.steps)}", file=sys.stderr)
+
+
+def profile_act(args, device):
+    """The Llama-style 1.3B MLP (gate_up 2048 -> 2 x 5632, down 5632 -> 2048) at width M, eager,
+    rotating over 8 weight sets (552 MB): the fused gate/up + SiLU-and-multiply launch, the gate/up
+    projection alone, and the MLP as one chained launch (gate/up with its activation, then down)."""
+    import torch
+
+    from plm_amd import _lib, gemm_tables
+    from plm_amd.chain import Link, LinearChain
+    from plm_amd.fast_gemm import gate_up_silu, hip_linear
+    from plm_amd.tiles import packed_chain_split, packed_chain_tile
+
+    M, K, I = args.M, 2048, 5632
+    cfg = gemm_tables.read_table(K)[(M, 2 * I, K)]
+    gen = torch.Generator(device=device).manual_seed(78)
+    x = torch.randn(M, K, generator=gen, device=device).bfloat16()
+    sets = [((0.02 * torch.randn(2 * I, K, generator=gen, device=device)).bfloat16(),
+             (0.02 * torch.randn(K, I, generator=gen, device=device)).bfloat16()) for _ in range(8)]
+    ccfg = packed_chain_tile(M)
+    G = _lib.lib().plm_gemm_packed_resident_workgroups(_lib.PLM_BF16, M, _lib.Tile.from_config(ccfg))
+    _lib.check(min(G, 0), "plm_gemm_packed_resident_workgroups")
+    act = torch.empty(M, I, device=device, dtype=torch.bfloat16)
+    out = torch.empty(M, K, device=device, dtype=torch.bfloat16)
+    chains = [LinearChain([Link(x, wg, act, -1, packed_chain_split(2 * I, K, ccfg, G), True),
+                           Link(act, wd, out, 0, packed_chain_split(K, I, ccfg, G))], ccfg) for wg, wd in sets]
+    n = max(1, args.steps)
+    for i in range(n):
+        gate_up_silu(x, sets[i % 8][0], cfg)
+    for i in range(n):
+        hip_linear(x, sets[i % 8][0], cfg)
+    for i in range(n):
+        chains[i % 8].run()
+    torch.cuda.synchronize()
+    chains[0].check()
+    print(f"[bench] gate_up_silu {cfg} x {n}, gate_up GEMM x {n}, MLP chain {ccfg} x {n}", file=sys.stderr)
 
 
 def time_llama_rounds(args, device):

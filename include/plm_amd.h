@@ -198,7 +198,7 @@ typedef struct plm_chain_gemm {
  * `w` a packed weight (ldw is ignored). After every linear whose Y a later one reads, all
  * workgroups meet at a grid barrier, so such a linear must not write fp32. The tile gives
  * wave_frags, k_waves and unroll for every linear; each linear's split_k is its own. The launch
- * (the chain kernel and a one-thread kernel that advances the workspace's launch epoch) needs
+ * (one kernel; its last workgroup to finish advances the workspace's launch epoch) needs
  * every workgroup resident at once (the device to itself while it runs); a barrier that does not
  * complete in about a second sets the int at PLM_WORKSPACE_ERROR_INDEX to 1.
  * plm_gemm_chain_packed_prepare fills the derived fields and returns the workspace bytes.

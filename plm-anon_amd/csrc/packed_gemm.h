@@ -35,8 +35,8 @@
 // workgroup: launch epoch and the number of such linears it has finished, so flags only grow and
 // need no reset). It requests the next linear's first weight fragments, so the weight stream
 // overlaps the wait, and then polls every workgroup's flag until all have finished the linear: a
-// grid barrier made of plain stores and loads, with no contended atomic. The epoch is advanced by
-// a one-thread kernel after every chained launch. All workgroups of a chained launch are resident
+// grid barrier made of plain stores and loads, with no contended atomic. The last workgroup to
+// finish a chained launch advances the epoch (chain_exit). All workgroups of a chained launch are resident
 // at once; every wait is bounded and sets the error flag if it gives up.
 //
 // Results are bitwise reproducible run to run: every sum has a fixed order (K steps ascending
@@ -67,6 +67,7 @@ constexpr int kPkMaxWorkgroups = 2048;  // progress flags: int64 per workgroup a
 constexpr int kPkTileFlags = 1024;
 constexpr int kPkLoraHDone = 12;   // gated-LoRA launch: tiles of h written
 constexpr int kPkLoraPast = 13;    // gated-LoRA launch: base tiles past their wait for h
+constexpr int kPkExitSlot = 14;    // chained launch: workgroups that have finished it
 
 // Gated low-rank correction inside one launch (plm_gemm_packed_lora, plm/gated_lora.py:45-57):
 // linear 0 forms h = X A^T in the model dtype for every row (each tile counts itself in once
@@ -900,13 +901,18 @@ __device__ __forceinline__ void wait_producer_tiles(const PackedArgs& a, const P
   }
 }
 
-// Advances the packed-chain epoch after a chained launch (the next launch's flags then exceed
-// every flag of this one).
-template <int kUnused = 0>  // a template, so that every translation unit may instantiate it
-__global__ void packed_epoch_kernel(int* counters) {
+// End of a chained launch: the last workgroup to finish advances the epoch, so that the next
+// launch's flags exceed every flag of this one. Every workgroup reads the epoch when it starts and
+// counts itself out only after all its wavefronts are past the end, so no workgroup of this
+// launch reads the advanced value; the counter is left at zero for the next launch.
+__device__ __forceinline__ void chain_exit(const PackedArgs& a) {
+  __syncthreads();
   if (threadIdx.x == 0) {
-    int64_t* epoch = reinterpret_cast<int64_t*>(counters + kPkEpochSlot);
-    publish(epoch, collect(epoch) + 1);
+    if (__hip_atomic_fetch_add(a.counters + kPkExitSlot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.G - 1) {
+      __hip_atomic_store(a.counters + kPkExitSlot, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      int64_t* epoch = reinterpret_cast<int64_t*>(a.counters + kPkEpochSlot);
+      publish(epoch, collect(epoch) + 1);
+    }
   }
 }
 
@@ -1082,6 +1088,7 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
     }
   }
   __builtin_amdgcn_s_waitcnt(0);
+  if (a.sync) chain_exit(a);
 }
 
 // Compiled configurations (all without scratch): 1 <= MT <= 8, NF in {1, 2, 4}, D in
@@ -1149,7 +1156,6 @@ hipError_t packed_launch(PackedArgs& a, int cus, hipStream_t stream, bool dry) {
     a.G = a.sync ? resident : min(a.G, resident);
     if (a.G < 1) return hipErrorInvalidConfiguration;
     hipLaunchKernelGGL(kern, dim3(a.G), dim3(64 * packed_waves<KW>()), lds, stream, a);
-    if (a.sync) hipLaunchKernelGGL(packed_epoch_kernel<>, dim3(1), dim3(64), 0, stream, a.counters);
     return hipGetLastError();
   }
 }
