@@ -153,6 +153,44 @@ def test_packed_argument_validation_happens_before_launch():
     assert lib.plm_gemm_chain_packed_prepare(arr, 2, 56, tile) == -1
 
 
+def test_silu_mul_argument_validation_happens_before_launch():
+    """plm_gemm_packed_silu_mul and chain links with the SiLU-and-multiply epilogue (out_f32 =
+    PLM_OUT_SILU_MUL) refuse what the epilogue cannot do, before touching the device."""
+    lib = _lib.lib()
+    fake = 1 << 20
+    tile = _lib.Tile(2, 8, 1, 2)
+
+    def silu(N, t=tile, ldy=None, y=fake, M=56):
+        return lib.plm_gemm_packed_silu_mul(0, fake, 2048, fake, y, N // 2 if ldy is None else ldy, M, N, 2048, t,
+                                            None, 0, None)
+
+    assert silu(11264 + 16) == -1                       # N not a multiple of 32
+    assert silu(16) == -1                               # fewer than one gate/up pair of fragments
+    assert silu(11264, t=_lib.Tile(1, 8, 1, 2)) == -1   # wave_frags 1: gate and up unpaired
+    assert silu(11264, ldy=5631) == -1                  # ldy below N/2
+    assert silu(11264, ldy=5634) == -1                  # ldy not a multiple of 4
+    assert silu(11264, y=fake + 2) == -2                # Y not 8-byte aligned
+    assert silu(11264, M=129) == -1                     # the skinny kernel's widths only
+    assert silu(11264, t=_lib.Tile(2, 8, 1, 3)) == -3   # no such pipeline depth
+    # Chains: an act link needs an even wave_frags, and its reader's K is at most N/2.
+    arr = (_lib.ChainGemm * 2)()
+    arr[0].x, arr[0].w, arr[0].y, arr[0].ldx, arr[0].ldw, arr[0].ldy = fake, 1 << 33, 1 << 24, 2048, 2048, 5632
+    arr[0].N, arr[0].K, arr[0].split_k, arr[0].dep, arr[0].out_f32 = 11264, 2048, 1, -1, _lib.PLM_OUT_SILU_MUL
+    arr[1].x, arr[1].w, arr[1].y, arr[1].ldx, arr[1].ldw, arr[1].ldy = 1 << 24, 1 << 34, 1 << 26, 5632, 5632, 2048
+    arr[1].N, arr[1].K, arr[1].split_k, arr[1].dep = 2048, 5632, 1, 0
+
+    def chain(t):
+        need = lib.plm_gemm_chain_packed_prepare(arr, 2, 56, t)
+        assert need > 0
+        return lib.plm_gemm_chain_packed(0, arr, fake, 2, 56, t, None, 0, None)
+
+    assert chain(tile) == -4                            # valid: it stops at the missing workspace
+    assert chain(_lib.Tile(1, 8, 1, 2)) == -1
+    arr[1].K = arr[1].ldw = 5664                        # reads past the activation's 5632 columns
+    arr[1].ldx = 5664
+    assert chain(tile) == -1
+
+
 def test_packed_sizes_and_chain_prepare():
     lib = _lib.lib()
     # Fragments of 16 rows x 32 K: N and K round up.
