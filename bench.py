@@ -364,6 +364,17 @@ def main():
     print(f"[bench] per-GEMM graph round: {us_graph:.1f} us, {rnd.bytes / (us_graph * 1e-6) / 1e9:.0f} GB/s",
           file=sys.stderr, flush=True)
 
+    # For comparison only (not a path of this build): the same 97 linears through the vendor
+    # library (torch F.linear -> hipBLASLt) on the row-major weights, one graph.
+    us_blas = None
+    if not args.only_round:
+        graph = capture_graph(lambda: [torch.nn.functional.linear(x, w)
+                                       for x, w in zip(rnd.inputs, rnd.weights)])
+        us_blas = time_graph(graph, args.steps, args.warmup) * 1000.0
+        del graph
+        print(f"[bench] the same round through hipBLASLt (F.linear, row-major weights): {us_blas:.1f} us",
+              file=sys.stderr, flush=True)
+
     # value: the faster of the two complete implementations of the round (both verified above:
     # the chain bit for bit against the per-linear launches, those against the oracle in the tests).
     chain_wins = us_round <= us_graph
@@ -389,6 +400,10 @@ def main():
         "per_gemm_graph": {"us": round(us_graph, 2), "gbps": round(rnd.bytes / (us_graph * 1e-6) / 1e9, 1),
                            "launches": len(gemms)},
     }
+    if us_blas is not None:
+        result["hipblaslt_round"] = {"us": round(us_blas, 2), "gbps": round(rnd.bytes / (us_blas * 1e-6) / 1e9, 1),
+                                     "note": "comparison only: the 97 linears as torch F.linear (hipBLASLt) on "
+                                             "row-major weights, one graph; not a path of this build"}
     if not args.only_round:
         rows = dominant_kernel_roofline(rnd, args.steps)
         result["per_gemm_kernels"] = [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}
