@@ -60,6 +60,20 @@ def test_gate_up_silu_matches_the_two_launches(device, M, I, K, cfg):
     assert bool(ok.all()), float(diff.max())
 
 
+@pytest.mark.parametrize("M,I,K", [(1, 16, 64), (128, 48, 1416), (17, 1008, 200), (64, 2048, 8192)])
+def test_edge_shapes_default_tile(device, M, I, K):
+    """One row and the widest skinny width, the smallest pair of fragments (I = 16), K past the
+    last 32-element step (1416, 200), a long K; the tile gate_up_silu picks by default."""
+    g = torch.Generator(device=device).manual_seed(M * 7 + I + K)
+    x = torch.randn(M, K, generator=g, device=device).bfloat16()
+    w = (0.03 * torch.randn(2 * I, K, generator=g, device=device)).bfloat16()
+    got = gate_up_silu(x, w)
+    ref = oracle.silu_mul(oracle.linear(x.cpu(), w.cpu())).float()
+    diff = (got.cpu().float() - ref).abs()
+    ok = (diff <= 2e-2 + 1e-3 * ref.abs()) | (_steps(got.cpu().float(), ref, torch.bfloat16) <= 2.0001)
+    assert bool(ok.all()), float(diff.max())
+
+
 def test_fp16_wide_rows_and_released_weight(device):
     g = torch.Generator(device=device).manual_seed(5)
     I, K = 1024, 1024
