@@ -325,15 +325,20 @@ __device__ __forceinline__ void packed_offsets(const PLinear& L, int M, int lane
   }
 }
 
-// Loads the weight half of one pipeline stage (the cursor's K step).
+// Loads the weight half of one pipeline stage (the cursor's K step). The cursor is the same in
+// every lane of a wavefront; its offset goes to the load's scalar operand through readfirstlane,
+// so that the compiler, which cannot always prove the cursor uniform, does not wrap each load in a
+// loop over the lanes' distinct values (such loops also leave its load-count waits conservative:
+// a full drain of the pipeline once per D steps).
 template <int NF>
 __device__ __forceinline__ void issue_w(__amdgpu_buffer_rsrc_t wr, const PCursor& c, int items,
                                         const uint32_t (&wo)[NF], u32x4 (&wb)[NF]) {
   const bool live = c.item < items && c.st < c.end;
-  const uint32_t ws = live ? static_cast<uint32_t>(c.wbase + c.st * kFragBytes) : kNoLoad;
+  const int ws = __builtin_amdgcn_readfirstlane(
+      static_cast<int>(live ? static_cast<uint32_t>(c.wbase + c.st * kFragBytes) : kNoLoad));
 #pragma unroll
   for (int f = 0; f < NF; ++f)
-    wb[f] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, wo[f], static_cast<int>(ws), 0));
+    wb[f] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, wo[f], ws, 0));
 }
 
 // Loads the X half of one pipeline stage. X lanes past K in the last step load zeros (the packed
@@ -342,12 +347,11 @@ template <int MT, int NF, int XN>
 __device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t xr, const PCursor& c, int items, int Ks,
                                         const POffsets<MT, NF, XN>& o, u32x4 (&xb)[XN]) {
   const bool live = c.item < items && c.st < c.end;
-  const uint32_t xs = live ? static_cast<uint32_t>(c.st * 64) : kNoLoad;
+  const int xs = __builtin_amdgcn_readfirstlane(static_cast<int>(live ? static_cast<uint32_t>(c.st * 64) : kNoLoad));
   const bool last = c.st == Ks - 1;
 #pragma unroll
   for (int t = 0; t < XN; ++t)
-    xb[t] = __builtin_bit_cast(
-        u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, last ? o.xo_last[t] : o.xo[t], static_cast<int>(xs), 0));
+    xb[t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, last ? o.xo_last[t] : o.xo[t], xs, 0));
 }
 
 // Four columns n..n+3 of Y row m (fewer at N's end); written through to the device-coherent level
@@ -845,10 +849,9 @@ __device__ __forceinline__ void warm_weights(const PLinear& Ln, int G, int wave,
                                              __amdgpu_buffer_rsrc_t wr, const uint32_t* wo, PkLdsVoid* dst) {
   for (int n = 0; n < kWarmFragments / NF && nx.item < Ln.items; ++n) {
     if (nx.st < nx.end) {
-      const uint32_t ws = static_cast<uint32_t>(nx.wbase + nx.st * kFragBytes);
+      const int ws = __builtin_amdgcn_readfirstlane(static_cast<int>(nx.wbase + nx.st * kFragBytes));
 #pragma unroll
-      for (int f = 0; f < NF; ++f)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, dst, 16, wo[f], static_cast<int>(ws), 0, 0);
+      for (int f = 0; f < NF; ++f) __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, dst, 16, wo[f], ws, 0, 0);
     }
     pc_advance<NF, D, KW>(Ln, G, wave, nx);
   }
@@ -1021,36 +1024,44 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
         for (int f = 0; f < NF; ++f)
 #pragma unroll
           for (int t = 0; t < MT; ++t) acc[f][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-        const int steps = cp.pend - cp.st;  // a multiple of D
-        for (int i = 0; i < steps; i += D) {
+        const int steps = cp.pend - cp.st;  // a multiple of D, at least D
+        // One pipeline stage: stage j's X into the MFMA operand layout, its MFMAs, then stage j's
+        // loads for D steps ahead.
+        auto stage = [&](int j) __attribute__((always_inline)) {
+          u32x4 xop[MT];
+          if constexpr (KW != 1) {
 #pragma unroll
-          for (int j = 0; j < D; ++j) {
-            u32x4 xop[MT];
-            if constexpr (KW != 1) {
+            for (int t = 0; t < MT; ++t) *reinterpret_cast<u32x4*>(xt + t * kXTileBytes + xt_write) = xb[j][t];
 #pragma unroll
-              for (int t = 0; t < MT; ++t) *reinterpret_cast<u32x4*>(xt + t * kXTileBytes + xt_write) = xb[j][t];
+            for (int t = 0; t < MT; ++t) xop[t] = *reinterpret_cast<const u32x4*>(xt + t * kXTileBytes + xt_read);
+          } else {
+            // Stage j's X tile set (j alternates parity: D is even and items pad to a multiple).
+            char* xs = xt + (j & 1) * MT * kXTileBytes;
 #pragma unroll
-              for (int t = 0; t < MT; ++t) xop[t] = *reinterpret_cast<const u32x4*>(xt + t * kXTileBytes + xt_read);
-            } else {
-              // Stage j's X tile set (j alternates parity: D is even and items pad to a multiple).
-              char* xs = xt + (j & 1) * MT * kXTileBytes;
+            for (int i = 0; i < XN; ++i)
+              if (wave + 4 * i < MT) *reinterpret_cast<u32x4*>(xs + (wave + 4 * i) * kXTileBytes + xt_write) = xb[j][i];
+            lds_sync();
 #pragma unroll
-              for (int i = 0; i < XN; ++i)
-                if (wave + 4 * i < MT)
-                  *reinterpret_cast<u32x4*>(xs + (wave + 4 * i) * kXTileBytes + xt_write) = xb[j][i];
-              lds_sync();
-#pragma unroll
-              for (int t = 0; t < MT; ++t) xop[t] = *reinterpret_cast<const u32x4*>(xs + t * kXTileBytes + xt_read);
-            }
-#pragma unroll
-            for (int f = 0; f < NF; ++f)
-#pragma unroll
-              for (int t = 0; t < MT; ++t) acc[f][t] = mfma_16x16x32<DT>(wb[j][f], xop[t], acc[f][t]);
-            issue_w<NF>(wr, ld, L.items, o.wo, wb[j]);
-            issue_x<MT, NF, XN>(xr, ld, L.items, L.Ks, o, xb[j]);
-            pc_advance<NF, D, KW>(L, a.G, wave, ld);
-            __builtin_amdgcn_sched_barrier(0);
+            for (int t = 0; t < MT; ++t) xop[t] = *reinterpret_cast<const u32x4*>(xs + t * kXTileBytes + xt_read);
           }
+#pragma unroll
+          for (int f = 0; f < NF; ++f)
+#pragma unroll
+            for (int t = 0; t < MT; ++t) acc[f][t] = mfma_16x16x32<DT>(wb[j][f], xop[t], acc[f][t]);
+          issue_w<NF>(wr, ld, L.items, o.wo, wb[j]);
+          issue_x<MT, NF, XN>(xr, ld, L.items, L.Ks, o, xb[j]);
+          pc_advance<NF, D, KW>(L, a.G, wave, ld);
+          __builtin_amdgcn_sched_barrier(0);
+        };
+        // The item's first D steps are peeled off the loop: the loop is then entered only from a
+        // block that leaves the loads in flight in the loop's own order, so the compiler's
+        // load-count waits inside it stay exact (entered straight from the item's start, where
+        // paths with other load orders meet, it waited for every load once per D steps).
+#pragma unroll
+        for (int j = 0; j < D; ++j) stage(j);
+        for (int i = D; i < steps; i += D) {
+#pragma unroll
+          for (int j = 0; j < D; ++j) stage(j);
         }
         if constexpr (KW != 1)
           packed_finish<DT, MT, NF, KW, EPI>(a, L, a.M, cp.item, wave, lane, acc, red, &last_flag);
