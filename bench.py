@@ -69,6 +69,7 @@ class Round:
     def __init__(self, M, hidden, mlp, layers, weights, tables, device, gemms=None, act=False):
         import torch
 
+        from plm_amd import gemm_tables
         from plm_amd.workloads import GPT2_VOCAB, gpt_block
 
         self.M = M
@@ -79,9 +80,12 @@ class Round:
         self.weights = weights
         self.cfgs = [tables[(M, g.N, g.K)] for g in self.gemms]
         self.act = [act and gm.name == "gate_up" for gm in self.gemms]
+        act_tables = gemm_tables.read_act_table(hidden) if act else {}
         for i, a in enumerate(self.act):
-            if a and self.cfgs[i]["wave_frags"] % 2:
-                self.cfgs[i] = dict(self.cfgs[i], wave_frags=2)   # gate and up fragments in pairs
+            if a:   # the fastest tile whose gate and up fragments pair up
+                self.cfgs[i] = act_tables.get((M, self.gemms[i].N, self.gemms[i].K), self.cfgs[i])
+                if self.cfgs[i]["wave_frags"] % 2:
+                    self.cfgs[i] = dict(self.cfgs[i], wave_frags=2)
         g = torch.Generator(device=device).manual_seed(3000 + M)
         self.x0 = torch.randn(M, hidden, generator=g, device=device).bfloat16()
         self.outs = [torch.empty(M, gm.N // 2 if a else gm.N, device=device, dtype=torch.bfloat16)
@@ -841,6 +845,7 @@ def time_gate_up_silu(args, device):
     M, K, I = args.M, 2048, 5632
     N = 2 * I
     cfg = gemm_tables.read_table(K)[(M, N, K)]
+    act_cfg = gemm_tables.read_act_table(K).get((M, N, K), cfg)
     gen = torch.Generator(device=device).manual_seed(78)
     x = torch.randn(M, K, generator=gen, device=device).bfloat16()
     ws = [(0.02 * torch.randn(N, K, generator=gen, device=device)).bfloat16() for _ in range(8)]  # 8 x 46 MB
@@ -850,7 +855,7 @@ def time_gate_up_silu(args, device):
         return F.silu(y[:, :I]) * y[:, I:]
 
     res = {}
-    for name, fn in (("fused_us", lambda w: gate_up_silu(x, w, cfg)), ("gemm_then_act_us", separate),
+    for name, fn in (("fused_us", lambda w: gate_up_silu(x, w, act_cfg)), ("gemm_then_act_us", separate),
                      ("gemm_alone_us", lambda w: hip_linear(x, w, cfg))):
         for w in ws:
             fn(w)
@@ -863,7 +868,7 @@ def time_gate_up_silu(args, device):
         res[name] = round(time_graph(graph, max(5, args.steps // 4), 2) * 1000.0 / len(ws), 2)
         del graph
     print(f"[bench] gate_up + SiLU-and-multiply: {res}", file=sys.stderr, flush=True)
-    return dict(res, shape=f"M={M} N={N} K={K}")
+    return dict(res, shape=f"M={M} N={N} K={K}", fused_tile=act_cfg, gemm_tile=cfg)
 
 
 def time_prefill(args, device, block_weights):

@@ -355,7 +355,9 @@ __device__ __forceinline__ void own_logit_wave(const VerifyArgs& a, int r, int l
     if (lane == 0) publish(a.own + r, NAN);
     return;
   }
-  const int pid = static_cast<int>(pid64);
+  // The same in every lane (row r is the wavefront's): made a scalar so that the weight's buffer
+  // resource is one, and its loads are not wrapped in loops over the lanes' values.
+  const int pid = __builtin_amdgcn_readfirstlane(static_cast<int>(pid64));
   const int Ks = (a.K + 31) >> 5;
   const int k_last = a.K - 32 * (Ks - 1);
   // The packed fragment row (16 vocabulary rows) holding pid, and row r's X fragment in the MFMA
@@ -640,27 +642,32 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D
       for (int f = 0; f < NF; ++f)
 #pragma unroll
         for (int t = 0; t < MT; ++t) acc[f][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const int steps = cp.pend - cp.st;  // a multiple of D
-      for (int i = 0; i < steps; i += D) {
+      const int steps = cp.pend - cp.st;  // a multiple of D, at least D
+      auto stage = [&](int j) __attribute__((always_inline)) {
+        u32x4 xop[MT];
+        char* xs = xt + (j & 1) * MT * kXTileBytes;
 #pragma unroll
-        for (int j = 0; j < D; ++j) {
-          u32x4 xop[MT];
-          char* xs = xt + (j & 1) * MT * kXTileBytes;
+        for (int q = 0; q < XN; ++q)
+          if (wave + 4 * q < MT) *reinterpret_cast<u32x4*>(xs + (wave + 4 * q) * kXTileBytes + xt_write) = xb[j][q];
+        lds_sync();
 #pragma unroll
-          for (int q = 0; q < XN; ++q)
-            if (wave + 4 * q < MT) *reinterpret_cast<u32x4*>(xs + (wave + 4 * q) * kXTileBytes + xt_write) = xb[j][q];
-          lds_sync();
+        for (int t = 0; t < MT; ++t) xop[t] = *reinterpret_cast<const u32x4*>(xs + t * kXTileBytes + xt_read);
 #pragma unroll
-          for (int t = 0; t < MT; ++t) xop[t] = *reinterpret_cast<const u32x4*>(xs + t * kXTileBytes + xt_read);
+        for (int f = 0; f < NF; ++f)
 #pragma unroll
-          for (int f = 0; f < NF; ++f)
+          for (int t = 0; t < MT; ++t) acc[f][t] = mfma_16x16x32<DT>(wb[j][f], xop[t], acc[f][t]);
+        issue_w<NF>(wr, ld, L.items, o.wo, wb[j]);
+        issue_x<MT, NF, XN>(xr, ld, L.items, L.Ks, o, xb[j]);
+        pc_advance<NF, D, KW>(L, a.G, wave, ld);
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      // The first D steps peeled off the loop, as in packed_gemm_kernel: the loop is entered only
+      // with its own load order in flight, so its load-count waits stay exact.
 #pragma unroll
-            for (int t = 0; t < MT; ++t) acc[f][t] = mfma_16x16x32<DT>(wb[j][f], xop[t], acc[f][t]);
-          issue_w<NF>(wr, ld, L.items, o.wo, wb[j]);
-          issue_x<MT, NF, XN>(xr, ld, L.items, L.Ks, o, xb[j]);
-          pc_advance<NF, D, KW>(L, a.G, wave, ld);
-          __builtin_amdgcn_sched_barrier(0);
-        }
+      for (int j = 0; j < D; ++j) stage(j);
+      for (int i = D; i < steps; i += D) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) stage(j);
       }
       // Fold this wavefront's 16*NF columns into the row states (rounding mode resolved once per
       // item, not per element).

@@ -35,6 +35,9 @@ Config = dict[str, int]
 HALF_DTYPES = (torch.bfloat16, torch.float16)
 
 CONFIGS: dict[tuple[int, int, int], Config] = {}
+# Tiles for the fused gate/up projection with its SiLU-and-multiply (gate_up_silu), keyed like
+# CONFIGS: the fastest tile with an even wave_frags (gemm_tables.install fills it).
+ACT_CONFIGS: dict[tuple[int, int, int], Config] = {}
 
 _tiles: dict[tuple[int, int, int, int], _lib.Tile] = {}
 # weight tensor -> ((data_ptr, shape, row stride, version counter), packed copy); entries go with
@@ -233,8 +236,9 @@ def gate_up_silu(x: torch.Tensor, w: torch.Tensor, cfg: Config | None = None,
     ``[M, I]`` in x's dtype, in one launch (``plm_gemm_packed_silu_mul``): the Llama-style MLP's
     gate_up_proj GEMM (routed through plm/fast_gemm.py:104-110) and the ``SiluAndMul`` vLLM runs on
     its output as a second launch, with the same roundings (the projection's output rounded to the
-    model dtype, silu rounded, then the product). ``cfg``: the tile (wave_frags 2 or 4); by default
-    the projection's tuned tile, with wave_frags 2 where it has 1. Widths above 128 rows run as the
+    model dtype, silu rounded, then the product). ``cfg``: the tile, by default ``ACT_CONFIGS``'
+    (the fastest even-wave_frags tile the tuner found) or the projection's; a tile with
+    wave_frags 1 runs with 2. Widths above 128 rows run as the
     projection then the activation, each as its own launch."""
     _check_operands(x, w)
     M, K = x.shape
@@ -248,9 +252,9 @@ def gate_up_silu(x: torch.Tensor, w: torch.Tensor, cfg: Config | None = None,
             return out
         return act
     if cfg is None:
-        cfg = CONFIGS.get((M, N, K)) or default_config(M, N, K)
-        if cfg["wave_frags"] % 2:
-            cfg = dict(cfg, wave_frags=2)
+        cfg = ACT_CONFIGS.get((M, N, K)) or CONFIGS.get((M, N, K)) or default_config(M, N, K)
+    if cfg["wave_frags"] % 2:
+        cfg = dict(cfg, wave_frags=2)   # gate and up fragments pair up in a wavefront's or a tile's
     if out is None:
         out = torch.empty(M, half, device=x.device, dtype=x.dtype)
     elif out.shape != (M, half) or out.dtype != x.dtype or out.stride(1) != 1:
@@ -444,4 +448,5 @@ def uninstall() -> None:
     """Restore ``F.linear`` in the build's slot and forget every configured shape."""
     global default_unquantized_gemm
     CONFIGS.clear()
+    ACT_CONFIGS.clear()
     default_unquantized_gemm = _default_gemm

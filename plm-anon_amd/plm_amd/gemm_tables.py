@@ -42,6 +42,15 @@ def read_table(hidden: int) -> dict[tuple[int, int, int], dict]:
     return {tuple(int(v) for v in key.split(",")): cfg for key, cfg in json.loads(path.read_text()).items()}
 
 
+def read_act_table(hidden: int) -> dict[tuple[int, int, int], dict]:
+    """``act_tiles_hidden<hidden>.json``: per key the fastest tile with an even wave_frags, which
+    the fused gate/up projection with its SiLU-and-multiply runs (empty if there is none)."""
+    path = TABLES / f"act_tiles_hidden{hidden}.json"
+    if not path.exists():
+        return {}
+    return {tuple(int(v) for v in key.split(",")): cfg for key, cfg in json.loads(path.read_text()).items()}
+
+
 def load_table(hf_config, width: int) -> dict[tuple[int, int, int], dict]:
     """The five tiles of ``hf_config`` at round width ``width`` (plm/gemm_tables.py:30-43)."""
     path = TABLES / f"tiles_hidden{hf_config.hidden_size}.json"
@@ -60,3 +69,7 @@ def load_table(hf_config, width: int) -> dict[tuple[int, int, int], dict]:
 
 def install(hf_config, width: int) -> None:
     fast_gemm.install(load_table(hf_config, width))
+    gate_up = (width, *model_shapes(hf_config)["gate_up"])
+    act = read_act_table(hf_config.hidden_size).get(gate_up)
+    if act is not None:
+        fast_gemm.ACT_CONFIGS[gate_up] = act

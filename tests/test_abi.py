@@ -301,6 +301,29 @@ def test_tables_hold_only_compiled_tiles():
             assert fast_gemm.tile_supported(M, K, cfg), (path.name, key, cfg)
 
 
+def test_act_tables_pair_gate_and_up_fragments():
+    """act_tiles_hidden<H>.json covers every key of tiles_hidden<H>.json with a compiled tile whose
+    wave_frags is even (the SiLU-and-multiply epilogue pairs gate and up fragments), and
+    gemm_tables.install puts the gate/up projection's entry where gate_up_silu reads it."""
+    for path in sorted(gemm_tables.TABLES.glob("tiles_hidden*.json")):
+        hidden = int(path.stem.removeprefix("tiles_hidden"))
+        act = gemm_tables.read_act_table(hidden)
+        assert set(act) == set(gemm_tables.read_table(hidden)), path.name
+        for (M, N, K), cfg in act.items():
+            assert cfg["wave_frags"] % 2 == 0 and fast_gemm.tile_supported(M, K, cfg), (hidden, M, N, K, cfg)
+
+    class Cfg:   # the 1.3B Llama shapes
+        hidden_size, intermediate_size, head_dim = 2048, 5632, 64
+        num_attention_heads, num_key_value_heads, vocab_size = 32, 8, 50257
+
+    try:
+        gemm_tables.install(Cfg, 56)
+        assert fast_gemm.ACT_CONFIGS[(56, 11264, 2048)] == gemm_tables.read_act_table(2048)[(56, 11264, 2048)]
+    finally:
+        fast_gemm.uninstall()
+    assert not fast_gemm.ACT_CONFIGS
+
+
 def test_load_table_missing_hidden_size_exits():
     with pytest.raises(SystemExit, match="no tile table for hidden size 1536"):
         gemm_tables.load_table(llama(1536, 4096, 12, 12), 42)
