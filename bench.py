@@ -698,6 +698,7 @@ def profile_act(args, device):
 
     M, K, I = args.M, 2048, 5632
     cfg = gemm_tables.read_table(K)[(M, 2 * I, K)]
+    act_cfg = gemm_tables.read_act_table(K).get((M, 2 * I, K), cfg)
     gen = torch.Generator(device=device).manual_seed(78)
     x = torch.randn(M, K, generator=gen, device=device).bfloat16()
     sets = [((0.02 * torch.randn(2 * I, K, generator=gen, device=device)).bfloat16(),
@@ -711,14 +712,14 @@ def profile_act(args, device):
                            Link(act, wd, out, 0, packed_chain_split(K, I, ccfg, G))], ccfg) for wg, wd in sets]
     n = max(1, args.steps)
     for i in range(n):
-        gate_up_silu(x, sets[i % 8][0], cfg)
+        gate_up_silu(x, sets[i % 8][0], act_cfg)
     for i in range(n):
         hip_linear(x, sets[i % 8][0], cfg)
     for i in range(n):
         chains[i % 8].run()
     torch.cuda.synchronize()
     chains[0].check()
-    print(f"[bench] gate_up_silu {cfg} x {n}, gate_up GEMM x {n}, MLP chain {ccfg} x {n}", file=sys.stderr)
+    print(f"[bench] gate_up_silu {act_cfg} x {n}, gate_up GEMM {cfg} x {n}, MLP chain {ccfg} x {n}", file=sys.stderr)
 
 
 def time_llama_rounds(args, device):
