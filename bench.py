@@ -244,17 +244,17 @@ def capture_graph(fn):
 
 class ChainedRound:
     """The round as two launches: its 96 block linears chained output-to-input in one persistent
-    launch over packed weights (plm_gemm_chain_packed, each linear's K split chosen for the resident
-    grid), then the LM head (read by no later linear) as its own launch with its tuned tile, which
+    launch over packed weights (plm_gemm_chain_packed, on the chain tile measured fastest for the
+    round's hidden size and width, each linear's K split chosen for the resident grid), then the LM head (read by no later linear) as its own launch with its tuned tile, which
     streams a 206 MB weight faster than the chain's tile does."""
 
     def __init__(self, rnd):
-        from plm_amd import _lib
+        from plm_amd import _lib, gemm_tables
         from plm_amd.chain import Link, LinearChain
         from plm_amd.fast_gemm import _tile
-        from plm_amd.tiles import packed_chain_split, packed_chain_tile
+        from plm_amd.tiles import packed_chain_split
 
-        cfg = packed_chain_tile(rnd.M)
+        cfg = gemm_tables.round_chain_tile(rnd.x0.shape[1], rnd.M, act=any(rnd.act))
         G = _lib.lib().plm_gemm_packed_resident_workgroups(_lib.PLM_BF16, rnd.M, _tile(cfg))
         _lib.check(min(G, 0), "plm_gemm_packed_resident_workgroups")
         n = len(rnd.gemms) - 1

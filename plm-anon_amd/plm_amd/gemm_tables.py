@@ -51,6 +51,27 @@ def read_act_table(hidden: int) -> dict[tuple[int, int, int], dict]:
     return {tuple(int(v) for v in key.split(",")): cfg for key, cfg in json.loads(path.read_text()).items()}
 
 
+def read_chain_table(hidden: int) -> dict[int, dict]:
+    """``chain_tiles_hidden<hidden>.json``: per round width M the tile a chained round of that
+    hidden size runs fastest on (measured; empty if the size was not tuned)."""
+    path = TABLES / f"chain_tiles_hidden{hidden}.json"
+    if not path.exists():
+        return {}
+    return {int(M): cfg for M, cfg in json.loads(path.read_text()).items()}
+
+
+def round_chain_tile(hidden: int, M: int, act: bool = False) -> dict:
+    """The tile of a chained round of hidden size ``hidden`` at width ``M``: the measured entry,
+    else ``tiles.packed_chain_tile(M)`` (also when ``act``, a chain with a gate/up link carrying
+    its SiLU-and-multiply, meets an entry whose wave_frags is odd)."""
+    from .tiles import packed_chain_tile
+
+    cfg = read_chain_table(hidden).get(M)
+    if cfg is None or (act and cfg["wave_frags"] % 2):
+        cfg = packed_chain_tile(M)
+    return dict(cfg)
+
+
 def load_table(hf_config, width: int) -> dict[tuple[int, int, int], dict]:
     """The five tiles of ``hf_config`` at round width ``width`` (plm/gemm_tables.py:30-43)."""
     path = TABLES / f"tiles_hidden{hf_config.hidden_size}.json"

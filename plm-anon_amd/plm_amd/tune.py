@@ -2,7 +2,9 @@
 
 ``python -m plm_amd.tune --heuristic`` writes every table from ``tiles.heuristic_tile`` (no GPU).
 ``python -m plm_amd.tune [--hidden 2048 ...]`` times every candidate tile of every key on the GPU
-and writes the fastest into ``gpu_tuning/tiles_hidden<H>.json``.
+and writes the fastest into ``gpu_tuning/tiles_hidden<H>.json``. ``--chain`` instead times every
+compiled tile as the tile of a chained round (``chain.LinearChain``) of GPT-style blocks and writes
+the fastest per round width into ``gpu_tuning/chain_tiles_hidden<H>.json``.
 
 Timing: each candidate runs as a HIP graph of back-to-back launches that rotate over enough
 distinct weight copies (>= 1 GiB in total) that no launch finds its weight in the 256 MB
@@ -155,17 +157,145 @@ def tune_key(M: int, N: int, K: int, verbose: bool = True) -> tuple[dict, float,
     return best, best_us, results
 
 
+# --------------------------------------------------------------------------- chain tiles
+
+# The chained rounds the benchmark runs, per hidden size: the block's linears (each reading the
+# output before it: GPT-style QKV 3H, attn-out, MLP up, down; at 3072 the Llama 3B set's GQA QKV,
+# o, fused gate/up and down) and the round widths.
+def chain_rounds() -> dict[int, tuple[list, tuple[int, ...]]]:
+    from .workloads import LLAMA_SETS, gpt_block, llama_block
+
+    s = LLAMA_SETS["3B"]
+    return {2048: (gpt_block(2048, 8192), (*M_SWEEP, 110)), 2560: (gpt_block(2560, 10240), (56,)),
+            3072: (llama_block(s["hidden"], s["qkv"], s["intermediate"]), (56,))}
+
+
+def chain_candidates() -> list[dict]:
+    return [{"wave_frags": nf, "k_waves": kw, "split_k": 1, "unroll": d}
+            for nf in (1, 2, 4) for kw in (1, 4, 8, 16) for d in (2, 4, 6, 8)]
+
+
+def tune_chain(hidden: int, block: list, M: int, verbose: bool = True) -> tuple[dict, float, list]:
+    """The fastest tile for a chained round at width M: a chain of ``block``'s linears with distinct
+    weights (at least 1 GiB of them, so that the Infinity Cache holds none across replays), timed
+    as graph replays per linear. Each candidate's outputs must equal per-linear launches of the
+    same tile and K splits bit for bit; a tile that is not compiled for M, or whose chain does not
+    fit the counter area, is skipped."""
+    import torch
+
+    from . import _lib
+    from .chain import Link, LinearChain
+    from .fast_gemm import _tile, hip_linear
+
+    dev = torch.device("cuda")
+    block_bytes = sum(2 * g.N * g.K for g in block)
+    blocks = max(4, math.ceil((1 << 30) / block_bytes))
+    gemms = [g for _ in range(blocks) for g in block]
+    gen = torch.Generator(device=dev).manual_seed(hidden * 31 + M)
+    weights = [((g.K ** -0.5) * torch.randn(g.N, g.K, generator=gen, device=dev)).bfloat16() for g in gemms]
+    x0 = torch.randn(M, hidden, generator=gen, device=dev).bfloat16()
+    outs = [torch.empty(M, -(-g.N // 64) * 64, device=dev, dtype=torch.bfloat16)[:, :g.N] for g in gemms]
+    inputs, x = [], x0
+    for g, y in zip(gemms, outs):
+        inputs.append(x[:, :g.K])
+        x = y
+    results = []
+    for cfg in chain_candidates():
+        G = int(_lib.lib().plm_gemm_packed_resident_workgroups(_lib.PLM_BF16, M, _tile(cfg)))
+        if G <= 0:
+            continue
+        links = [Link(xi, w, y, i - 1, tiles.packed_chain_split(g.N, g.K, cfg, G))
+                 for i, (g, xi, w, y) in enumerate(zip(gemms, inputs, weights, outs))]
+        try:
+            chain = LinearChain(links, cfg, packed=True)
+        except RuntimeError:
+            continue
+        chain.run()
+        chain.check()
+        got = [y.clone() for y in outs]
+        for ln in links:
+            hip_linear(ln.x, ln.w, dict(cfg, split_k=ln.split_k), ln.y)
+        if not all(torch.equal(a, b) for a, b in zip(got, outs)):
+            raise RuntimeError(f"chain tile {cfg} differs from its per-linear launches at hidden {hidden}, M={M}")
+        stream = torch.cuda.Stream()
+        with torch.cuda.stream(stream):
+            chain.run()
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                chain.run()
+            graph.replay()
+            torch.cuda.synchronize()
+            best = math.inf
+            for _ in range(3):
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record(stream)
+                graph.replay()
+                end.record(stream)
+                end.synchronize()
+                best = min(best, start.elapsed_time(end) * 1000.0 / len(links))
+        chain.check()
+        del graph, chain
+        results.append((best, cfg))
+        if verbose:
+            print(f"  chain h{hidden} M{M} {cfg}: {best:.2f} us per linear", flush=True)
+    results.sort(key=lambda r: r[0])
+    best_cfg, best_us = _pick_chain(results, tiles.packed_chain_tile(M))
+    if verbose:
+        print(f"chain h{hidden} M{M}: {best_cfg} {best_us:.2f} us per linear ({len(results)} candidates)", flush=True)
+    del weights, outs
+    torch.cuda.empty_cache()
+    return best_cfg, best_us, results
+
+
+def _pick_chain(results: list[tuple[float, dict]], default: dict) -> tuple[dict, float]:
+    """The fastest chain tile, or the width's default tile (``tiles.packed_chain_tile``) when it is
+    within TIE of the fastest."""
+    best_us = results[0][0]
+    for us, cfg in results:
+        if cfg == default and us <= best_us * (1 + TIE):
+            return cfg, us
+    return results[0][1], best_us
+
+
+def write_chain_table(hidden: int, table: dict[int, dict]) -> None:
+    text = json.dumps({str(M): cfg for M, cfg in sorted(table.items())}, indent=1)
+    (TABLES / f"chain_tiles_hidden{hidden}.json").write_text(text + "\n")
+
+
+def tune_chains(hiddens: list[int] | None, log: dict) -> None:
+    from .gemm_tables import read_chain_table
+
+    rounds = chain_rounds()
+    for hidden in hiddens or sorted(rounds):
+        block, widths = rounds[hidden]
+        table = read_chain_table(hidden)
+        for M in widths:
+            best, _, results = tune_chain(hidden, block, M)
+            table[M] = best
+            log[f"chain,{hidden},{M}"] = [(us, cfg) for us, cfg in results]
+            write_chain_table(hidden, table)
+
+
 def main(argv: list[str] | None = None) -> None:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--heuristic", action="store_true", help="write heuristic tables without a GPU")
     ap.add_argument("--hidden", type=int, nargs="*", help="hidden sizes to tune (default: all)")
     ap.add_argument("--keys", nargs="*", help="only these M,N,K keys")
     ap.add_argument("--log", help="write every candidate's timing to this JSON file")
+    ap.add_argument("--chain", action="store_true", help="tune the chained rounds' tiles instead")
     args = ap.parse_args(argv)
     if args.heuristic:
         heuristic_tables()
         return
     log = {}
+    if args.chain:
+        tune_chains(args.hidden, log)
+        if args.log:
+            with open(args.log, "w") as fh:
+                json.dump(log, fh)
+        print("chain tuning done", file=sys.stderr)
+        return
     for hidden in args.hidden or all_hidden():
         path = TABLES / f"tiles_hidden{hidden}.json"
         table = {tuple(int(v) for v in k.split(",")): c for k, c in json.loads(path.read_text()).items()} \

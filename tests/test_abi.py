@@ -324,6 +324,30 @@ def test_act_tables_pair_gate_and_up_fragments():
     assert not fast_gemm.ACT_CONFIGS
 
 
+def test_chain_tables_hold_compiled_tiles_and_fall_back_to_the_rule():
+    """chain_tiles_hidden<H>.json: one tile per round width, each a compiled packed tile for that
+    width (tile_supported) with the fields a chain reads; a width or hidden size without an entry
+    gets tiles.packed_chain_tile."""
+    from plm_amd import tiles
+
+    paths = sorted(gemm_tables.TABLES.glob("chain_tiles_hidden*.json"))
+    assert paths
+    for path in paths:
+        hidden = int(path.stem.removeprefix("chain_tiles_hidden"))
+        table = gemm_tables.read_chain_table(hidden)
+        assert table, path.name
+        for M, cfg in table.items():
+            assert set(cfg) == {"wave_frags", "k_waves", "split_k", "unroll"} and cfg["split_k"] == 1, (hidden, M)
+            assert fast_gemm.tile_supported(M, hidden, cfg), (hidden, M, cfg)
+            assert gemm_tables.round_chain_tile(hidden, M) == cfg
+    assert gemm_tables.round_chain_tile(2560, 42) == tiles.packed_chain_tile(42)
+    assert gemm_tables.round_chain_tile(1536, 56) == tiles.packed_chain_tile(56)
+    for path in paths:
+        hidden = int(path.stem.removeprefix("chain_tiles_hidden"))
+        for M in gemm_tables.read_chain_table(hidden):
+            assert gemm_tables.round_chain_tile(hidden, M, act=True)["wave_frags"] % 2 == 0
+
+
 def test_load_table_missing_hidden_size_exits():
     with pytest.raises(SystemExit, match="no tile table for hidden size 1536"):
         gemm_tables.load_table(llama(1536, 4096, 12, 12), 42)

@@ -232,6 +232,45 @@ def _oracle_columns(x, w, y, cols):
     assert int((~in_tol).sum()) <= max(1, got.numel() // 1000)
 
 
+def _chain_table_entries():
+    from plm_amd import gemm_tables
+
+    return [(int(p.stem.removeprefix("chain_tiles_hidden")), M)
+            for p in sorted(gemm_tables.TABLES.glob("chain_tiles_hidden*.json"))
+            for M in sorted(gemm_tables.read_chain_table(int(p.stem.removeprefix("chain_tiles_hidden"))))]
+
+
+@pytest.mark.parametrize("hidden,M", _chain_table_entries(), ids=lambda v: str(v))
+def test_round_chain_table_tiles(device, hidden, M):
+    """Every measured chain tile (chain_tiles_hidden<H>.json) on one block of the round it was
+    measured on, at its width, each linear reading the one before it (the tile-flag launch), launched twice
+    with a new input and NaN-filled outputs: bit for bit the single-linear kernel, and the oracle
+    within the GEMM tolerance."""
+    from plm_amd import _lib, gemm_tables
+    from plm_amd.fast_gemm import _tile
+    from plm_amd.tiles import packed_chain_split
+
+    cfg = gemm_tables.round_chain_tile(hidden, M)
+    G = _lib.lib().plm_gemm_packed_resident_workgroups(_lib.PLM_BF16, M, _tile(cfg))
+    assert G > 0
+    from plm_amd.tune import chain_rounds
+
+    shapes = [(gm.N, gm.K) for gm in chain_rounds()[hidden][0]]
+    ws = _weights(shapes, 70 + M, device)
+    g = torch.Generator(device=device).manual_seed(71 + hidden)
+    x = torch.randn(M, hidden, generator=g, device=device).bfloat16()
+    links, ys = _chain(x, ws, [packed_chain_split(n, k, cfg, G) for n, k in shapes])
+    chain = LinearChain(links, cfg, packed=True)
+    assert chain.sync_mode == 2
+    for _ in range(2):
+        x.copy_(torch.randn(M, hidden, generator=g, device=device).bfloat16())
+        for y in ys:
+            y.fill_(float("nan"))
+        chain.run()
+        _check_against_single(links, cfg)
+    assert chain.error_flag() == 0
+
+
 def test_round_chain_graph_replays_with_new_inputs(device):
     """The benchmark's chained round, all 96 block linears of the 1.3B-shape round at M = 56 in one
     tile-flag launch, recorded as a HIP graph and replayed 8 times. Before every replay the round's
@@ -239,12 +278,12 @@ def test_round_chain_graph_replays_with_new_inputs(device):
     producer tiles were written (or a line left from an earlier replay) would show up: each replay
     must equal per-linear launches bit for bit, and sampled columns of the first and last block
     must match the CPU oracle."""
-    from plm_amd import _lib
+    from plm_amd import _lib, gemm_tables
     from plm_amd.fast_gemm import _tile
-    from plm_amd.tiles import packed_chain_split, packed_chain_tile
+    from plm_amd.tiles import packed_chain_split
 
     M = 56
-    cfg = packed_chain_tile(M)
+    cfg = gemm_tables.round_chain_tile(2048, M)
     G = _lib.lib().plm_gemm_packed_resident_workgroups(_lib.PLM_BF16, M, _tile(cfg))
     assert G > 0
     block = workloads.gpt_block(2048, 8192)
