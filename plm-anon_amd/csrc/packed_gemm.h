@@ -1103,8 +1103,8 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
 }
 
 // Compiled configurations (all without scratch): 1 <= MT <= 8, NF in {1, 2, 4}, D in
-// {2, 4, 6, 8}, at most 20 accumulator fragments, and either two workgroups per CU or, for
-// MT <= 4, one workgroup per CU with the pipeline's registers within 320 of a lane's 512.
+// {2, 4, 6, 8}, at most 20 accumulator fragments, and either two workgroups per CU or one
+// workgroup per CU with the pipeline's registers within 320 of a lane's 512.
 template <int MT, int NF, int D, int KW>
 constexpr bool packed_compiled() {
   if (MT < 1 || MT > 8 || (NF != 1 && NF != 2 && NF != 4) || (D != 2 && D != 4 && D != 6 && D != 8)) return false;
@@ -1125,7 +1125,7 @@ constexpr bool packed_compiled() {
 template <int MT, int NF, int D, int KW, int EPI>
 constexpr bool packed_fits() {
   constexpr int r = packed_regs<MT, NF, D, KW>();
-  if constexpr (KW == 1) return r <= (EPI == kEpiLora ? 240 : 244) || (EPI == kEpiAct && r <= 292);
+  if constexpr (KW == 1) return r <= 240 || (EPI == kEpiAct && r <= 292);
   if constexpr (EPI != kEpiLora) return true;
   if constexpr (KW == 4) return packed_two_per_cu<MT, NF, D, KW>() || r <= 288;
   if constexpr (KW == 16) return r <= 48;

@@ -91,6 +91,21 @@ def test_fp16_and_narrow_rounds(device):
         _check(got, oracle.gated_lora(x, w, a, bs, gate), torch.float16)
 
 
+@pytest.mark.parametrize("M,gate,d", [(110, 10, 4), (96, 90, 2)])
+def test_wide_rounds(device, M, gate, d):
+    """Seven and six X fragments per K step (the relaxed setting's width 110) on the four-wavefront
+    K split: the reference composition within tolerance, the rows before the gate bit for bit the
+    plain linear."""
+    x, w, a, bs, (xg, wg, ag, bsg) = _operands(M, (2048, 512, 512), 2048, 16, 40 + M, device)
+    cfg = {"wave_frags": 2, "k_waves": 4, "split_k": 1, "unroll": d}
+    from plm_amd import gated_lora
+
+    assert gated_lora._eligible(xg, wg, ag, bsg, gate, None, cfg)   # the one-launch kernel runs
+    got = gated_linear(xg, wg, ag, bsg, gate, cfg=cfg)
+    _check(got, oracle.gated_lora(x, w, a, bs, gate))
+    assert torch.equal(got[:gate], hip_linear(xg, wg, cfg)[:gate])
+
+
 def test_method_wrapper_routes_through_rows_from(device):
     """GatedLoraMethod.apply: outside rows_from the inner method runs; inside, the gated linear."""
     shards, K, rank, cfg = CASES["gate_up"]

@@ -126,12 +126,15 @@ def test_every_candidate_tile(device, shape):
         check(y, x, w)
 
 
-@pytest.mark.parametrize("M", [1, 15, 16, 17, 33, 64, 65, 110, 128])
+@pytest.mark.parametrize("M", [1, 15, 16, 17, 33, 64, 65, 96, 97, 110, 128])
 def test_round_widths_edge_cases(device, M):
     N, K = 1000, 1416   # N not a multiple of any tile; K a multiple of 8 but not of 32
     x, w = _inputs(M, N, K, 5)
     supported = lambda c: fast_gemm.tile_supported(M, K, c)  # noqa: E731
     for cfg in (tiles.heuristic_tile(M, N, K, supported=supported),
+                {"wave_frags": 4, "k_waves": 4, "split_k": 1, "unroll": 4},   # 64-row tiles (M <= 80)
+                {"wave_frags": 4, "k_waves": 4, "split_k": 3, "unroll": 2},
+                {"wave_frags": 4, "k_waves": 1, "split_k": 1, "unroll": 6},   # depth capped where it spills
                 {"wave_frags": 1, "k_waves": 4, "split_k": 3, "unroll": 2},
                 {"wave_frags": 1, "k_waves": 1, "split_k": 1, "unroll": 2},
                 {"wave_frags": 2, "k_waves": 1, "split_k": 3, "unroll": 4},

@@ -35,6 +35,8 @@ CASES = [
     (42, 8192, 3072, {"wave_frags": 2, "k_waves": 4, "split_k": 1, "unroll": 4}),
     (7, 1024, 1024, {"wave_frags": 2, "k_waves": 16, "split_k": 2, "unroll": 2}),
     (110, 5632, 2048, {"wave_frags": 2, "k_waves": 1, "split_k": 1, "unroll": 4}),  # row-split
+    (110, 5632, 2048, {"wave_frags": 2, "k_waves": 4, "split_k": 1, "unroll": 4}),  # seven X fragments, K split
+    (96, 1408, 512, {"wave_frags": 2, "k_waves": 4, "split_k": 2, "unroll": 2}),
     (56, 1408, 512, {"wave_frags": 4, "k_waves": 1, "split_k": 3, "unroll": 2}),    # row-split, K split
 ]
 
