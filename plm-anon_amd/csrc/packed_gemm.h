@@ -1119,16 +1119,18 @@ constexpr bool packed_compiled() {
 
 // Whether a configuration's epilogue fits the registers its pipeline leaves (measured: no scratch
 // in the compiler's resource report for either element type). KW = 1 configurations are held to
-// 256 VGPRs; the LoRA epilogue keeps the low-rank correction's operands beside the pipeline. A
-// configuration that does not fit runs at a lower pipeline depth D (packed_pick_d): the K steps
-// are summed in the same order at every depth, so the results are the same.
+// 256 VGPRs, KW = 16 ones to 128; the LoRA epilogue keeps the low-rank correction's operands beside
+// the pipeline. A configuration that does not fit runs at a lower pipeline depth D (packed_pick_d):
+// the K steps are summed in the same order at every depth, so the results are the same. At D = 2
+// only the LoRA epilogue on 16-wavefront tiles with 4 accumulator fragments does not fit; those
+// tiles are not compiled for it.
 template <int MT, int NF, int D, int KW, int EPI>
 constexpr bool packed_fits() {
   constexpr int r = packed_regs<MT, NF, D, KW>();
   if constexpr (KW == 1) return r <= 240 || (EPI == kEpiAct && r <= 292);
+  if constexpr (KW == 16) return EPI == kEpiLora ? r <= 48 : (r <= 52 || MT == 1 || D == 2);
   if constexpr (EPI != kEpiLora) return true;
   if constexpr (KW == 4) return packed_two_per_cu<MT, NF, D, KW>() || r <= 288;
-  if constexpr (KW == 16) return r <= 48;
   return true;
 }
 
@@ -1142,7 +1144,7 @@ constexpr size_t packed_lds_bytes() {
 // checks that the kernel exists.
 template <int DT, int MT, int NF, int D, int KW, int EPI>
 hipError_t packed_launch(PackedArgs& a, int cus, hipStream_t stream, bool dry) {
-  if constexpr (!packed_compiled<MT, NF, D, KW>() || (D > 2 && !packed_fits<MT, NF, D, KW, EPI>())) {
+  if constexpr (!packed_compiled<MT, NF, D, KW>() || !packed_fits<MT, NF, D, KW, EPI>()) {
     return hipErrorInvalidConfiguration;
   } else {
     if (dry) return hipSuccess;
@@ -1173,10 +1175,10 @@ hipError_t packed_launch(PackedArgs& a, int cus, hipStream_t stream, bool dry) {
 
 template <int DT, int MT, int NF, int KW, int EPI>
 hipError_t packed_pick_d(PackedArgs& a, int d, int cus, hipStream_t s, bool dry) {
-  // The tile's depth is a cap: lowered to one whose epilogue fits (packed_fits).
-  if (d == 8 && !packed_fits<MT, NF, 8, KW, EPI>()) d = 6;
-  if (d == 6 && !packed_fits<MT, NF, 6, KW, EPI>()) d = 4;
-  if (d == 4 && !packed_fits<MT, NF, 4, KW, EPI>()) d = 2;
+  // The depth of a compiled tile is a cap: lowered to one whose epilogue fits (packed_fits).
+  if (d == 8 && packed_compiled<MT, NF, 8, KW>() && !packed_fits<MT, NF, 8, KW, EPI>()) d = 6;
+  if (d == 6 && packed_compiled<MT, NF, 6, KW>() && !packed_fits<MT, NF, 6, KW, EPI>()) d = 4;
+  if (d == 4 && packed_compiled<MT, NF, 4, KW>() && !packed_fits<MT, NF, 4, KW, EPI>()) d = 2;
   if (d == 2) return packed_launch<DT, MT, NF, 2, KW, EPI>(a, cus, s, dry);
   if (d == 4) return packed_launch<DT, MT, NF, 4, KW, EPI>(a, cus, s, dry);
   if (d == 6) return packed_launch<DT, MT, NF, 6, KW, EPI>(a, cus, s, dry);

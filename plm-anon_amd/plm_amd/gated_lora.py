@@ -21,7 +21,7 @@ from contextlib import contextmanager
 
 import torch
 
-from . import _lib
+from . import _lib, tiles
 from .fast_gemm import CONFIGS, HALF_DTYPES, Config, dispatch_unquantized_gemm, packed_weight, workspace
 
 _rows_from: int | None = None
@@ -69,6 +69,10 @@ def _eligible(x, weight, lora_a, lora_bs, first_gated_row, bias, cfg) -> bool:
         return False
     M, K = x.shape
     if sum(b.shape[0] for b in lora_bs) != weight.shape[0] or K % 8:
+        return False
+    # Sixteen-wavefront tiles above 48 estimated registers even at depth 2 have no LoRA kernel (its
+    # epilogue would spill: packed_fits in csrc/packed_gemm.h).
+    if cfg["k_waves"] == 16 and tiles._regs(-(-M // 16), cfg["wave_frags"], 2, 16) > 48:
         return False
     return tile_supported(M, K, cfg, x.dtype)
 

@@ -106,6 +106,18 @@ def test_wide_rounds(device, M, gate, d):
     assert torch.equal(got[:gate], hip_linear(xg, wg, cfg)[:gate])
 
 
+def test_sixteen_wave_tiles_without_a_lora_kernel_take_the_composition(device):
+    """A 16-wavefront tile with four accumulator fragments has a plain kernel but no LoRA one (its
+    epilogue would spill): the call takes the reference's composition and still matches."""
+    from plm_amd import fast_gemm, gated_lora
+
+    x, w, a, bs, (xg, wg, ag, bsg) = _operands(7, (1024, 256, 256), 1024, 8, 77, device)
+    cfg = {"wave_frags": 4, "k_waves": 16, "split_k": 1, "unroll": 2}
+    assert fast_gemm.tile_supported(7, 1024, cfg)
+    assert not gated_lora._eligible(xg, wg, ag, bsg, 3, None, cfg)
+    _check(gated_linear(xg, wg, ag, bsg, 3, cfg=cfg), oracle.gated_lora(x, w, a, bs, 3))
+
+
 def test_method_wrapper_routes_through_rows_from(device):
     """GatedLoraMethod.apply: outside rows_from the inner method runs; inside, the gated linear."""
     shards, K, rank, cfg = CASES["gate_up"]
