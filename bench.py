@@ -1054,7 +1054,11 @@ def time_verify(w_lm, hidden, device, steps):
 
     mfma = mfma_for("verify_packed_main_kernel<bf16, MT=4, NF=%d, D=%d>" % (
         VERIFY_CONFIG["wave_frags"], VERIFY_CONFIG["unroll"])) or {}
-    head = mfma_for("packed_gemm_kernel<bf16, MT=4, NF=4, D=8, KW=1>") or {}
+    from plm_amd import gemm_tables
+    from plm_amd.workloads import GPT2_VOCAB
+
+    head_cfg = gemm_tables.read_table(hidden)[(56, GPT2_VOCAB, hidden)]
+    head = mfma_for(kernel_name(kernel_class(56, hidden, head_cfg))) or {}
     return {"us": round(ms * 1000.0, 2), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "pct_of_hbm_peak": round(100.0 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 2),
             "bytes": nbytes, "accepted": int(acc.sum().item()), "round_us": round(ms_round * 1000.0, 2),
