@@ -348,6 +348,22 @@ def test_chain_tables_hold_compiled_tiles_and_fall_back_to_the_rule():
             assert gemm_tables.round_chain_tile(hidden, M, act=True)["wave_frags"] % 2 == 0
 
 
+def test_tuner_tie_rules():
+    """Per-GEMM tables: a tie within 1 % goes to the fastest even wave_frags; outside it, the fastest
+    tile. Chain tables: the width's default chain tile wins a tie, else the fastest."""
+    from plm_amd import tune
+
+    odd, even = {"wave_frags": 1, "k_waves": 8, "split_k": 1, "unroll": 2}, {"wave_frags": 2, "k_waves": 8,
+                                                                             "split_k": 1, "unroll": 2}
+    assert tune.pick([(10.0, odd), (10.05, even)]) == (even, 10.05)
+    assert tune.pick([(10.0, odd), (10.2, even)]) == (odd, 10.0)
+    default = tiles.packed_chain_tile(56)
+    other = dict(default, wave_frags=4, k_waves=4)
+    assert tune._pick_chain([(10.0, other), (10.05, default)], default) == (default, 10.05)
+    assert tune._pick_chain([(10.0, other), (10.5, default)], default) == (other, 10.0)
+    assert tune._pick_chain([(10.0, other)], default) == (other, 10.0)
+
+
 def test_load_table_missing_hidden_size_exits():
     with pytest.raises(SystemExit, match="no tile table for hidden size 1536"):
         gemm_tables.load_table(llama(1536, 4096, 12, 12), 42)
