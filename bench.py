@@ -384,9 +384,11 @@ def main():
     chain_wins = us_round <= us_graph
     us_value = us_round if chain_wins else us_graph
     gbps_value = rnd.bytes / (us_value * 1e-6) / 1e9
-    timing = ("HIP graph replay, HIP events; value = the round as one chained launch of its 96 block linears "
-              "over packed weights (plm_gemm_chain_packed) + the LM-head launch (plm_gemm_packed)" if chain_wins else
-              "HIP graph replay, HIP events; value = the round as 97 fast_gemm launches (plm_gemm_packed, "
+    n_lin = len(rnd.gemms)
+    timing = (f"HIP graph replay, HIP events; value = the round as one chained launch of its {n_lin - 1} block "
+              "linears over packed weights (plm_gemm_chain_packed) + the LM-head launch (plm_gemm_packed)"
+              if chain_wins else
+              f"HIP graph replay, HIP events; value = the round as {n_lin} fast_gemm launches (plm_gemm_packed, "
               "tuned tile per shape) in one graph")
     result = {
         "metric": METRIC, "value": round(us_value, 2), "unit": "us/round", "n_gpus": 1, "steps": args.steps,
