@@ -167,7 +167,7 @@ def chain_rounds() -> dict[int, tuple[list, tuple[int, ...]]]:
 
     s = LLAMA_SETS["3B"]
     return {2048: (gpt_block(2048, 8192), (*M_SWEEP, 110)), 2560: (gpt_block(2560, 10240), (56,)),
-            3072: (llama_block(s["hidden"], s["qkv"], s["intermediate"]), (56,))}
+            3072: (llama_block(s["hidden"], s["qkv"], s["intermediate"]), (42, 56, 110))}
 
 
 def chain_candidates() -> list[dict]:
