@@ -18,7 +18,8 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .fast_gemm import Config, HALF_DTYPES, _tile, packed_gate_up, packed_weight, row_major_weight, workspace
+from .fast_gemm import (Config, HALF_DTYPES, _tile, packed_gate_up, packed_weight, reset_counters, row_major_weight,
+                        workspace)
 
 
 @dataclass
@@ -111,11 +112,13 @@ class LinearChain:
 
     def check(self) -> None:
         """Raises if a launch since the last check had a wait give up (its outputs, and those of
-        every launch after it until this check, are invalid), and clears the flag so later
-        launches are judged on their own. Synchronises the device; call it outside graph capture,
-        after the launches (or graph replays) it vouches for."""
+        every launch after it until this check, are invalid), and resets the workspace's whole
+        counter area (the error int, split arrival counters, flags and epochs: the workspace is
+        shared with the other entry points, whose counters a failed launch can leave off zero) so
+        later launches are judged on their own. Synchronises the device; call it outside graph
+        capture, after the launches (or graph replays) it vouches for."""
         if self.error_flag():
-            self.ws[4 * _lib.ERROR_INDEX: 4 * (_lib.ERROR_INDEX + 1)].zero_()
+            reset_counters(self.ws)
             torch.cuda.synchronize(self.device)
             raise RuntimeError(f"a chained launch of {len(self.links)} linears had a wait for another workgroup give "
                                "up (another process on the device, or the grid was not resident): outputs invalid")

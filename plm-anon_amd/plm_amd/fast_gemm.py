@@ -80,6 +80,14 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return buf
 
 
+def reset_counters(buf: torch.Tensor) -> None:
+    """Zeroes the counter area at the start of workspace ``buf`` (a uint8 tensor): every arrival
+    counter, flag, epoch and the error int. After a bounded wait gave up, a late workgroup of the
+    failed launch can have counted itself in after the counter's owner reset it; only a whole reset
+    leaves every counter ready for the next launch."""
+    buf[: _lib.COUNTER_BYTES].zero_()
+
+
 def check_workspace(device: torch.device) -> None:
     """Raises if a launch on ``device``'s workspace reported a bounded wait that gave up (the int at
     ``PLM_WORKSPACE_ERROR_INDEX``: chained launches, the gated-LoRA launch, the fused verify), whose
@@ -92,7 +100,7 @@ def check_workspace(device: torch.device) -> None:
         return
     flag = int(buf[: 4 * (_lib.ERROR_INDEX + 1)].view(torch.int32)[_lib.ERROR_INDEX].item())
     if flag:
-        buf[: _lib.COUNTER_BYTES].zero_()
+        reset_counters(buf)
         raise RuntimeError(f"a launch on cuda:{index}'s workspace gave up a bounded wait (another process "
                            "holding CUs?): its results are invalid; the counter area was reset")
 

@@ -55,7 +55,7 @@ def stack_b(lora_bs: list[torch.Tensor]) -> torch.Tensor:
 def _eligible(x, weight, lora_a, lora_bs, first_gated_row, bias, cfg) -> bool:
     """Whether the fused HIP path takes this call: everything ``plm_gemm_packed_lora`` checks, so
     that an ineligible call takes the reference's composition instead of failing."""
-    from .fast_gemm import tile_supported
+    from .fast_gemm import WIDE_ROWS, tile_supported
 
     shards = len(lora_bs)
     if cfg is None or bias is not None or x.dim() != 2 or x.dtype not in HALF_DTYPES or not x.is_cuda:
@@ -69,6 +69,11 @@ def _eligible(x, weight, lora_a, lora_bs, first_gated_row, bias, cfg) -> bool:
         return False
     M, K = x.shape
     if sum(b.shape[0] for b in lora_bs) != weight.shape[0] or K % 8:
+        return False
+    # The one-launch correction runs on the skinny packed kernel only (plm_gemm_packed_lora takes
+    # up to WIDE_ROWS rows); wider calls (prefill chunks) take the reference's composition, whose
+    # GEMMs fast_gemm routes to the wide kernel or F.linear.
+    if M > WIDE_ROWS:
         return False
     # Sixteen-wavefront tiles above 48 estimated registers even at depth 2 have no LoRA kernel (its
     # epilogue would spill: packed_fits in csrc/packed_gemm.h).

@@ -532,3 +532,21 @@ def test_voronoi_host_checks_refuse_cpu_and_bad_sizes():
     scheme = voronoi.LogitVoronoiAuxiliary(1024, 64, 1000)
     assert scheme.masked_value == 1024 and scheme.placeholder_token_id == 1000
     assert set(scheme.state_dict()) == {"auxiliary_vocabulary", "mask_auxiliary"}
+
+
+def test_chain_check_resets_the_whole_counter_area(monkeypatch):
+    """A chained launch whose wait gave up can leave any counter of the shared workspace off zero
+    (a late workgroup counting in after the owner's reset): check() raises and zeroes the whole
+    counter area, not only the error int, and leaves the scratch past it alone."""
+    from plm_amd.chain import LinearChain
+
+    ws = torch.full((_lib.COUNTER_BYTES + 4096,), 7, dtype=torch.uint8)
+    ws[: _lib.COUNTER_BYTES].view(torch.int32)[_lib.ERROR_INDEX] = 1
+    chain = LinearChain.__new__(LinearChain)
+    chain.ws, chain.device, chain.links = ws, torch.device("cpu"), [None]
+    monkeypatch.setattr(torch.cuda, "synchronize", lambda *a, **k: None)
+    with pytest.raises(RuntimeError, match="give up"):
+        chain.check()
+    assert int(ws[: _lib.COUNTER_BYTES].count_nonzero()) == 0
+    assert bool((ws[_lib.COUNTER_BYTES:] == 7).all())
+    chain.check()  # a clean workspace passes

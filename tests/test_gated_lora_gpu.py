@@ -208,3 +208,13 @@ def test_check_workspace_reports_and_resets_the_error_flag(device):
     assert int(ws[: _lib.COUNTER_BYTES].count_nonzero().item()) == 0
     _check(gated_linear(xg, wg, ag, bsg, 7, cfg=cfg), oracle.gated_lora(x, w, a, bs, 7))
     fast_gemm.check_workspace(device)
+
+
+def test_prefill_width_with_an_explicit_tile_takes_the_composition(device):
+    """Above the skinny kernel's 128 rows the one-launch correction does not apply: a call with an
+    explicit round tile (a prefill chunk, plm/rounds.py:16) takes the reference's composition
+    instead of failing, and matches the oracle."""
+    shards, K, rank, cfg = CASES["qkv"]
+    x, w, a, bs, (xg, wg, ag, bsg) = _operands(129, shards, K, rank, 21, device)
+    got = gated_linear(xg, wg, ag, bsg, 7, cfg=cfg)
+    _check(got, oracle.gated_lora(x, w, a, bs, 7))
