@@ -237,51 +237,6 @@ int64_t plm_gemm_chain_prepare(plm_chain_gemm* gemms, int32_t count, int64_t M, 
 int plm_gemm_chain(int32_t dtype, const plm_chain_gemm* host_gemms, const plm_chain_gemm* device_gemms, int32_t count,
                    int64_t M, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream);
 
-/*
- * One linear of a ring chain (plm_ring_chain): Y[M,N] = X[M,K] · W[N,K]^T with W packed
- * (plm_pack_weight). The first block is the caller's; plm_ring_chain_prepare fills the rest.
- */
-typedef struct plm_ring_link {
-  const void* x;          /* X row-major (ldx, 16-byte aligned); for dep >= 0 the producer's y */
-  const void* w;          /* packed weight */
-  void* y;                /* Y row-major (ldy) */
-  int64_t ldx, ldy;
-  int32_t N, K;           /* K % 8 == 0 */
-  int32_t dep;            /* -1, or the earlier link whose Y (its leading K columns) this X is; that
-                             link must write the model dtype and have N % 8 == 0 */
-  int32_t out_f32;        /* PLM_OUT_MODEL or PLM_OUT_F32 (the latter only for a link no other reads) */
-  int32_t tile_rows;      /* 16-row weight fragments per tile, 1..4, or 0: prepare chooses */
-  int32_t split_k;        /* workgroups splitting K, or 0: prepare chooses (at most 32 K steps of 32
-                             elements per workgroup) */
-  /* filled by plm_ring_chain_prepare */
-  int32_t consumed;       /* 1 when a later link reads this Y */
-  int32_t tiles;
-  int64_t flag_offset;    /* workspace byte offsets: tile flags, arrival counters, split partials, */
-  int64_t arrive_offset;  /* and the Y copy in the reader's operand layout */
-  int64_t partial_offset;
-  int64_t mbox_offset;
-} plm_ring_link;
-
-/*
- * The round's linears in one launch with the weight stream on a wavefront of its own (replacing the
- * per-GEMM graph nodes of plm/decoder.py:312-324, each of them the reference's gemm_kernel +
- * splitk_reduce_kernel, plm/fast_gemm.py:17-61): per compute unit, one wavefront streams the packed
- * weights into LDS ahead of four that multiply, so the next linear's weights arrive while its input
- * is still being produced. Each linear's output depends only on its own tile_rows and split_k (the
- * same values from a one-link chain). M <= 64. One workgroup per compute unit, all resident at
- * once; a wait that does not complete in about a second sets the int at PLM_WORKSPACE_ERROR_INDEX.
- * The workspace is this entry point's own: zeroed before the first call, it keeps tile flags and
- * arrival counters between calls, so it must not be handed to other entry points (it may serve
- * several ring chains in turn on one stream).
- * plm_ring_chain_prepare fills the derived fields for `workgroups` workgroups (0: one per compute
- * unit of the current device) and returns the workspace bytes, or a negative status.
- */
-int64_t plm_ring_chain_prepare(plm_ring_link* links, int32_t count, int64_t M, int32_t workgroups);
-/* Workgroups a ring chain launches on the current device (its compute units), or a negative status. */
-int plm_ring_chain_workgroups(void);
-int plm_ring_chain(int32_t dtype, const plm_ring_link* host_links, const plm_ring_link* device_links, int32_t count,
-                   int64_t M, void* workspace, size_t workspace_bytes, void* stream);
-
 /* Workspace bytes plm_gemm needs for this shape and tile (the reference's _partial_buffer,
  * plm/fast_gemm.py:70-79): PLM_WORKSPACE_COUNTER_BYTES plus the fp32 split partials. 0 when
  * split_k == 1. */

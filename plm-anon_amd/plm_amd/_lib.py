@@ -65,9 +65,6 @@ EXPORTS = (
     "plm_voronoi_argmin",
     "plm_voronoi_assign",
     "plm_voronoi_assign_workspace_bytes",
-    "plm_ring_chain_prepare",
-    "plm_ring_chain_workgroups",
-    "plm_ring_chain",
     "plm_status_string",
 )
 
@@ -91,17 +88,6 @@ class ChainGemm(ctypes.Structure):
                 ("N", ctypes.c_int32), ("K", ctypes.c_int32), ("split_k", ctypes.c_int32), ("dep", ctypes.c_int32),
                 ("out_f32", ctypes.c_int32), ("consumed", ctypes.c_int32), ("arrive_base", ctypes.c_int32),
                 ("done_base", ctypes.c_int32), ("partial_offset", ctypes.c_int64)]
-
-
-class RingLink(ctypes.Structure):
-    """``struct plm_ring_link``: one linear of a ring chain (104 bytes, natural alignment)."""
-
-    _fields_ = [("x", ctypes.c_void_p), ("w", ctypes.c_void_p), ("y", ctypes.c_void_p),
-                ("ldx", ctypes.c_int64), ("ldy", ctypes.c_int64),
-                ("N", ctypes.c_int32), ("K", ctypes.c_int32), ("dep", ctypes.c_int32), ("out_f32", ctypes.c_int32),
-                ("tile_rows", ctypes.c_int32), ("split_k", ctypes.c_int32), ("consumed", ctypes.c_int32),
-                ("tiles", ctypes.c_int32), ("flag_offset", ctypes.c_int64), ("arrive_offset", ctypes.c_int64),
-                ("partial_offset", ctypes.c_int64), ("mbox_offset", ctypes.c_int64)]
 
 
 _lib: ctypes.CDLL | None = None
@@ -193,13 +179,6 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.plm_voronoi_assign.restype = ctypes.c_int
     lib.plm_voronoi_assign_workspace_bytes.argtypes = [c_i64, c_i64, c_i64, c_i64]
     lib.plm_voronoi_assign_workspace_bytes.restype = c_sz
-    ring_p = ctypes.POINTER(RingLink)
-    lib.plm_ring_chain_prepare.argtypes = [ring_p, c_i32, c_i64, c_i32]
-    lib.plm_ring_chain_prepare.restype = c_i64
-    lib.plm_ring_chain_workgroups.argtypes = []
-    lib.plm_ring_chain_workgroups.restype = ctypes.c_int
-    lib.plm_ring_chain.argtypes = [c_i32, ring_p, c_p, c_i32, c_i64, c_p, c_sz, c_p]
-    lib.plm_ring_chain.restype = ctypes.c_int
     lib.plm_status_string.argtypes = [c_i32]
     lib.plm_status_string.restype = ctypes.c_char_p
 
