@@ -59,7 +59,9 @@ extern "C" {
 
 int plm_gemm_packed_noalloc(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy,
                             int64_t M, int64_t N, int64_t K, const plm_tile* tile, void* stream) {
-  const int64_t need = plm::packed_gemm_workspace(M, N, K, tile);
+  // Wide calls (M > 128) split K only as far as the scratch holds.
+  const int64_t cap = static_cast<int64_t>(plm::kScratchBytes);
+  const int64_t need = plm::packed_gemm_workspace(M, N, K, tile, cap);
   if (need < 0)  // an invalid tile or size: the regular checks name it
     return plm::packed_gemm_call(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, nullptr, 0, stream, 0);
   if (static_cast<uint64_t>(need) > plm::kScratchBytes) return PLM_ERR_WORKSPACE;
@@ -69,7 +71,7 @@ int plm_gemm_packed_noalloc(int32_t dtype, const void* x, int64_t ldx, const voi
     if (status != PLM_OK) return status;
   }
   return plm::packed_gemm_call(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, ws, need > 0 ? plm::kScratchBytes : 0,
-                               stream, 0);
+                               stream, 0, cap);
 }
 
 }  // extern "C"

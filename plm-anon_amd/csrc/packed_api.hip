@@ -206,7 +206,8 @@ int packed_entry(int32_t dtype, const void* x, int64_t ldx, const void* wp, void
 // shapes); the tile configuration applies to the skinny kernel only and is checked for validity.
 // Every argument is checked before the launch.
 int packed_rows(int32_t dtype, const void* x, int64_t ldx, const void* wp, void* y, int64_t ldy, int64_t M, int64_t N,
-                int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream, int out_f32) {
+                int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream, int out_f32,
+                int64_t cap = kNoCap) {
   if (M <= kPackedMaxM) return packed_entry(dtype, x, ldx, wp, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, out_f32);
   if (!packed_tile_valid(tile)) return PLM_ERR_TILE;
   if (N < 1 || N > (int64_t(1) << 30) || K > (int64_t(1) << 30)) return PLM_ERR_ARGUMENT;
@@ -225,7 +226,7 @@ int packed_rows(int32_t dtype, const void* x, int64_t ldx, const void* wp, void*
   if (status != PLM_OK) return status;
   if (M > (int64_t(1) << 24) || M * ldx * 2 >= (int64_t(1) << 31)) return PLM_ERR_ARGUMENT;
   return wide_gemm(dtype, x, ldx, wp, y, ldy, M, N, K, workspace, workspace_bytes, static_cast<hipStream_t>(stream),
-                   out_f32);
+                   out_f32, cap);
 }
 
 // How the linears of a chain wait for the ones they read: 0 (none reads another), 2 (every linear
@@ -304,13 +305,13 @@ PSpan pspan(const void* p, int64_t rows, int64_t ld, int64_t cols, int64_t elem)
 
 int packed_gemm_call(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy, int64_t M,
                      int64_t N, int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream,
-                     int out_f32) {
-  return packed_rows(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, out_f32);
+                     int out_f32, int64_t cap) {
+  return packed_rows(dtype, x, ldx, packed_w, y, ldy, M, N, K, tile, workspace, workspace_bytes, stream, out_f32, cap);
 }
 
-int64_t packed_gemm_workspace(int64_t M, int64_t N, int64_t K, const plm_tile* tile) {
+int64_t packed_gemm_workspace(int64_t M, int64_t N, int64_t K, const plm_tile* tile, int64_t cap) {
   if (!packed_tile_valid(tile) || M < 1 || N < 1 || K < 1) return -1;
-  return M > kPackedMaxM ? wide_workspace(M, N, K) : packed_workspace(M, N, *tile);
+  return M > kPackedMaxM ? wide_workspace(M, N, K, cap) : packed_workspace(M, N, *tile);
 }
 
 }  // namespace plm

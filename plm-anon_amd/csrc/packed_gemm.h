@@ -1216,11 +1216,12 @@ hipError_t packed_dispatch_kw(PackedArgs& a, int nf, int d, int cus, hipStream_t
 
 // The single-linear entry behind plm_gemm_packed / plm_gemm_packed_f32out (argument checks, then
 // the launch), and the workspace bytes it needs for a shape and tile (-1 for an invalid tile): for
-// other translation units that launch the same kernel over their own scratch.
+// other translation units that launch the same kernel over their own scratch. `cap` bounds the
+// scratch a wide call (M > 128) may use: its K split, which only sets the speed, is chosen to fit.
 int packed_gemm_call(int32_t dtype, const void* x, int64_t ldx, const void* packed_w, void* y, int64_t ldy, int64_t M,
                      int64_t N, int64_t K, const plm_tile* tile, void* workspace, size_t workspace_bytes, void* stream,
-                     int out_f32);
-int64_t packed_gemm_workspace(int64_t M, int64_t N, int64_t K, const plm_tile* tile);
+                     int out_f32, int64_t cap = INT64_MAX);
+int64_t packed_gemm_workspace(int64_t M, int64_t N, int64_t K, const plm_tile* tile, int64_t cap = INT64_MAX);
 
 // One translation unit per (dtype, workgroup layout) so that they build in parallel.
 hipError_t packed_dispatch_bf16_k1(PackedArgs& a, int nf, int d, int cus, hipStream_t s, bool dry);

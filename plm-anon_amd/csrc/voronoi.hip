@@ -13,10 +13,11 @@
 //      of cost + offset (iterate.py:87-107).
 //   3. voronoi_fit_kernel, one 1024-thread workgroup: the annealed Sinkhorn sweeps on the condensed
 //      problem (iterate.py:110-159). Each thread owns items and all their k slots, so an item's
-//      softmax needs no exchange. The per-token loads are summed in 64-bit fixed point (units of
-//      2^-48) with integer LDS atomics: integer addition is associative, so the sums, and the
-//      fitted factors, are the same bit for bit whatever order the lanes add in (the reference's
-//      fp32 atomics are not, iterate.py:8-9).
+//      softmax needs no exchange. The per-token loads are fp32 sums in a fixed order: every sweep
+//      writes the slots' weights into LDS in target order (an order built once per fit), cut into
+//      pieces each summed by one thread, and each target adds its pieces with a fixed butterfly.
+//      No atomics, so the sums, and the fitted factors, are the same bit for bit on every run (the
+//      reference adds fp32 atomics in arrival order, which is not, iterate.py:8-9).
 //   2-3 repeat per round; the last fit also resolves the problem's one auxiliary value.
 //   4. voronoi_argmin_kernel (only when sigma is asked for): the assignment of every item.
 #include <hip/hip_runtime.h>

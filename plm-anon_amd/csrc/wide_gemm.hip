@@ -200,21 +200,22 @@ int64_t wide_tiles(int64_t M, int64_t N) { return ((N + kWideRows - 1) / kWideRo
 
 }  // namespace
 
-int wide_split(int64_t M, int64_t N, int64_t K) {
+int wide_split(int64_t M, int64_t N, int64_t K, int64_t cap) {
   const int64_t tiles = wide_tiles(M, N), ks = (K + 31) / 32;
+  const auto bytes = [&](int64_t s) { return static_cast<int64_t>(kCounterBytes) + tiles * s * kWideWaves * 16 * 1024; };
   int64_t split = 1;
-  while (tiles * split * 2 <= 320 && ks / (split * 2) >= 16 && split < 8) split *= 2;
+  while (tiles * split * 2 <= 320 && ks / (split * 2) >= 16 && split < 8 && bytes(split * 2) <= cap) split *= 2;
   return static_cast<int>(split);
 }
 
-int64_t wide_workspace(int64_t M, int64_t N, int64_t K) {
-  const int split = wide_split(M, N, K);
+int64_t wide_workspace(int64_t M, int64_t N, int64_t K, int64_t cap) {
+  const int split = wide_split(M, N, K, cap);
   if (split == 1) return 0;
   return static_cast<int64_t>(kCounterBytes) + wide_tiles(M, N) * split * kWideWaves * 16 * 1024;
 }
 
 int wide_gemm(int32_t dtype, const void* x, int64_t ldx, const void* wp, void* y, int64_t ldy, int64_t M, int64_t N,
-              int64_t K, void* workspace, size_t workspace_bytes, hipStream_t stream, int out_f32) {
+              int64_t K, void* workspace, size_t workspace_bytes, hipStream_t stream, int out_f32, int64_t cap) {
   WideArgs a{};
   a.x = x;
   a.w = wp;
@@ -226,11 +227,11 @@ int wide_gemm(int32_t dtype, const void* x, int64_t ldx, const void* wp, void* y
   a.Ks = static_cast<int>((K + 31) / 32);
   a.k_last = static_cast<int>(K - 32 * (a.Ks - 1));
   a.mtiles = static_cast<int>((M + kWideRows - 1) / kWideRows);
-  a.split = wide_split(M, N, K);
+  a.split = wide_split(M, N, K, cap);
   a.out_f32 = out_f32;
   const int64_t items = wide_tiles(M, N) * a.split;
   if (a.split > 1) {
-    const int64_t need = wide_workspace(M, N, K);
+    const int64_t need = wide_workspace(M, N, K, cap);
     if (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < need ||
         (reinterpret_cast<uintptr_t>(workspace) & 15) != 0)
       return PLM_ERR_WORKSPACE;
