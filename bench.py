@@ -51,6 +51,7 @@ def parse_args():
     ap.add_argument("--only-round", action="store_true", help="time the round only (for profiling runs)")
     ap.add_argument("--no-voronoi", action="store_true", help="skip the verify rows' auxiliary decode timing")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-width timing")
+    ap.add_argument("--no-fp16", action="store_true", help="skip the fp16 round timing")
     ap.add_argument("--profile", choices=("eager", "copy", "verify", "voronoi", "lora", "act"),
                     help="no JSON: 'eager' launches the round and the fused verify step --steps times without a "
                          "graph (for rocprofv3 counter runs); 'copy' runs a 1 GiB device copy, the reference "
@@ -66,9 +67,10 @@ class Round:
     down: the MLP's real dataflow); otherwise each linear reads the leading columns of the one
     before it."""
 
-    def __init__(self, M, hidden, mlp, layers, weights, tables, device, gemms=None, act=False):
+    def __init__(self, M, hidden, mlp, layers, weights, tables, device, gemms=None, act=False, dtype=None):
         import torch
 
+        dtype = dtype or torch.bfloat16
         from plm_amd import gemm_tables
         from plm_amd.workloads import GPT2_VOCAB, gpt_block
 
@@ -87,8 +89,8 @@ class Round:
                 if self.cfgs[i]["wave_frags"] % 2:
                     self.cfgs[i] = dict(self.cfgs[i], wave_frags=2)
         g = torch.Generator(device=device).manual_seed(3000 + M)
-        self.x0 = torch.randn(M, hidden, generator=g, device=device).bfloat16()
-        self.outs = [torch.empty(M, gm.N // 2 if a else gm.N, device=device, dtype=torch.bfloat16)
+        self.x0 = torch.randn(M, hidden, generator=g, device=device).to(dtype)
+        self.outs = [torch.empty(M, gm.N // 2 if a else gm.N, device=device, dtype=dtype)
                      for gm, a in zip(self.gemms, self.act)]
         self.inputs = []
         x = self.x0
@@ -255,7 +257,7 @@ class ChainedRound:
         from plm_amd.tiles import packed_chain_split
 
         cfg = gemm_tables.round_chain_tile(rnd.x0.shape[1], rnd.M, act=any(rnd.act))
-        G = _lib.lib().plm_gemm_packed_resident_workgroups(_lib.PLM_BF16, rnd.M, _tile(cfg))
+        G = _lib.lib().plm_gemm_packed_resident_workgroups(_lib.DTYPE_CODES[rnd.x0.dtype], rnd.M, _tile(cfg))
         _lib.check(min(G, 0), "plm_gemm_packed_resident_workgroups")
         n = len(rnd.gemms) - 1
         links = [Link(x, w, y, i - 1, packed_chain_split(g.N, g.K, cfg, G), a)
@@ -446,6 +448,10 @@ def main():
             print(f"[bench] M sweep: {sweep}", file=sys.stderr, flush=True)
         if not args.no_verify:
             result["verify"] = time_verify(weights[-1], args.hidden, device, args.steps)
+            if args.cpu_seconds > 0:
+                result["verify"]["cpu_baseline"] = cpu_verify_baseline(args.hidden, args.cpu_seconds)
+        if not args.no_fp16:
+            result["fp16_round"] = time_fp16_round(args, device, tables)
         if not args.no_voronoi:
             result["voronoi"] = time_voronoi(args, device, weights[-1])
         if not args.no_configs:
@@ -459,6 +465,75 @@ def main():
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_baseline(args.hidden, args.mlp, args.M, args.cpu_seconds)
     print(json.dumps(result), flush=True)
+
+
+def cpu_verify_baseline(hidden, budget_s):
+    """The verify step of config 5 on this host's CPU, the reference's composition: torch-CPU
+    F.linear logits in bf16 (plm/fast_gemm.py:111), then nucleus acceptance and the argmax
+    (plm/decoder.py:71-75, 362) over them; median of >= 5 reps after one warm-up."""
+    import torch
+
+    import oracle
+    from plm_amd.workloads import GPT2_VOCAB, TOP_P, normal, proposals
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    x = normal((56, hidden), 5000)
+    w = normal((GPT2_VOCAB, hidden), 5001, 0.02)
+    pending = proposals(56)
+    oracle.verify(oracle.linear(x, w).float(), pending, TOP_P)  # warm-up
+    times = []
+    deadline = time.perf_counter() + budget_s / 3
+    while len(times) < 5 or (time.perf_counter() < deadline and len(times) < 30):
+        t0 = time.perf_counter()
+        oracle.verify(oracle.linear(x, w).float(), pending, TOP_P)
+        times.append(time.perf_counter() - t0)
+    return {"us": round(sorted(times)[len(times) // 2] * 1e6, 1), "cores": threads, "kind": "port",
+            "sample": "torch CPU F.linear bf16 logits [56, 50257], then the oracle's nucleus acceptance "
+                      "(top-p 0.94) and argmax; median over the reps"}
+
+
+def time_fp16_round(args, device, tables):
+    """The 1.3B round in fp16, the reference's default round dtype (plm/rounds.py:50): the chained
+    launch of the block linears + the LM head, and the per-GEMM graph, on fp16 weights drawn from the
+    same seeds; the chain is checked bit for bit against per-linear launches with its tile."""
+    import torch
+
+    from plm_amd.fast_gemm import hip_linear
+    from plm_amd.workloads import GPT2_VOCAB, gpt_block
+
+    gemms = [g for _ in range(args.layers) for g in gpt_block(args.hidden, args.mlp)]
+    gemms.append(type(gemms[0])("lm_head", GPT2_VOCAB, args.hidden))
+    gen = torch.Generator(device=device)
+    weights = []
+    for i, g in enumerate(gemms):
+        gen.manual_seed(1 + 1000 * 3 + i)
+        weights.append((0.02 * torch.randn(g.N, g.K, generator=gen, device=device)).half())
+    rnd = Round(args.M, args.hidden, args.mlp, args.layers, weights, tables, device, dtype=torch.float16)
+    chained = ChainedRound(rnd)
+    graph = capture_graph(chained.run)
+    us_chain = time_graph(graph, args.steps, args.warmup) * 1000.0
+    del graph
+    if chained.chain.error_flag():
+        raise RuntimeError("fp16 chained launch reported a timed-out wait")
+    chain_outs = [o.clone() for o in rnd.outs]
+    for i, ln in enumerate(chained.chain.links):
+        hip_linear(ln.x, ln.w, dict(chained.chain.cfg, split_k=ln.split_k), rnd.outs[i])
+    hip_linear(*chained.head)
+    torch.cuda.synchronize()
+    bit_exact = all(torch.equal(a, b) for a, b in zip(chain_outs, rnd.outs))
+    graph = rnd.capture()
+    us_graph = time_graph(graph, args.steps, args.warmup) * 1000.0
+    del graph, rnd, chained, weights
+    print(f"[bench] fp16 round: chained {us_chain:.1f} us, per-GEMM {us_graph:.1f} us", file=sys.stderr, flush=True)
+    return {"chained_us": round(us_chain, 2), "per_gemm_us": round(us_graph, 2),
+            "gbps": round(gemm_bytes(gemms, args.M) / (min(us_chain, us_graph) * 1e-6) / 1e9, 1),
+            "chain_bit_exact_vs_per_linear": bit_exact,
+            "note": "fp16 weights and activations (the reference's default round dtype); tiles as tuned for bf16"}
+
+
+def gemm_bytes(gemms, M):
+    return sum(g.bytes(M) for g in gemms)
 
 
 def cpu_linear_us(shapes, M, budget_s):

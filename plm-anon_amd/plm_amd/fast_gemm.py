@@ -282,6 +282,39 @@ def gate_up_silu(x: torch.Tensor, w: torch.Tensor, cfg: Config | None = None,
     return out
 
 
+def llama_mlp(x: torch.Tensor, gate_up_weight: torch.Tensor, down_weight: torch.Tensor,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    """The Llama-style MLP's linears as the reference's rounds run them through vLLM:
+    ``down_proj(SiluAndMul(gate_up_proj(x)))``, both projections routed through ``fast_gemm``
+    (plm/fast_gemm.py:104-110; the model forward at plm/decoder.py:250-259). A drop-in for the MLP
+    forward of one layer: ``gate_up_weight`` is the fused ``[2I, K]`` projection (gate rows first),
+    ``down_weight`` ``[K, I]``; the result is ``[M, K]`` in x's dtype with the reference's three
+    roundings (projection output, silu, product) and the down projection's.
+
+    Up to 128 rows it is two launches: the gate/up projection with its SiLU-and-multiply
+    (``gate_up_silu``, one launch, tile from ``ACT_CONFIGS``), then down (the tuned tile, or
+    ``default_config``). One chained launch of the two (``LinearChain`` with ``Link(act=True)``)
+    computes the same values bit for bit with matching tiles, but measured no faster on MI355X
+    (hidden 2048, M = 56: 31.75 against 31.74 us; hidden 3072: 48.81 against 47.63 us). Wider
+    calls (prefill chunks) run the projection, the activation and down through ``fast_gemm``'s own
+    routing."""
+    _check_operands(x, gate_up_weight)
+    M, K = x.shape
+    I = gate_up_weight.shape[0] // 2
+    if gate_up_weight.shape[0] != 2 * I or down_weight.shape != (K, I) or down_weight.dtype != x.dtype:
+        raise ValueError(f"llama_mlp expects gate_up [2I, {K}] and down [{K}, I], got "
+                         f"{tuple(gate_up_weight.shape)} and {tuple(down_weight.shape)} {down_weight.dtype}")
+    act = gate_up_silu(x, gate_up_weight)
+    if M > 128:
+        y = fast_gemm(None, act, down_weight)
+        if out is None:
+            return y
+        out.copy_(y)
+        return out
+    cfg = CONFIGS.get((M, K, I)) or default_config(M, K, I)
+    return hip_linear(act, down_weight, cfg, out)
+
+
 def reserve_workspace(device: torch.device, shapes: dict[tuple[int, int, int], Config] | None = None) -> None:
     """Size the device workspace for every configured shape, so later calls can be graph-captured."""
     shapes = CONFIGS if shapes is None else shapes
