@@ -388,8 +388,8 @@ int plm_gemm_packed_silu_mul(int32_t dtype, const void* x, int64_t ldx, const vo
  *
  * Ties the reference leaves to torch (topk, an unstable argsort) are fixed: the shortlist is the
  * n_targets largest logits by (value descending, token id ascending); equal quota remainders rank
- * by shortlist position. The fit's per-token loads are fp32 sums in a fixed target and piece order
- * (no atomics), so every output is reproducible bit for bit.
+ * by shortlist position. The fit's per-token loads are exact integer sums of the weights in units
+ * of 2^-31 (no float atomics), so every output is reproducible bit for bit.
  */
 
 /* Voronoi.shortlist + spread + prior (iterate.py:248-290) in one launch: tokens[N, M] (int64),

@@ -13,11 +13,10 @@
 //      of cost + offset (iterate.py:87-107).
 //   3. voronoi_fit_kernel, one 1024-thread workgroup: the annealed Sinkhorn sweeps on the condensed
 //      problem (iterate.py:110-159). Each thread owns items and all their k slots, so an item's
-//      softmax needs no exchange. The per-token loads are fp32 sums in a fixed order: every sweep
-//      writes the slots' weights into LDS in target order (an order built once per fit), cut into
-//      pieces each summed by one thread, and each target adds its pieces with a fixed butterfly.
-//      No atomics, so the sums, and the fitted factors, are the same bit for bit on every run (the
-//      reference adds fp32 atomics in arrival order, which is not, iterate.py:8-9).
+//      softmax needs no exchange. The per-token loads are exact integer sums: each weight enters
+//      as round(w 2^31) into a 64-bit LDS counter per target, so the sums, and the fitted factors,
+//      are the same bit for bit on every run whatever order the adds land in (the reference adds
+//      fp32 atomics in arrival order, which is not, iterate.py:8-9).
 //   2-3 repeat per round; the last fit also resolves the problem's one auxiliary value.
 //   4. voronoi_argmin_kernel (only when sigma is asked for): the assignment of every item.
 #include <hip/hip_runtime.h>
@@ -249,12 +248,14 @@ __device__ float spread_unit(const uint16_t* table, int A, const int* tok_s, int
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int cols = min(min(sample, kSpreadSample), A);
   float lo = INFINITY, hi = -INFINITY;
-  // Every read of this lane in flight at once (rows of a large table: each one an HBM round trip).
+  // Every read of this lane in flight at once (rows of a large table: each one an HBM round trip):
+  // the reads carry no condition, lanes and targets past the end re-read the last ones, and the
+  // loop below leaves them out.
   uint16_t raw[kMaxTargets / kRowWaves];
 #pragma unroll
   for (int i = 0; i < kMaxTargets / kRowWaves; ++i) {
-    const int m = wave + kRowWaves * i;
-    raw[i] = (lane < cols && m < M) ? table[static_cast<int64_t>(tok_s[m]) * A + lane] : 0;
+    const int m = min(wave + kRowWaves * i, M - 1);
+    raw[i] = table[static_cast<int64_t>(tok_s[m]) * A + min(lane, cols - 1)];
   }
 #pragma unroll
   for (int i = 0; i < kMaxTargets / kRowWaves; ++i) {
@@ -327,23 +328,31 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_shortlist_kernel(ShortArg
   // The row as order keys, two per register; key 0 marks a position outside the vocabulary. The
   // row is read in 16-byte pieces from the 16-byte boundary at or below its start, which lies
   // `shift` tokens before it: element j of this thread is token 8 (t + 1024 (j / 8)) + j % 8 - shift.
-  // Pieces lying wholly inside the row are one load; the (at most two) straddling an end are read
-  // token by token.
+  // Pieces [first, last] lie wholly inside the row. Every thread reads all of its pieces at once
+  // with no condition, a piece outside that range re-reading one inside it; then the (at most
+  // two) pieces straddling an end are read again token by token.
   uint32_t kk[JT / 2];
   uint32_t kmax = 0;
   const int shift = static_cast<int>((reinterpret_cast<uintptr_t>(row) & 15u) >> 1);
   const uint16_t* base = row - shift;
+  const int first = shift > 0 ? 1 : 0, last = (shift + a.V) / 8 - 1;
+  const bool any_whole = first <= last;
   auto token_of = [&](int j) -> int { return 8 * (t + kRowThreads * (j >> 3)) + (j & 7) - shift; };
+  u32x4 piece[JT / 8];
+  if (any_whole) {
+#pragma unroll
+    for (int c = 0; c < JT / 8; ++c)
+      piece[c] = *reinterpret_cast<const u32x4*>(base + 8 * min(max(t + kRowThreads * c, first), last));
+  }
 #pragma unroll
   for (int c = 0; c < JT / 8; ++c) {
     const int i0 = 8 * (t + kRowThreads * c) - shift;
     uint32_t h[8];
-    if (i0 >= 0 && i0 + 8 <= a.V) {
-      const u32x4 w = *reinterpret_cast<const u32x4*>(base + 8 * (t + kRowThreads * c));
+    if (any_whole && i0 >= 0 && i0 + 8 <= a.V) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        h[2 * e] = w[e] & 0xFFFFu;
-        h[2 * e + 1] = w[e] >> 16;
+        h[2 * e] = piece[c][e] & 0xFFFFu;
+        h[2 * e + 1] = piece[c][e] >> 16;
       }
     } else {
 #pragma unroll
@@ -560,8 +569,10 @@ __device__ __forceinline__ int32_t pack_cost(float c, int target) {
   return (ordered & ~0x7F) | target;
 }
 
-// A workgroup takes 64 items; its four wavefronts each rank a quarter of the targets for them (all
-// of a lane's table reads in flight at once), and the four sorted lists merge in LDS.
+// A workgroup takes 64 items; its four wavefronts each rank a quarter of the targets for them, and
+// the four sorted lists merge pairwise in LDS. Lane b of a wavefront fetches its b-th target's row
+// offset and cost offset; every table read then takes them from that lane as scalars, so the reads
+// carry no condition and all of a lane's reads are in flight at once.
 constexpr int kCondenseItems = 64;
 constexpr int kCondenseWaves = kItemThreads / 64;
 constexpr int kTargetsPerWave = kMaxTargets / kCondenseWaves;
@@ -576,39 +587,70 @@ __device__ __forceinline__ void insert_key(int32_t (&best)[K], int32_t x) {
   }
 }
 
+// The K smallest of two ascending lists, ascending, into a: min(a[i], b[K-1-i]) holds them as an
+// ascending-then-descending sequence, which the bitonic half-cleaners sort.
+template <int K>
+__device__ __forceinline__ void merge_lists(int32_t (&a)[K], const int32_t (&b)[K]) {
+#pragma unroll
+  for (int i = 0; i < K; ++i) a[i] = min(a[i], b[K - 1 - i]);
+#pragma unroll
+  for (int d = K / 2; d >= 1; d >>= 1)
+#pragma unroll
+    for (int i = 0; i < K; ++i)
+      if ((i & d) == 0) {
+        const int32_t lo = min(a[i], a[i + d]), hi = max(a[i], a[i + d]);
+        a[i] = lo;
+        a[i + d] = hi;
+      }
+}
+
 template <int DT, int K>
 __global__ __launch_bounds__(kItemThreads) void voronoi_condense_kernel(CondenseArgs a) {
-  __shared__ int64_t row_s[kMaxTargets];
-  __shared__ float off_s[kMaxTargets];
-  __shared__ int32_t part[kCondenseWaves][K][kCondenseItems];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  __shared__ int32_t part[2][K][kCondenseItems];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int64_t p = blockIdx.y;
-  if (t < a.M) {
-    row_s[t] = table_row(a.tokens[p * a.M + t], a.V) * a.A;
-    off_s[t] = a.offset[p * a.M + t];
-  }
-  __syncthreads();
-  const int item = blockIdx.x * kCondenseItems + lane;
-  const bool live = item < a.A;
   const int per = (a.M + kCondenseWaves - 1) / kCondenseWaves;
   const int m0 = wave * per, m1 = min(a.M, m0 + per);
+  // V * A <= 65528 * 8192 elements, so element offsets fit an int and byte offsets its double.
+  const int mb = min(m0 + (lane & (kTargetsPerWave - 1)), a.M - 1);
+  const int row_bytes = 2 * static_cast<int>(table_row(a.tokens[p * a.M + mb], a.V)) * a.A;
+  const float off = a.offset[p * a.M + mb];
+  const int item = blockIdx.x * kCondenseItems + lane;
+  const uint32_t item_bytes = 2u * static_cast<uint32_t>(min(item, a.A - 1));
+  const __amdgpu_buffer_rsrc_t table = make_rsrc(a.table, 2u * static_cast<uint32_t>(a.V) * static_cast<uint32_t>(a.A));
+  uint16_t raw[kTargetsPerWave];
+#pragma unroll
+  for (int b = 0; b < kTargetsPerWave; ++b)
+    raw[b] = __builtin_amdgcn_raw_buffer_load_b16(table, static_cast<int>(item_bytes),
+                                                  __builtin_amdgcn_readlane(row_bytes, b), 0);
   int32_t best[K];
 #pragma unroll
   for (int s = 0; s < K; ++s) best[s] = INT_MAX;
-  uint16_t raw[kTargetsPerWave];
-#pragma unroll
-  for (int b = 0; b < kTargetsPerWave; ++b) raw[b] = (live && m0 + b < m1) ? a.table[row_s[m0 + b] + item] : 0;
 #pragma unroll
   for (int b = 0; b < kTargetsPerWave; ++b)
-    if (m0 + b < m1) insert_key<K>(best, pack_cost(from_bits16<DT>(raw[b]) + off_s[m0 + b], m0 + b));
+    if (m0 + b < m1) insert_key<K>(best, pack_cost(from_bits16<DT>(raw[b]) + lane_value(off, b), m0 + b));
+  // Waves 1 and 3 hand their lists to 0 and 2, then 2 to 0 (through the slot it read itself).
+  if (wave & 1) {
 #pragma unroll
-  for (int s = 0; s < K; ++s) part[wave][s][lane] = best[s];
+    for (int s = 0; s < K; ++s) part[wave >> 1][s][lane] = best[s];
+  }
   __syncthreads();
-  if (wave != 0 || !live) return;
+  int32_t other[K];
+  if ((wave & 1) == 0) {
 #pragma unroll
-  for (int w = 1; w < kCondenseWaves; ++w)
+    for (int s = 0; s < K; ++s) other[s] = part[wave >> 1][s][lane];
+    merge_lists<K>(best, other);
+    if (wave == 2) {
 #pragma unroll
-    for (int s = 0; s < K; ++s) insert_key<K>(best, part[w][s][lane]);
+      for (int s = 0; s < K; ++s) part[1][s][lane] = best[s];
+    }
+  }
+  __syncthreads();
+  if (wave != 0 || item >= a.A) return;
+#pragma unroll
+  for (int s = 0; s < K; ++s) other[s] = part[1][s][lane];
+  merge_lists<K>(best, other);
 #pragma unroll
   for (int s = 0; s < K; ++s) a.key[(p * K + s) * a.A + item] = best[s];
 }
@@ -630,73 +672,44 @@ struct FitArgs {
   int64_t* decoded;       // [N]
 };
 
-// The condensed problem of one problem holds k * A <= 32768 entries (item, slot). The fit keeps
-// their sweep weights in LDS ordered by target, so a target's load is the sum of its segment; the
-// segments are cut at every multiple of the piece length L into pieces, one thread per piece, so
-// the sums are balanced however unequal the targets' shares are. L is the smallest of 16, 32, 64
-// that keeps the pieces (at most entries / L + 128) within the workgroup.
-constexpr int kMaxEntries = 32768;
-constexpr int kMaxPieces = kRowThreads;
-__device__ __forceinline__ int piece_shift(int entries) {
-  return entries + kMaxTargets * 16 <= kRowThreads * 16 ? 4 : (entries + kMaxTargets * 32 <= kRowThreads * 32 ? 5 : 6);
-}
-// LDS slot of position i: one word of skew every L positions, so the lanes summing consecutive
-// pieces (L apart) read different banks, and a piece (inside one L-block) is contiguous.
-__device__ __forceinline__ int skewed(int i, int shift) { return i + (i >> shift); }
-constexpr int kWsumSlots = kMaxEntries + kMaxEntries / 64 + 8;  // + reads past the last piece
-
-// Entry layout in registers: base cost (float) and, packed, during the setup the entry's target
-// (bits 0..7) and its rank (bits 8..); for the sweeps the byte offset of its target's correction
-// (target * 4, bits 0..8) and of its weight's LDS slot (bits 9..).
-__device__ __forceinline__ int entry_target(uint32_t packed) { return static_cast<int>(packed & 0xFFu); }
-__device__ __forceinline__ int entry_pos(uint32_t packed) { return static_cast<int>(packed >> 8); }
-__device__ __forceinline__ uint32_t corr_offset(uint32_t packed) { return packed & 0x1FFu; }
-__device__ __forceinline__ uint32_t slot_offset(uint32_t packed) { return packed >> 9; }
-
-// Exclusive prefix sum of v over threads 0..127 (the targets), run by the first two wavefronts;
-// thread 127's inclusive value is the total. Every thread calls it (it holds one barrier).
-__device__ __forceinline__ int target_exclusive_scan(int v, int* carry) {
-  const int t = threadIdx.x, lane = t & 63;
-  int inc = 0;
-  if (t < kMaxTargets) {
-    inc = wave_inclusive_scan(v);
-    if (t == 63) *carry = inc;
-  }
-  __syncthreads();
-  return (t >= 64 && t < kMaxTargets ? *carry : 0) + inc - v + 0 * lane;
-}
+// The loads are sums of up to k * A <= 32768 weights. Each weight w (in [0, 1]) enters as the
+// integer round(w 2^31) into a 64-bit LDS counter per target (integer adds: the sum is exact, so
+// it is the same whatever order the workgroup's adds land in); the factor step reads it back as
+// sum 2^-31. Rounding moves a weight by at most 2^-32, and a load by at most its entry count
+// times that, which the load floor (1e-2) dwarfs.
+constexpr float kFixedScale = 2147483648.0f;  // 2^31: w = 1 is 2^31, a u32
+constexpr double kFixedUnit = 1.0 / 2147483648.0;
 
 template <int DT, int K, int IPT>
 __global__ __launch_bounds__(kRowThreads) void voronoi_fit_kernel(FitArgs a) {
-  // wsum: the sweep's weights in target order (target m's segment is [seg[m], seg[m+1])). Before
-  // the sweeps the same storage holds the setup's per-wavefront target masks and counts.
-  __shared__ float wsum[kWsumSlots];
-  __shared__ float psum[kMaxPieces];
+  __shared__ unsigned long long load_fx[kMaxTargets];
   __shared__ float corr[kMaxTargets];
   __shared__ float share_s[kMaxTargets];
   __shared__ int live_s[kMaxTargets];
-  __shared__ int seg[kMaxTargets + 1];
-  __shared__ int pstart[kMaxTargets + 1];
-  __shared__ int carry[2];
+  __shared__ float scale_s;
   __shared__ float best_v[kMaxTargets / 64];
   __shared__ int best_i[kMaxTargets / 64];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int t = threadIdx.x, lane = t & 63;
   const int64_t p = blockIdx.x;
   const int M = a.M, A = a.A;
+  const float u = a.unit[p];
+  float temperature = a.epsilon * u;
+  const float bound = a.limit * u;
+  // A sweep's cost scale -log2(e) / T, formed by one thread and read by all.
+  constexpr float kNegLog2e = -1.4426950408889634f;
   if (t < kMaxTargets) {
     const int64_t c = t < M ? a.counts[p * M + t] : 0;
     live_s[t] = c > 0;
     share_s[t] = logf(fmaxf(static_cast<float>(c), 1e-9f));
     corr[t] = 0.f;
+    load_fx[t] = 0ull;
+    if (t == 0) scale_s = kNegLog2e / temperature;
   }
-  const float u = a.unit[p];
-  float temperature = a.epsilon * u;
-  const float bound = a.limit * u;
 
   // The condensed problem, decoded once (iterate.py:130-134): thread t holds items t + 1024 q and
-  // their K slots.
+  // their K slots: base cost and target.
   float base[IPT][K];
-  uint32_t ent[IPT][K];
+  int target[IPT][K];
   bool valid[IPT];
 #pragma unroll
   for (int q = 0; q < IPT; ++q) {
@@ -704,181 +717,54 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_fit_kernel(FitArgs a) {
     valid[q] = item < A;
 #pragma unroll
     for (int j = 0; j < K; ++j) {
-      const int32_t key = valid[q] ? a.key[(p * K + j) * A + item] : 0;
+      const int32_t key = a.key[(p * K + j) * A + min(item, A - 1)];
       const int32_t carried = key & ~0x7F;
       base[q][j] = __builtin_bit_cast(float, carried >= 0 ? carried : (carried ^ 0x7FFFFFFF));
-      ent[q][j] = static_cast<uint32_t>(key & 0x7F);
+      target[q][j] = key & 0x7F;
     }
   }
-
-  const int shift = piece_shift(K * A);
-  // Target order, item order within a target: deterministic, so the float sums below are too. An
-  // item lists a target at most once, so an entry's rank in its target's segment is the number of
-  // earlier items listing the target: a 64-bit lane mask per (q, wavefront, target) gives the rank
-  // among the wavefront's items, a prefix over (q, wavefront) the rest.
-  constexpr int J = IPT * kRowWaves;  // (q, wavefront) slots, in item order
-  unsigned long long* mask = reinterpret_cast<unsigned long long*>(wsum);      // [16][128]
-  int* wcount = reinterpret_cast<int*>(wsum + 2 * kRowWaves * kMaxTargets);     // [J][128]
-  int* gsum = wcount + J * kMaxTargets;                                         // [8][128]
-#pragma unroll
-  for (int q = 0; q < IPT; ++q) {
-    mask[wave * kMaxTargets + lane] = 0ull;
-    mask[wave * kMaxTargets + 64 + lane] = 0ull;
-    __syncthreads();
-    if (valid[q]) {
-#pragma unroll
-      for (int j = 0; j < K; ++j)
-        __hip_atomic_fetch_or(&mask[wave * kMaxTargets + entry_target(ent[q][j])], 1ull << lane, __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_WORKGROUP);
-    }
-    __syncthreads();
-    const unsigned long long below = (1ull << lane) - 1ull;
-    if (valid[q]) {
-#pragma unroll
-      for (int j = 0; j < K; ++j) {
-        const int m = entry_target(ent[q][j]);
-        ent[q][j] |= static_cast<uint32_t>(__popcll(mask[wave * kMaxTargets + m] & below)) << 8;
-      }
-    }
-    wcount[(q * kRowWaves + wave) * kMaxTargets + lane] = __popcll(mask[wave * kMaxTargets + lane]);
-    wcount[(q * kRowWaves + wave) * kMaxTargets + 64 + lane] = __popcll(mask[wave * kMaxTargets + 64 + lane]);
-    __syncthreads();
-  }
-  // Per target, exclusive prefix over the J slots: thread (g, m) (8 groups x 128 targets) scans J / 8
-  // consecutive slots, then adds the groups before it.
-  {
-    constexpr int SPAN = J / 8;
-    const int m = t & (kMaxTargets - 1), g = t >> 7;
-    int run = 0;
-#pragma unroll
-    for (int i = 0; i < SPAN; ++i) {
-      int* c = &wcount[(g * SPAN + i) * kMaxTargets + m];
-      const int n = *c;
-      *c = run;
-      run += n;
-    }
-    gsum[g * kMaxTargets + m] = run;
-    __syncthreads();
-    int before = 0, len = 0;
-#pragma unroll
-    for (int h = 0; h < 8; ++h) {
-      const int n = gsum[h * kMaxTargets + m];
-      before += h < g ? n : 0;
-      len += n;
-    }
-#pragma unroll
-    for (int i = 0; i < SPAN; ++i) wcount[(g * SPAN + i) * kMaxTargets + m] += before;
-    // Segment starts and piece starts: exclusive scans over the targets of their lengths.
-    const int start = target_exclusive_scan(len, &carry[0]);
-    // Pieces of this target: the L-blocks its segment [start, start + len) overlaps.
-    const int pieces = len > 0 ? ((start + len - 1) >> shift) - (start >> shift) + 1 : 0;
-    const int pfirst = target_exclusive_scan(pieces, &carry[1]);
-    if (t < kMaxTargets) {
-      seg[t] = start;
-      pstart[t] = pfirst;
-      if (t == kMaxTargets - 1) {
-        seg[kMaxTargets] = start + len;
-        pstart[kMaxTargets] = pfirst + pieces;
-      }
-    }
-    __syncthreads();
-  }
-#pragma unroll
-  for (int q = 0; q < IPT; ++q) {
-    if (!valid[q]) continue;
-#pragma unroll
-    for (int j = 0; j < K; ++j) {
-      const int m = entry_target(ent[q][j]);
-      const int pos = seg[m] + wcount[(q * kRowWaves + wave) * kMaxTargets + m] + entry_pos(ent[q][j]);
-      ent[q][j] = (static_cast<uint32_t>(4 * skewed(pos, shift)) << 9) | static_cast<uint32_t>(4 * m);
-    }
-  }
-  // This thread's piece: [piece_lo, piece_hi) of wsum (empty past the last piece).
-  int piece_lo = 0, piece_hi = 0;
-  if (t < pstart[kMaxTargets]) {
-    int m = 0;
-#pragma unroll
-    for (int stride = kMaxTargets / 2; stride >= 1; stride >>= 1)
-      if (pstart[m + stride] <= t) m += stride;
-    const int block = (seg[m] >> shift) + (t - pstart[m]);
-    piece_lo = max(seg[m], block << shift);
-    piece_hi = min(seg[m + 1], (block + 1) << shift);
-  }
-  __syncthreads();  // the setup's storage becomes wsum
+  __syncthreads();
 
   for (int it = 0; it < a.iterations; ++it) {
-    // Each item's softmax over its K slots (iterate.py:142-145), into target order.
-    // exp(-cost / T - max) as exp2 of cost * (-log2(e) / T) less its maximum.
-    const float scale = -1.4426950408889634f / temperature;
-    const char* corr_b = reinterpret_cast<const char*>(corr);
-    char* wsum_b = reinterpret_cast<char*>(wsum);
+    // Each item's softmax over its K slots (iterate.py:142-145), added into the loads
+    // (iterate.py:146-149). exp(-cost / T - max) as exp2 of cost * (-log2(e) / T) less its maximum;
+    // the scale is negative, so the maximum is the cheapest cost times it (rounding is monotone).
+    const float scale = scale_s;
 #pragma unroll
     for (int q = 0; q < IPT; ++q) {
       if (!valid[q]) continue;
       float x[K];
-      float xm = -INFINITY;
+      float cmin = INFINITY;
 #pragma unroll
       for (int j = 0; j < K; ++j) {
-        x[j] = (base[q][j] + *reinterpret_cast<const float*>(corr_b + corr_offset(ent[q][j]))) * scale;
-        xm = fmaxf(xm, x[j]);
+        x[j] = base[q][j] + corr[target[q][j]];
+        cmin = fminf(cmin, x[j]);
       }
+      const float xm = cmin * scale;
       float se = 0.f;
 #pragma unroll
       for (int j = 0; j < K; ++j) {
-        x[j] = __builtin_amdgcn_exp2f(x[j] - xm);
+        x[j] = __builtin_amdgcn_exp2f(fmaf(x[j], scale, -xm));
         se += x[j];
       }
-      const float r = 1.f / se;
+      const float r = __builtin_amdgcn_rcpf(se) * kFixedScale;
 #pragma unroll
-      for (int j = 0; j < K; ++j) *reinterpret_cast<float*>(wsum_b + slot_offset(ent[q][j])) = x[j] * r;
+      for (int j = 0; j < K; ++j) {
+        const uint32_t w = static_cast<uint32_t>(fmaf(x[j], r, 0.5f));
+        __hip_atomic_fetch_add(&load_fx[target[q][j]], static_cast<unsigned long long>(w), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
     }
     __syncthreads();
-    // The loads (iterate.py:146-149): piece sums, then each target adds its pieces in order.
-    if (piece_hi > piece_lo) {
-      // The piece is contiguous in LDS and ends inside its L-block (or at the block's last slot,
-      // followed by the skew word): reads eight at a time past its end stay inside the array and
-      // are masked out of the sum, which runs in position order.
-      const float* src = wsum + skewed(piece_lo, shift);
-      const int len = piece_hi - piece_lo;
-      float sum = 0.f;
-#pragma unroll 1
-      for (int i = 0; i < len; i += 8) {
-        float v[8];
-#pragma unroll
-        for (int w = 0; w < 8; ++w) v[w] = src[i + w];
-#pragma unroll
-        for (int w = 0; w < 8; ++w) sum += i + w < len ? v[w] : 0.f;
-      }
-      psum[t] = sum;
-    }
-    __syncthreads();
-    // The factor step (iterate.py:150-154). Eight threads per target (8 m + g) add contiguous
-    // shares of its pieces; the octet combines them in a fixed butterfly.
-    {
-      const int m = t >> 3, g = t & 7;
-      float load = 0.f;
-      if (m < M) {
-        const int first = pstart[m], count = pstart[m + 1] - first;
-        const int share = (count + 7) >> 3;
-        const int lo = first + min(count, g * share), hi = first + min(count, (g + 1) * share);
-#pragma unroll 1
-        for (int i = lo; i < hi; i += 8) {
-          float v[8];
-#pragma unroll
-          for (int w = 0; w < 8; ++w) v[w] = psum[min(i + w, hi - 1)];
-#pragma unroll
-          for (int w = 0; w < 8; ++w) load += i + w < hi ? v[w] : 0.f;
-        }
-      }
-      load += dpp<kDppXor1>(load);
-      load += dpp<kDppXor2>(load);
-      load += dpp<kDppHalfMirror>(load);
-      if (g == 0 && m < M) {
-        float step = temperature * (logf(fmaxf(load, kLoadFloor)) - share_s[m]);
-        step = fminf(fmaxf(step, -bound), bound);
-        const float c = corr[m] + a.relax * step;
-        corr[m] = live_s[m] ? c : 0.f;
-      }
+    // The factor step (iterate.py:150-154), one thread per target; its counter restarts at zero.
+    if (t < M) {
+      const float load = static_cast<float>(static_cast<double>(load_fx[t]) * kFixedUnit);
+      load_fx[t] = 0ull;
+      float step = temperature * (logf(fmaxf(load, kLoadFloor)) - share_s[t]);
+      step = fminf(fmaxf(step, -bound), bound);
+      const float c = corr[t] + a.relax * step;
+      corr[t] = live_s[t] ? c : 0.f;
+      if (t == 0) scale_s = kNegLog2e / (temperature * a.anneal);
     }
     __syncthreads();
     temperature *= a.anneal;
