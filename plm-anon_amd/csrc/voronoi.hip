@@ -45,13 +45,24 @@ constexpr float kBlocked = 1e3f;   // iterate.py:25
 constexpr float kLoadFloor = 1e-2f;
 constexpr float kEmpty = -1e30f;   // iterate.py:26
 
-// Order-preserving 16-bit key of a bf16 or fp16 value (both keep the sign in bit 15): a larger
-// value has a larger key. -0 is folded onto +0 first so equal values have equal keys.
-__device__ __forceinline__ uint32_t order_key16(uint32_t bits) {
-  if (bits == 0x8000u) bits = 0;
-  return bits ^ ((bits & 0x8000u) ? 0xFFFFu : 0x8000u);
+// Order-preserving 16-bit keys of bf16 or fp16 values (both keep the sign in bit 15): a larger
+// value has a larger key, -0 and +0 share 0x8000, and no value has key 0, which marks a position
+// outside the vocabulary. A negative value maps to 0x10000 - bits, the rest to bits | 0x8000. Two
+// keys per 32-bit word, in packed 16-bit integer instructions.
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t order_keys2(uint32_t w) {
+  const uint32_t negative = __builtin_bit_cast(uint32_t, __builtin_bit_cast(s16x2, w) >> (s16x2){15, 15});
+  const uint32_t flipped = __builtin_bit_cast(uint32_t, (u16x2){0, 0} - __builtin_bit_cast(u16x2, w));
+  return (flipped & negative) | ((w | 0x80008000u) & ~negative);
 }
-__device__ __forceinline__ uint32_t key16_bits(uint32_t key) { return key ^ ((key & 0x8000u) ? 0x8000u : 0xFFFFu); }
+__device__ __forceinline__ uint32_t max_keys2(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
+}
+__device__ __forceinline__ uint32_t order_key16(uint32_t bits) { return order_keys2(bits & 0xFFFFu) & 0xFFFFu; }
+__device__ __forceinline__ uint32_t key16_bits(uint32_t key) {
+  return key >= 0x8000u ? key & 0x7FFFu : (0x10000u - key) & 0xFFFFu;
+}
 
 // A caller's token id as a table row, clamped into [0, V) so no input reads outside the table.
 __device__ __forceinline__ int64_t table_row(int64_t token, int V) { return token < 0 ? 0 : (token >= V ? V - 1 : token); }
@@ -106,16 +117,6 @@ __device__ __forceinline__ uint32_t wave_max(uint32_t u) {
   return max(max(static_cast<uint32_t>(lane_value(v, 0)), static_cast<uint32_t>(lane_value(v, 16))),
              max(static_cast<uint32_t>(lane_value(v, 32)), static_cast<uint32_t>(lane_value(v, 48))));
 }
-__device__ __forceinline__ uint32_t wave_min(uint32_t u) {
-  int v = static_cast<int>(u);
-  v = static_cast<int>(min(static_cast<uint32_t>(v), static_cast<uint32_t>(dpp<kDppXor1>(v))));
-  v = static_cast<int>(min(static_cast<uint32_t>(v), static_cast<uint32_t>(dpp<kDppXor2>(v))));
-  v = static_cast<int>(min(static_cast<uint32_t>(v), static_cast<uint32_t>(dpp<kDppHalfMirror>(v))));
-  v = static_cast<int>(min(static_cast<uint32_t>(v), static_cast<uint32_t>(dpp<kDppMirror>(v))));
-  return min(min(static_cast<uint32_t>(lane_value(v, 0)), static_cast<uint32_t>(lane_value(v, 16))),
-             min(static_cast<uint32_t>(lane_value(v, 32)), static_cast<uint32_t>(lane_value(v, 48))));
-}
-
 // Inclusive prefix sum over the 64 lanes (row-wise shifts, then the row carries broadcast).
 __device__ __forceinline__ int wave_inclusive_scan(int v) {
   v += dpp<kDppShr1>(v);
@@ -132,43 +133,18 @@ __device__ __forceinline__ int wave_inclusive_scan(int v) {
 // posts (one per lane) and reduces them the same way. Calls alternate between two scratch rows,
 // so consecutive calls need no barrier between them.
 struct BlockScratch {
-  int i[2][3][kRowWaves];
+  int i[2][kRowWaves];
   float f[2][kRowWaves];
   uint32_t u[2][kRowWaves];
 };
 
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x & 63); }
 
-__device__ __forceinline__ int block_count(bool pred, BlockScratch& s, int& parity) {
-  const int n = __popcll(__ballot(pred));
-  if (lane_id() == 0) s.i[parity][0][threadIdx.x >> 6] = n;
-  __syncthreads();
-  const int total = wave_sum(lane_id() < kRowWaves ? s.i[parity][0][lane_id()] : 0);
-  parity ^= 1;
-  return total;
-}
-
-// Three counts in one barrier.
-__device__ __forceinline__ void block_count3(bool p0, bool p1, bool p2, int (&n)[3], BlockScratch& s, int& parity) {
-  const int c0 = __popcll(__ballot(p0)), c1 = __popcll(__ballot(p1)), c2 = __popcll(__ballot(p2));
-  if (lane_id() == 0) {
-    s.i[parity][0][threadIdx.x >> 6] = c0;
-    s.i[parity][1][threadIdx.x >> 6] = c1;
-    s.i[parity][2][threadIdx.x >> 6] = c2;
-  }
-  __syncthreads();
-  const bool in = lane_id() < kRowWaves;
-  n[0] = wave_sum(in ? s.i[parity][0][lane_id()] : 0);
-  n[1] = wave_sum(in ? s.i[parity][1][lane_id()] : 0);
-  n[2] = wave_sum(in ? s.i[parity][2][lane_id()] : 0);
-  parity ^= 1;
-}
-
 __device__ __forceinline__ int block_sum_int(int v, BlockScratch& s, int& parity) {
   v = wave_sum(v);
-  if (lane_id() == 0) s.i[parity][0][threadIdx.x >> 6] = v;
+  if (lane_id() == 0) s.i[parity][threadIdx.x >> 6] = v;
   __syncthreads();
-  const int total = wave_sum(lane_id() < kRowWaves ? s.i[parity][0][lane_id()] : 0);
+  const int total = wave_sum(lane_id() < kRowWaves ? s.i[parity][lane_id()] : 0);
   parity ^= 1;
   return total;
 }
@@ -191,22 +167,13 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t v, BlockScratch& s, i
   return total;
 }
 
-__device__ __forceinline__ uint32_t block_min_u32(uint32_t v, BlockScratch& s, int& parity) {
-  v = wave_min(v);
-  if (lane_id() == 0) s.u[parity][threadIdx.x >> 6] = v;
-  __syncthreads();
-  const uint32_t total = wave_min(lane_id() < kRowWaves ? s.u[parity][lane_id()] : 0xFFFFFFFFu);
-  parity ^= 1;
-  return total;
-}
-
 // Exclusive prefix sum over the workgroup in thread order; `total` gets the sum.
 __device__ __forceinline__ int block_exclusive_scan(int v, int& total, BlockScratch& s, int& parity) {
   const int lane = lane_id(), wave = threadIdx.x >> 6;
   const int inc = wave_inclusive_scan(v);
-  if (lane == 63) s.i[parity][0][wave] = inc;
+  if (lane == 63) s.i[parity][wave] = inc;
   __syncthreads();
-  const int c = lane < kRowWaves ? s.i[parity][0][lane] : 0;
+  const int c = lane < kRowWaves ? s.i[parity][lane] : 0;
   const int base = wave_sum(lane < wave ? c : 0);
   total = wave_sum(c);
   parity ^= 1;
@@ -239,26 +206,34 @@ __device__ __forceinline__ float round_model(float v) {
 }
 
 // Spread (iterate.py:275-284): the mean over the first min(sample, A) items of the gap between the
-// worst and best of the M targets tok_s[] (in LDS), the gap rounded to the table's dtype as the
-// reference subtracts in it. Called by all 1024 threads.
-template <int DT>
-__device__ float spread_unit(const uint16_t* table, int A, const int* tok_s, int M, int sample,
-                             float (*lo_s)[kSpreadSample], float (*hi_s)[kSpreadSample], BlockScratch& red,
-                             int& parity) {
+// worst and best of the M targets, the gap rounded to the table's dtype as the reference subtracts
+// in it. In three steps, all 1024 threads taking part, so a caller can work while the reads are in
+// flight:
+// spread_reads issues this thread's table reads (column min(lane, cols - 1) of the rows of targets
+// wave + 16 i, clamped to M - 1: no conditions, all in flight at once, each an HBM round trip);
+// spread_post posts each wavefront's column minima and maxima; after a barrier, spread_mean gives
+// wavefront 0 the mean over the columns of the rounded gap.
+constexpr int kSpreadReads = kMaxTargets / kRowWaves;
+__device__ __forceinline__ int spread_cols(int A, int sample) { return min(min(sample, kSpreadSample), A); }
+
+template <typename RowOf>
+__device__ __forceinline__ void spread_reads(const uint16_t* table, int A, int M, int sample, RowOf row_of,
+                                             uint16_t (&raw)[kSpreadReads]) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int cols = min(min(sample, kSpreadSample), A);
+  const int cols = spread_cols(A, sample);
+#pragma unroll
+  for (int i = 0; i < kSpreadReads; ++i)
+    raw[i] = table[static_cast<int64_t>(row_of(min(wave + kRowWaves * i, M - 1))) * A + min(lane, cols - 1)];
+}
+
+template <int DT>
+__device__ __forceinline__ void spread_post(const uint16_t (&raw)[kSpreadReads], int A, int M, int sample,
+                                            float (*lo_s)[kSpreadSample], float (*hi_s)[kSpreadSample]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int cols = spread_cols(A, sample);
   float lo = INFINITY, hi = -INFINITY;
-  // Every read of this lane in flight at once (rows of a large table: each one an HBM round trip):
-  // the reads carry no condition, lanes and targets past the end re-read the last ones, and the
-  // loop below leaves them out.
-  uint16_t raw[kMaxTargets / kRowWaves];
 #pragma unroll
-  for (int i = 0; i < kMaxTargets / kRowWaves; ++i) {
-    const int m = min(wave + kRowWaves * i, M - 1);
-    raw[i] = table[static_cast<int64_t>(tok_s[m]) * A + min(lane, cols - 1)];
-  }
-#pragma unroll
-  for (int i = 0; i < kMaxTargets / kRowWaves; ++i) {
+  for (int i = 0; i < kSpreadReads; ++i) {
     if (lane < cols && wave + kRowWaves * i < M) {
       const float v = from_bits16<DT>(raw[i]);
       lo = fminf(lo, v);
@@ -267,19 +242,20 @@ __device__ float spread_unit(const uint16_t* table, int A, const int* tok_s, int
   }
   lo_s[wave][lane] = lo;
   hi_s[wave][lane] = hi;
-  __syncthreads();
-  float gap = 0.f;
-  if (wave == 0) {
-    lo = lo_s[0][lane];
-    hi = hi_s[0][lane];
+}
+
+template <int DT>
+__device__ __forceinline__ float spread_mean(int A, int sample, const float (*lo_s)[kSpreadSample],
+                                             const float (*hi_s)[kSpreadSample]) {
+  const int lane = threadIdx.x & 63;
+  const int cols = spread_cols(A, sample);
+  float lo = lo_s[0][lane], hi = hi_s[0][lane];
 #pragma unroll
-    for (int g = 1; g < kRowWaves; ++g) {
-      lo = fminf(lo, lo_s[g][lane]);
-      hi = fmaxf(hi, hi_s[g][lane]);
-    }
-    gap = lane < cols ? round_model<DT>(hi - lo) : 0.f;
+  for (int g = 1; g < kRowWaves; ++g) {
+    lo = fminf(lo, lo_s[g][lane]);
+    hi = fmaxf(hi, hi_s[g][lane]);
   }
-  return block_sum_float(gap, red, parity) / static_cast<float>(cols);
+  return wave_sum(lane < cols ? round_model<DT>(hi - lo) : 0.f) / static_cast<float>(cols);
 }
 
 // Prior (iterate.py:286-290), in the reference's operation order.
@@ -309,30 +285,59 @@ struct ShortArgs {
 // larger ones go through a bitonic sort.
 constexpr int kRankCap = 256;
 
+// Threads whose largest key reaches the threshold hand their keys to the workgroup through LDS, up
+// to this many (more only when many equal values sit at the threshold: then each scans its own).
+constexpr int kQualifyCap = 256;
+
+// Wavefront 0 over a 256-bin histogram: the largest bin b whose count of bins >= b reaches `need`.
+// out[0] = b, out[1] = need less the count of bins above b (>= 1).
+__device__ __forceinline__ void select_bin(const int* hist, int need, int* out) {
+  const int lane = threadIdx.x & 63;
+  const int c0 = hist[4 * lane], c1 = hist[4 * lane + 1], c2 = hist[4 * lane + 2], c3 = hist[4 * lane + 3];
+  const int inc = wave_inclusive_scan(c0 + c1 + c2 + c3);
+  const int above = lane_value(inc, 63) - inc;  // bins past 4 lane + 3
+  const int s3 = above + c3, s2 = s3 + c2, s1 = s2 + c1, s0 = s1 + c0;
+  if (s0 >= need && above < need) {
+    const int b = s3 >= need ? 3 : (s2 >= need ? 2 : (s1 >= need ? 1 : 0));
+    out[0] = 4 * lane + b;
+    out[1] = need - (b == 3 ? above : (b == 2 ? s3 : (b == 1 ? s2 : s1)));
+  }
+}
+
 // JT = elements per thread (a multiple of 8 covering V / 1024).
 template <int DT, int JT>
 __global__ __launch_bounds__(kRowThreads) void voronoi_shortlist_kernel(ShortArgs a) {
+  constexpr int W = JT / 2;  // key words per thread
   __shared__ __align__(16) uint32_t cand[kCandidateCap];
+  __shared__ __align__(16) uint32_t qkeys[kQualifyCap][W];
+  __shared__ int qowner[kQualifyCap];
+  __shared__ int hist[2][256];
+  __shared__ int sel[4];
+  __shared__ int counters[2];  // threads that reach the threshold, candidates
   __shared__ uint32_t top[kMaxTargets];
   __shared__ BlockScratch red;
   __shared__ float lo_s[kRowWaves][kSpreadSample], hi_s[kRowWaves][kSpreadSample];
   __shared__ __align__(16) float rem_s[kMaxTargets];
   __shared__ int rank_s[kMaxTargets];
-  __shared__ int tok_s[kMaxTargets];
   int parity = 0;
   const int t = threadIdx.x;
+  const int wave = t >> 6;
   const int64_t p = blockIdx.x;
   const int M = a.M;
   const uint16_t* row = a.logits + p * a.ld;
+  if (t < 512) (&hist[0][0])[t] = 0;
+  if (t < 2) counters[t] = 0;
+  if (t < kRankCap + 4) cand[t] = 0u;  // the ranking reads up to a multiple of four past the last candidate
 
-  // The row as order keys, two per register; key 0 marks a position outside the vocabulary. The
-  // row is read in 16-byte pieces from the 16-byte boundary at or below its start, which lies
-  // `shift` tokens before it: element j of this thread is token 8 (t + 1024 (j / 8)) + j % 8 - shift.
-  // Pieces [first, last] lie wholly inside the row. Every thread reads all of its pieces at once
-  // with no condition, a piece outside that range re-reading one inside it; then the (at most
-  // two) pieces straddling an end are read again token by token.
-  uint32_t kk[JT / 2];
-  uint32_t kmax = 0;
+  // The row as order keys, two per register (element j of this thread in half j % 2 of word j / 2);
+  // key 0 marks a position outside the vocabulary. The row is read in 16-byte pieces from the
+  // 16-byte boundary at or below its start, which lies `shift` tokens before it: element j of this
+  // thread is token 8 (t + 1024 (j / 8)) + j % 8 - shift. Pieces [first, last] lie wholly inside the
+  // row. Every thread reads all of its pieces at once with no condition, a piece outside that range
+  // re-reading one inside it; then the (at most two) pieces straddling an end are read again token
+  // by token.
+  uint32_t kk[W];
+  uint32_t kmax2 = 0;
   const int shift = static_cast<int>((reinterpret_cast<uintptr_t>(row) & 15u) >> 1);
   const uint16_t* base = row - shift;
   const int first = shift > 0 ? 1 : 0, last = (shift + a.V) / 8 - 1;
@@ -347,28 +352,22 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_shortlist_kernel(ShortArg
 #pragma unroll
   for (int c = 0; c < JT / 8; ++c) {
     const int i0 = 8 * (t + kRowThreads * c) - shift;
-    uint32_t h[8];
     if (any_whole && i0 >= 0 && i0 + 8 <= a.V) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        h[2 * e] = piece[c][e] & 0xFFFFu;
-        h[2 * e + 1] = piece[c][e] >> 16;
-      }
+      for (int e = 0; e < 4; ++e) kk[4 * c + e] = order_keys2(piece[c][e]);
     } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) h[e] = (i0 + e >= 0 && i0 + e < a.V) ? row[i0 + e] : 0x8000u;
+      for (int e = 0; e < 4; ++e) {
+        const int i = i0 + 2 * e;
+        const uint32_t lo = (i >= 0 && i < a.V) ? order_key16(row[i]) : 0u;
+        const uint32_t hi = (i + 1 >= 0 && i + 1 < a.V) ? order_key16(row[i + 1]) : 0u;
+        kk[4 * c + e] = lo | (hi << 16);
+      }
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t k = (i0 + e >= 0 && i0 + e < a.V) ? order_key16(h[e]) : 0u;
-      const int j = 8 * c + e;
-      if (j & 1)
-        kk[j >> 1] |= k << 16;
-      else
-        kk[j >> 1] = k;
-      kmax = max(kmax, k);
-    }
+    for (int e = 0; e < 4; ++e) kmax2 = max_keys2(kmax2, kk[4 * c + e]);
   }
+  const uint32_t kmax = max(kmax2 & 0xFFFFu, kmax2 >> 16);
   auto key_of = [&](int j) -> uint32_t { return (kk[j >> 1] >> (16 * (j & 1))) & 0xFFFFu; };
 
   // The normaliser max + log(sum exp(l - max)) (iterate.py:56-80, values clamped to the reference's
@@ -388,30 +387,55 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_shortlist_kernel(ShortArg
   }
 
   // Threshold: the M-th largest per-thread maximum. At least M elements reach it, so the M largest
-  // elements all do. The thread maxima share the key bits above the highest bit where the smallest
-  // and largest differ; the rest is found two bits per barrier.
-  const uint32_t klo = block_min_u32(kmax, red, parity);
-  const uint32_t khi = block_max_u32(kmax, red, parity);
-  int bits = klo == khi ? 0 : 32 - __clz(klo ^ khi);
-  uint32_t tau = klo & ~((1u << bits) - 1u);
-  while (bits >= 2) {
-    bits -= 2;
-    int n[3];
-    block_count3(kmax >= (tau | (1u << bits)), kmax >= (tau | (2u << bits)), kmax >= (tau | (3u << bits)), n, red,
-                 parity);
-    tau |= (n[2] >= M ? 3u : n[1] >= M ? 2u : n[0] >= M ? 1u : 0u) << bits;
-  }
-  if (bits == 1 && block_count(kmax >= (tau | 1u), red, parity) >= M) tau |= 1u;
+  // elements all do. Found as a radix selection over the 1024 maxima: a histogram of their high
+  // bytes picks the high byte, a histogram of the low bytes of the maxima in that bin the low one.
+  __syncthreads();  // the histograms and counters are zero
+  atomicAdd(&hist[0][kmax >> 8], 1);
+  __syncthreads();
+  if (wave == 0) select_bin(hist[0], M, &sel[0]);
+  __syncthreads();
+  if ((kmax >> 8) == static_cast<uint32_t>(sel[0])) atomicAdd(&hist[1][kmax & 0xFFu], 1);
+  __syncthreads();
+  if (wave == 0) select_bin(hist[1], sel[1], &sel[2]);
+  __syncthreads();
+  const uint32_t tau = (static_cast<uint32_t>(sel[0]) << 8) | static_cast<uint32_t>(sel[2]);
 
-  int mine = 0;
+  // Candidates: every element at or above the threshold, as sort keys (value key above, 0xFFFF -
+  // token below, so equal values order by ascending token id). Their order in cand[] is the order
+  // the LDS counter hands out slots in; the ranking below depends only on the set.
+  const bool reaches = kmax != 0 && kmax >= tau;
+  if (reaches) {
+    const int slot = atomicAdd(&counters[0], 1);
+    if (slot < kQualifyCap) {
+      qowner[slot] = t;
 #pragma unroll
-  for (int j = 0; j < JT; ++j) {
-    const uint32_t k = key_of(j);
-    mine += (k != 0 && k >= tau) ? 1 : 0;
+      for (int w = 0; w < W; w += 4)
+        *reinterpret_cast<u32x4*>(&qkeys[slot][w]) = u32x4{kk[w], kk[w + 1], kk[w + 2], kk[w + 3]};
+    }
   }
-  int total = 0;
-  int off = block_exclusive_scan(mine, total, red, parity);
-  // Sort key: value key above, 0xFFFF - token below, so equal values order by ascending token id.
+  __syncthreads();
+  auto is_candidate = [&](uint32_t k) { return k != 0 && k >= tau; };
+  auto take = [&](uint32_t k, int token) {
+    if (is_candidate(k)) {
+      const int pos = atomicAdd(&counters[1], 1);
+      if (pos < kCandidateCap) cand[pos] = (k << 16) | (0xFFFFu - static_cast<uint32_t>(token));
+    }
+  };
+  const int n_reach = counters[0];
+  if (n_reach <= kQualifyCap) {
+    for (int f = t; f < n_reach * W; f += kRowThreads) {
+      const int slot = f / W, w = f - slot * W;
+      const uint32_t k2 = qkeys[slot][w];
+      const int token = 8 * (qowner[slot] + kRowThreads * (w >> 2)) + 2 * (w & 3) - shift;
+      take(k2 & 0xFFFFu, token);
+      take(k2 >> 16, token + 1);
+    }
+  } else if (reaches) {
+#pragma unroll
+    for (int j = 0; j < JT; ++j) take(key_of(j), token_of(j));
+  }
+  __syncthreads();
+  int total = counters[1];
   if (total > kCandidateCap) {
     // Many elements tie at the threshold (flat logits): bisect the full 32-bit sort key instead,
     // which leaves exactly M elements at or above it. Rare, so the passes re-read the row rather
@@ -427,25 +451,19 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_shortlist_kernel(ShortArg
       for (int i = t; i < a.V; i += kRowThreads) n += sort_key(i) >= c ? 1 : 0;
       if (block_sum_int(n, red, parity) >= M) kappa = c;
     }
-    mine = 0;
+    int mine = 0;
     for (int i = t; i < a.V; i += kRowThreads) mine += sort_key(i) >= kappa ? 1 : 0;
-    off = block_exclusive_scan(mine, total, red, parity);
+    int off = block_exclusive_scan(mine, total, red, parity);
     for (int i = t; i < a.V; i += kRowThreads) {
       const uint32_t sk = sort_key(i);
       if (sk >= kappa && sk != 0) cand[off++] = sk;
     }
-  } else {
-#pragma unroll
-    for (int j = 0; j < JT; ++j) {
-      const uint32_t k = key_of(j);
-      if (k != 0 && k >= tau) cand[off++] = (k << 16) | (0xFFFFu - static_cast<uint32_t>(token_of(j)));
-    }
+    if (t >= total && t < kRankCap + 4) cand[t] = 0u;  // total == M here: clear the first pass's rest
+    __syncthreads();
   }
   if (total <= kRankCap) {
     // Rank by counting: sort keys are unique, so a candidate's rank is the number of larger ones.
     const int padded = (total + 3) & ~3;
-    if (t >= total && t < padded) cand[t] = 0u;
-    __syncthreads();
     // Thread 4 i + g counts, for candidate i, the larger keys among every fourth group of four.
     {
       const int i = t >> 2, g = t & 3;
@@ -459,7 +477,7 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_shortlist_kernel(ShortArg
       rank += dpp<kDppXor2>(rank);
       if (g == 0 && i < total && rank < M) top[rank] = key;
     }
-    // fewer than M candidates only for a degenerate row (NaN keys): those slots read as key 0
+    // every in-row element has a nonzero key and V >= M, so this only guards the slots
     if (t < M && t >= total) top[t] = 0u;
   } else {
     int n_sort = M;
@@ -471,27 +489,45 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_shortlist_kernel(ShortArg
   }
   __syncthreads();
 
-  // Quotas (iterate.py:214-223, 272-273): threads < M hold target t. The shortlist's softmax is
-  // formed against its largest logit.
-  const float v0 = from_bits16<DT>(static_cast<uint16_t>(key16_bits(top[0] >> 16)));
-  float val = 0.f, pr = 0.f;
-  if (t < M) {
-    const uint32_t sk = top[t];
-    tok_s[t] = min(static_cast<int>(0xFFFFu - (sk & 0xFFFFu)), a.V - 1);  // in range even for a degenerate row
-    val = from_bits16<DT>(static_cast<uint16_t>(key16_bits(sk >> 16)));
-    pr = expf(val - v0);
+  // The spread's reads go out first (every wavefront takes its targets' tokens from top[]); the
+  // quotas run while they are in flight.
+  auto top_token = [&](int m) { return min(static_cast<int>(0xFFFFu - (top[m] & 0xFFFFu)), a.V - 1); };
+  uint16_t spread_raw[kSpreadReads];
+  spread_reads(a.table, a.A, M, kSpreadSample, top_token, spread_raw);
+  // Quotas (iterate.py:214-223, 272-273) by wavefront 0, lane l holding targets l and l + 64. The
+  // shortlist's softmax is formed against its largest logit.
+  float val[2] = {0.f, 0.f};
+  int cnt[2] = {0, 0};
+  int remaining = 0;
+  if (wave == 0) {
+    const int lane = t;
+    const float v0 = from_bits16<DT>(static_cast<uint16_t>(key16_bits(top[0] >> 16)));
+    float pr[2] = {0.f, 0.f};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int m = lane + 64 * h;
+      if (m < M) {
+        val[h] = from_bits16<DT>(static_cast<uint16_t>(key16_bits(top[m] >> 16)));
+        pr[h] = expf(val[h] - v0);
+      }
+    }
+    const float psum = wave_sum(pr[0] + pr[1]);
+    int floors = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int m = lane + 64 * h;
+      if (m < M) {
+        const float exact = (pr[h] / psum) * static_cast<float>(a.A);
+        const float fl = floorf(exact);
+        cnt[h] = static_cast<int>(fl);
+        rem_s[m] = exact - fl;
+        floors += cnt[h];
+      }
+    }
+    remaining = a.A - wave_sum(floors);
   }
-  const float psum = block_sum_float(pr, red, parity);
-  float rem = 0.f;
-  int cnt = 0;
-  if (t < M) {
-    const float exact = (pr / psum) * static_cast<float>(a.A);
-    const float fl = floorf(exact);
-    cnt = static_cast<int>(fl);
-    rem = exact - fl;
-    rem_s[t] = rem;
-  }
-  const int remaining = a.A - block_sum_int(cnt, red, parity);  // its barrier also publishes rem_s / tok_s
+  spread_post<DT>(spread_raw, a.A, M, kSpreadSample, lo_s, hi_s);
+  __syncthreads();  // rem_s, the spread's minima and maxima
   // Remainder ranks: thread 8 m + g compares target m's remainder with targets [16 g, 16 g + 16);
   // the eight partial counts of m sit in one lane octet and add up there.
   {
@@ -512,18 +548,24 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_shortlist_kernel(ShortArg
     part += dpp<kDppHalfMirror>(part);
     if (g == 0 && m < M) rank_s[m] = part;
   }
-  __syncthreads();
-  if (t < M) cnt += rank_s[t] < remaining ? 1 : 0;
-
-  const float unit = spread_unit<DT>(a.table, a.A, tok_s, M, kSpreadSample, lo_s, hi_s, red, parity);
-  if (t < M) {
-    const int64_t o = p * M + t;
-    a.prior[o] = prior_factor(cnt, unit, a.A, a.weight);
-    a.tokens[o] = tok_s[t];
-    a.counts[o] = cnt;
-    if (a.values != nullptr) a.values[o] = val;
+  float unit = 0.f;
+  if (wave == 0) unit = spread_mean<DT>(a.A, kSpreadSample, lo_s, hi_s);
+  __syncthreads();  // rank_s
+  if (wave == 0) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int m = t + 64 * h;
+      if (m < M) {
+        const int c = cnt[h] + (rank_s[m] < remaining ? 1 : 0);
+        const int64_t o = p * M + m;
+        a.prior[o] = prior_factor(c, unit, a.A, a.weight);
+        a.tokens[o] = top_token(m);
+        a.counts[o] = c;
+        if (a.values != nullptr) a.values[o] = val[h];
+      }
+    }
+    if (t == 0) a.unit[p] = unit;
   }
-  if (t == 0) a.unit[p] = unit;
 }
 
 // Standalone spread and prior, for callers that run the engine's steps one by one.
@@ -536,15 +578,16 @@ struct SpreadArgs {
 
 template <int DT>
 __global__ __launch_bounds__(kRowThreads) void voronoi_spread_kernel(SpreadArgs a) {
-  __shared__ BlockScratch red;
   __shared__ float lo_s[kRowWaves][kSpreadSample], hi_s[kRowWaves][kSpreadSample];
-  __shared__ int tok_s[kMaxTargets];
-  int parity = 0;
   const int64_t p = blockIdx.x;
-  if (threadIdx.x < a.M) tok_s[threadIdx.x] = static_cast<int>(table_row(a.tokens[p * a.M + threadIdx.x], a.V));
+  uint16_t raw[kSpreadReads];
+  spread_reads(a.table, a.A, a.M, a.sample, [&](int m) { return table_row(a.tokens[p * a.M + m], a.V); }, raw);
+  spread_post<DT>(raw, a.A, a.M, a.sample, lo_s, hi_s);
   __syncthreads();
-  const float unit = spread_unit<DT>(a.table, a.A, tok_s, a.M, a.sample, lo_s, hi_s, red, parity);
-  if (threadIdx.x == 0) a.unit[p] = unit;
+  if (threadIdx.x < 64) {
+    const float unit = spread_mean<DT>(a.A, a.sample, lo_s, hi_s);
+    if (threadIdx.x == 0) a.unit[p] = unit;
+  }
 }
 
 __global__ __launch_bounds__(kMaxTargets) void voronoi_prior_kernel(const int64_t* counts, const float* unit,
