@@ -9,6 +9,8 @@ and HIP-graph replays give identical results (flags are per launch); the error f
 
 from __future__ import annotations
 
+import math
+
 import pytest
 import torch
 
@@ -319,6 +321,48 @@ def test_round_chain_graph_replays_with_new_inputs(device):
             for i in (0, 1, 2, 3, 92, 93, 94, 95):
                 cols = sample[sample < ws[i].shape[0]]
                 _oracle_columns(links[i].x, ws[i], ys[i], cols)
+    chain.check()
+
+
+def test_config4_round_chain_all_columns(device):
+    """Config 4's round: all 128 block linears of the 32-block hidden-2560 round (QKV 2560 -> 7680,
+    attn-out, MLP up 2560 -> 10240, down) at M = 56 in one tile-flag launch, with the round's chain
+    tile and splits, launched twice with a new input and NaN-filled outputs. Every link equals its
+    per-linear launch bit for bit, and the first and last blocks' four linears match the CPU oracle
+    on every column."""
+    from plm_amd import _lib, gemm_tables
+    from plm_amd.fast_gemm import _tile
+    from plm_amd.tiles import packed_chain_split
+
+    M, hidden = 56, 2560
+    cfg = gemm_tables.round_chain_tile(hidden, M)
+    G = _lib.lib().plm_gemm_packed_resident_workgroups(_lib.PLM_BF16, M, _tile(cfg))
+    assert G > 0
+    shapes = [(gm.N, gm.K) for gm in workloads.gpt_block(hidden, 4 * hidden)] * 32
+    # Weights ~ N(0, 1/K), so that activations keep their scale over the 128 links (with a fixed
+    # 0.02 they grow about 2x per block, to ~1e10: outputs with heavy cancellation then carry fp32
+    # accumulation error beyond one bf16 step, on the oracle's side of the comparison as much as
+    # on the kernel's).
+    gw = torch.Generator(device=device).manual_seed(90)
+    ws = [(torch.randn(n, k, generator=gw, device=device) / math.sqrt(k)).bfloat16() for n, k in shapes]
+    g = torch.Generator(device=device).manual_seed(91)
+    x = torch.randn(M, hidden, generator=g, device=device).bfloat16()
+    links, ys = _chain(x, ws, [packed_chain_split(n, k, cfg, G) for n, k in shapes])
+    chain = LinearChain(links, cfg, packed=True)
+    assert chain.sync_mode == 2
+    refs = [torch.empty_like(y) for y in ys]
+    for rep in range(2):
+        x.copy_(torch.randn(M, hidden, generator=g, device=device).bfloat16())
+        for y in ys:
+            y.fill_(float("nan"))
+        chain.run()
+        for ln, ref in zip(links, refs):
+            hip_linear(ln.x, ln.w, dict(cfg, split_k=ln.split_k), ref)
+        torch.cuda.synchronize()
+        bad = [i for i, (y, r) in enumerate(zip(ys, refs)) if not torch.equal(y, r)]
+        assert not bad, f"launch {rep}: links {bad[:8]} differ from per-linear launches"
+    for i in (0, 1, 2, 3, 124, 125, 126, 127):
+        _oracle_columns(links[i].x, ws[i], ys[i], torch.arange(ws[i].shape[0]))
     chain.check()
 
 

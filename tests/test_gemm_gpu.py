@@ -295,6 +295,15 @@ def test_every_table_entry(device, hidden):
         check_cols(hip_linear(x, w, cfg), x, w, cols)
 
 
+@pytest.mark.parametrize("gemm", workloads.gpt_block(2560, 10240), ids=lambda g: g.name)
+def test_config4_linears_all_columns(device, gemm):
+    """Config 4's block linears (hidden 2560) at M = 56 with their table tiles, every column
+    against the oracle (test_every_table_entry samples columns of every key)."""
+    M = 56
+    x, w = _inputs(M, gemm.N, gemm.K, 15)
+    check(_run(x, w, gemm_tables.read_table(2560)[(M, gemm.N, gemm.K)], device), x, w)
+
+
 def test_graph_capture_and_replay(device):
     shapes = [(56, 2048, 8192), (56, 6144, 2048), (56, 2048, 2048)]
     table = gemm_tables.read_table(2048)
