@@ -87,9 +87,13 @@ typedef struct plm_tile {
 /*
  * Packed weights. plm_pack_weight rearranges a row-major W[N,K] (ldw elements per row) into the
  * operand order of gfx950's 16x16x32 MFMA: fragment (f, s) = rows [16f, 16f+16) x K [32s, 32s+32)
- * as 64 lanes x 16 bytes, lane l holding row 16f + l%16, elements 32s + 8*(l/16) .. +8, laid out
- * [ceil(N/16)][ceil(K/32)] and zero-padded. Each weight load of plm_gemm_packed is then one
- * contiguous KiB. Packing is a one-time pass per weight (the reference reads its weights as they
+ * as 64 lanes x 16 bytes, lane l holding row 16f + l%16, elements 32s + 8*(l/16) .. +8. With the
+ * fragment rows zero-padded to R (a multiple of 16) and the K steps to a multiple of 8, fragment
+ * (f, s) lies at KiB (s/8)*8R + 8f + s%8: eight K steps of a row together, then the next eight of
+ * every row. Each weight load of plm_gemm_packed is then one contiguous KiB, and workgroups that
+ * stream their rows at the same K step read one contiguous stretch between them. The format is
+ * this library's own, read only by its kernels and plm_unpack_weight. Packing is a one-time pass
+ * per weight (the reference reads its weights as they
  * are, plm/fast_gemm.py:17-48; a caller keeps the packed copy next to the weight).
  * plm_packed_weight_bytes gives the size; `packed` must be 16-byte aligned.
  */

@@ -11,14 +11,25 @@
 
 namespace plm {
 
-// Weight packing: thread i writes lane (i % 64) of fragment i / 64 (16 bytes, zeros past N or K).
+// The fragment (row f, K step s) stored at fragment index `frag` of a packed weight with `rows`
+// fragment rows (the order tile.h describes: groups of kPackGroup steps, all rows per group).
+__device__ __forceinline__ void packed_frag_at(int64_t frag, int rows, int& f, int& s) {
+  const int64_t per_group = static_cast<int64_t>(rows) * kPackGroup;
+  const int g = static_cast<int>(frag / per_group);
+  const int rem = static_cast<int>(frag - g * per_group);
+  f = rem / kPackGroup;
+  s = g * kPackGroup + rem % kPackGroup;
+}
+
+// Weight packing: thread i writes lane (i % 64) of the fragment stored at i / 64 (16 bytes, zeros
+// past N or K, so the padding rows and steps are zero fragments).
 __global__ __launch_bounds__(256) void pack_weight_kernel(const uint16_t* __restrict__ w, int64_t ldw, int N, int K,
-                                                         int Ks, int64_t lanes, u32x4* __restrict__ out) {
+                                                         int rows, int64_t lanes, u32x4* __restrict__ out) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < lanes;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const int lane = static_cast<int>(i & 63);
-    const int64_t frag = i >> 6;
-    const int f = static_cast<int>(frag / Ks), s = static_cast<int>(frag - static_cast<int64_t>(f) * Ks);
+    int f, s;
+    packed_frag_at(i >> 6, rows, f, s);
     const int n = 16 * f + (lane & 15), k = 32 * s + 8 * (lane >> 4);
     u32x4 v = u32x4{0u, 0u, 0u, 0u};
     if (n < N && k < K) v = *reinterpret_cast<const u32x4*>(w + static_cast<int64_t>(n) * ldw + k);
@@ -26,15 +37,15 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(const uint16_t* __rest
   }
 }
 
-// The inverse of pack_weight_kernel: thread i writes lane (i % 64) of fragment i / 64 back to its 16
-// bytes of the row-major W (fragments' padding past N or K is dropped).
-__global__ __launch_bounds__(256) void unpack_weight_kernel(const u32x4* __restrict__ packed, int N, int K, int Ks,
+// The inverse of pack_weight_kernel: thread i writes lane (i % 64) of the fragment stored at i / 64
+// back to its 16 bytes of the row-major W (padding past N or K is dropped).
+__global__ __launch_bounds__(256) void unpack_weight_kernel(const u32x4* __restrict__ packed, int N, int K, int rows,
                                                            int64_t lanes, uint16_t* __restrict__ w, int64_t ldw) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < lanes;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const int lane = static_cast<int>(i & 63);
-    const int64_t frag = i >> 6;
-    const int f = static_cast<int>(frag / Ks), s = static_cast<int>(frag - static_cast<int64_t>(f) * Ks);
+    int f, s;
+    packed_frag_at(i >> 6, rows, f, s);
     const int n = 16 * f + (lane & 15), k = 32 * s + 8 * (lane >> 4);
     if (n < N && k < K) *reinterpret_cast<u32x4*>(w + static_cast<int64_t>(n) * ldw + k) = packed[i];
   }
@@ -59,7 +70,7 @@ int packed_cus() {
 
 int64_t ksteps(int64_t K) { return (K + 31) / 32; }
 
-int64_t packed_bytes(int64_t N, int64_t K) { return (N + 15) / 16 * ksteps(K) * kFragBytes; }
+int64_t packed_bytes(int64_t N, int64_t K) { return pack_bytes(N, ksteps(K)); }
 
 // k_waves = 4, 8, 16: the workgroup's k_waves wavefronts split the tile's K range (tile =
 // 16*wave_frags rows); k_waves = 1: each of four wavefronts takes its own 16*wave_frags rows
@@ -336,7 +347,7 @@ int plm_pack_weight(int32_t dtype, const void* w, int64_t ldw, int64_t N, int64_
   const int64_t blocks = std::min<int64_t>((lanes + 255) / 256, 65536);
   hipLaunchKernelGGL(plm::pack_weight_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(w), ldw, static_cast<int>(N),
-                     static_cast<int>(K), static_cast<int>(plm::ksteps(K)), lanes, static_cast<plm::u32x4*>(packed));
+                     static_cast<int>(K), static_cast<int>(plm::pack_rows(N)), lanes, static_cast<plm::u32x4*>(packed));
   return hipGetLastError() == hipSuccess ? PLM_OK : PLM_ERR_LAUNCH;
 }
 
@@ -353,7 +364,7 @@ int plm_unpack_weight(int32_t dtype, const void* packed, size_t packed_bytes, in
   const int64_t blocks = std::min<int64_t>((lanes + 255) / 256, 65536);
   hipLaunchKernelGGL(plm::unpack_weight_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const plm::u32x4*>(packed), static_cast<int>(N),
-                     static_cast<int>(K), static_cast<int>(plm::ksteps(K)), lanes, static_cast<uint16_t*>(w), ldw);
+                     static_cast<int>(K), static_cast<int>(plm::pack_rows(N)), lanes, static_cast<uint16_t*>(w), ldw);
   return hipGetLastError() == hipSuccess ? PLM_OK : PLM_ERR_LAUNCH;
 }
 

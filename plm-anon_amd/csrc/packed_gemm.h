@@ -9,9 +9,10 @@
 // Loaded from a row-major W, every quad of lanes touches four rows, so one load instruction is
 // 64 separate cache-line requests and the vector memory pipeline, not HBM, sets the speed. The
 // weights are therefore rearranged once (plm_pack_weight) into fragments: fragment (f, s) is rows
-// [16f, 16f+16) x K [32s, 32s+32) stored as 64 lanes x 16 bytes in exactly that lane order, laid
-// out [ceil(N/16)][ceil(K/32)] with zero padding. Every weight load is then one contiguous,
-// aligned KiB that lands in the registers as the MFMA operand, with no LDS staging.
+// [16f, 16f+16) x K [32s, 32s+32) stored as 64 lanes x 16 bytes in exactly that lane order, in
+// groups of eight K steps per row (tile.h: pack_row_offset, pack_step_offset). Every weight load
+// is then one contiguous, aligned KiB that lands in the registers as the MFMA operand, with no LDS
+// staging.
 // X (small, L2-resident) is loaded row-major and coalesced, and turned into the operand layout
 // through a wavefront-private LDS tile.
 //
@@ -122,6 +123,7 @@ struct PLinear {
   void* y;
   int64_t ldx, ldy;
   int N, Ks, k_last, split, tiles, items;  // tiles of 16*NF (KW = 4) or 64*NF (KW = 1) rows
+  uint32_t wgroup;  // packed weight: bytes from one group of K steps to the next (pack_group_bytes)
   int out_f32, consumed;
   int* arrive;     // split arrival counters, one per tile
   int seq;         // consumed linears up to and including this one
@@ -184,6 +186,7 @@ __device__ __forceinline__ PLinear load_linear(const PackedArgs& a, int gi, int6
   L.Ks = (K + 31) >> 5;
   L.k_last = K - 32 * (L.Ks - 1);
   L.split = sgpr(g.split_k);
+  L.wgroup = pack_group_bytes(L.N);
   L.tiles = (((L.N + 15) >> 4) + tile_frags<NF, KW>() - 1) / tile_frags<NF, KW>();
   L.items = L.tiles * L.split;
   L.out_f32 = sgpr(g.out_f32);
@@ -270,7 +273,7 @@ struct PCursor {
   int st;     // current K step
   int end;    // end of the steps that load data
   int pend;   // end of the padded steps
-  int wbase;  // byte offset of the item's first weight fragment at step 0
+  uint32_t wbase;  // byte offset of the item's first weight fragment at step 0
 };
 
 template <int NF, int D, int KW>
@@ -283,7 +286,7 @@ __device__ __forceinline__ void pc_enter(const PLinear& L, int wave, PCursor& c)
   c.st = b;
   c.end = e;
   c.pend = b + max(D, (e - b + D - 1) / D * D);
-  c.wbase = (tile * tile_frags<NF, KW>() + (KW == 1 ? wave * NF : 0)) * L.Ks * kFragBytes;
+  c.wbase = pack_row_offset(tile * tile_frags<NF, KW>() + (KW == 1 ? wave * NF : 0));
 }
 
 template <int NF, int D, int KW>
@@ -315,7 +318,7 @@ template <int MT, int NF, int KW>
 __device__ __forceinline__ void packed_offsets(const PLinear& L, int M, int lane, int wave,
                                                POffsets<MT, NF, x_per_wave<MT, KW>()>& o) {
 #pragma unroll
-  for (int f = 0; f < NF; ++f) o.wo[f] = static_cast<uint32_t>(f * L.Ks * kFragBytes + lane * 16);
+  for (int f = 0; f < NF; ++f) o.wo[f] = pack_row_offset(f) + static_cast<uint32_t>(lane * 16);
 #pragma unroll
   for (int i = 0; i < x_per_wave<MT, KW>(); ++i) {
     const int t = KW == 1 ? wave + 4 * i : i;
@@ -331,11 +334,11 @@ __device__ __forceinline__ void packed_offsets(const PLinear& L, int M, int lane
 // loop over the lanes' distinct values (such loops also leave its load-count waits conservative:
 // a full drain of the pipeline once per D steps).
 template <int NF>
-__device__ __forceinline__ void issue_w(__amdgpu_buffer_rsrc_t wr, const PCursor& c, int items,
+__device__ __forceinline__ void issue_w(__amdgpu_buffer_rsrc_t wr, const PCursor& c, int items, uint32_t wgroup,
                                         const uint32_t (&wo)[NF], u32x4 (&wb)[NF]) {
   const bool live = c.item < items && c.st < c.end;
   const int ws = __builtin_amdgcn_readfirstlane(
-      static_cast<int>(live ? static_cast<uint32_t>(c.wbase + c.st * kFragBytes) : kNoLoad));
+      static_cast<int>(live ? c.wbase + pack_step_offset(c.st, wgroup) : kNoLoad));
 #pragma unroll
   for (int f = 0; f < NF; ++f)
     wb[f] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, wo[f], ws, 0));
@@ -849,7 +852,7 @@ __device__ __forceinline__ void warm_weights(const PLinear& Ln, int G, int wave,
                                              __amdgpu_buffer_rsrc_t wr, const uint32_t* wo, PkLdsVoid* dst) {
   for (int n = 0; n < kWarmFragments / NF && nx.item < Ln.items; ++n) {
     if (nx.st < nx.end) {
-      const int ws = __builtin_amdgcn_readfirstlane(static_cast<int>(nx.wbase + nx.st * kFragBytes));
+      const int ws = __builtin_amdgcn_readfirstlane(static_cast<int>(nx.wbase + pack_step_offset(nx.st, Ln.wgroup)));
 #pragma unroll
       for (int f = 0; f < NF; ++f) __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, dst, 16, wo[f], ws, 0, 0);
     }
@@ -978,7 +981,7 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
     const PLinear L = load_linear<NF, KW, EPI>(a, gi, epoch);
     POffsets<MT, NF, XN> o;
     packed_offsets<MT, NF, KW>(L, a.M, lane, wave, o);
-    const auto wr = make_rsrc(L.wp, static_cast<uint32_t>((L.N + 15) >> 4) * L.Ks * kFragBytes);
+    const auto wr = make_rsrc(L.wp, static_cast<uint32_t>(pack_bytes(L.N, L.Ks)));
     const auto xr = make_rsrc(L.x, static_cast<uint32_t>(a.M * L.ldx * 2));
     PCursor ld{first_item<EPI>(a, gi), 0, 0, 0, 0};
     pc_enter<NF, D, KW>(L, wave, ld);
@@ -990,7 +993,7 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
         PCursor lw = ld;
 #pragma unroll
         for (int j = 0; j < D; ++j) {
-          issue_w<NF>(wr, lw, L.items, o.wo, wb[j]);
+          issue_w<NF>(wr, lw, L.items, L.wgroup, o.wo, wb[j]);
           pc_advance<NF, D, KW>(L, a.G, wave, lw);
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -1005,7 +1008,7 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
       } else if (!w_ready) {
 #pragma unroll
         for (int j = 0; j < D; ++j) {
-          issue_w<NF>(wr, ld, L.items, o.wo, wb[j]);
+          issue_w<NF>(wr, ld, L.items, L.wgroup, o.wo, wb[j]);
           issue_x<MT, NF, XN>(xr, ld, L.items, L.Ks, o, xb[j]);
           pc_advance<NF, D, KW>(L, a.G, wave, ld);
           __builtin_amdgcn_sched_barrier(0);
@@ -1048,7 +1051,7 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
           for (int f = 0; f < NF; ++f)
 #pragma unroll
             for (int t = 0; t < MT; ++t) acc[f][t] = mfma_16x16x32<DT>(wb[j][f], xop[t], acc[f][t]);
-          issue_w<NF>(wr, ld, L.items, o.wo, wb[j]);
+          issue_w<NF>(wr, ld, L.items, L.wgroup, o.wo, wb[j]);
           issue_x<MT, NF, XN>(xr, ld, L.items, L.Ks, o, xb[j]);
           pc_advance<NF, D, KW>(L, a.G, wave, ld);
           __builtin_amdgcn_sched_barrier(0);
@@ -1085,10 +1088,10 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
       if (nx.item < Ln.items) {
         POffsets<MT, NF, XN> on;
         packed_offsets<MT, NF, KW>(Ln, a.M, lane, wave, on);
-        const auto wrn = make_rsrc(Ln.wp, static_cast<uint32_t>((Ln.N + 15) >> 4) * Ln.Ks * kFragBytes);
+        const auto wrn = make_rsrc(Ln.wp, static_cast<uint32_t>(pack_bytes(Ln.N, Ln.Ks)));
 #pragma unroll
         for (int j = 0; j < D; ++j) {
-          issue_w<NF>(wrn, nx, Ln.items, on.wo, wb[j]);
+          issue_w<NF>(wrn, nx, Ln.items, Ln.wgroup, on.wo, wb[j]);
           pc_advance<NF, D, KW>(Ln, a.G, wave, nx);
           __builtin_amdgcn_sched_barrier(0);
         }

@@ -85,6 +85,36 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0));
 }
 
+// Packed weights (plm_pack_weight). Fragment (f, s) is weight rows [16f, 16f+16) x K [32s, 32s+32),
+// 64 lanes x 16 bytes in the MFMA A-operand order. The fragment rows are padded with zero
+// fragments to R = a multiple of 16 (every tile's rows then lie inside the weight, whatever its
+// height), the K steps to a multiple of 8, and fragment (f, s) lies at
+//   (s / 8) * R * 8 KiB + f * 8 KiB + (s % 8) KiB:
+// each fragment row keeps 8 KiB of consecutive K steps together, and the next 8 steps of every
+// row follow after all rows. The workgroups of a launch stream their own rows at about the same K
+// step at once; in this order they read one contiguous stretch per group of steps, where with
+// whole rows stored one after the other (2K bytes apart) the same-step reads landed on few HBM
+// channels (measured, a plain stream of the 50257-row LM head: 6.2 against 5.4 TB/s; MLP up 4.7
+// against 4.3; the other 1.3B block shapes within a few % either way).
+constexpr int kPackGroup = 8;      // K steps of a fragment row stored together
+constexpr int kPackRowAlign = 16;  // fragment rows padded to a multiple of this
+constexpr uint32_t kPackFragBytes = 1024;
+__host__ __device__ constexpr int64_t packed_steps(int64_t Ks) { return (Ks + kPackGroup - 1) / kPackGroup * kPackGroup; }
+__host__ __device__ constexpr int64_t pack_rows(int64_t N) {
+  return ((N + 15) / 16 + kPackRowAlign - 1) / kPackRowAlign * kPackRowAlign;
+}
+// Bytes of the packed weight of W[N, K] with Ks = ceil(K / 32) K steps.
+__host__ __device__ constexpr int64_t pack_bytes(int64_t N, int64_t Ks) { return pack_rows(N) * packed_steps(Ks) * kPackFragBytes; }
+// Bytes from one group of K steps (of every row) to the next.
+__host__ __device__ constexpr uint32_t pack_group_bytes(int64_t N) {
+  return static_cast<uint32_t>(pack_rows(N)) * kPackGroup * kPackFragBytes;
+}
+// Offset of fragment row f at K step 0, and the offset K step s adds to it.
+__host__ __device__ constexpr uint32_t pack_row_offset(int f) { return static_cast<uint32_t>(f) * kPackGroup * kPackFragBytes; }
+__host__ __device__ constexpr uint32_t pack_step_offset(int s, uint32_t group_bytes) {
+  return (static_cast<uint32_t>(s) / kPackGroup) * group_bytes + (static_cast<uint32_t>(s) % kPackGroup) * kPackFragBytes;
+}
+
 // Workspace layout common to every entry point: the counter area (zero between calls), then scratch.
 // Ints of the counter area, so that every entry point can share one workspace:
 //   0, 1      streaming chain: launch epoch, workgroups exited

@@ -362,20 +362,20 @@ __device__ __forceinline__ void own_logit_wave(const VerifyArgs& a, int r, int l
   const int k_last = a.K - 32 * (Ks - 1);
   // The packed fragment row (16 vocabulary rows) holding pid, and row r's X fragment in the MFMA
   // operand order: lane l = X row 16*(r/16) + l%16, K elements 8*(l/16) .. +8 of each step.
-  const auto wr = make_rsrc(reinterpret_cast<const char*>(a.w) + static_cast<int64_t>(pid >> 4) * Ks * kFragBytes,
-                            static_cast<uint32_t>(Ks) * kFragBytes);
+  const uint32_t wgroup = pack_group_bytes(a.V);
+  const auto wr = make_rsrc(a.w, static_cast<uint32_t>(pack_bytes(a.V, Ks)));
   const auto xr = make_rsrc(a.x, static_cast<uint32_t>(a.R * a.ldx * 2));
   const int xrow = 16 * (r >> 4) + (lane & 15);
   const uint32_t xo = xrow < a.R ? static_cast<uint32_t>(xrow * a.ldx * 2 + (lane >> 4) * 16) : kOutOfRange;
   const uint32_t xo_last = 8 * (lane >> 4) < k_last ? xo : kOutOfRange;
-  const uint32_t wo = static_cast<uint32_t>(lane * 16);
+  const uint32_t wo = pack_row_offset(pid >> 4) + static_cast<uint32_t>(lane * 16);
   u32x4 wb[D], xb[D];
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int j = 0; j < D; ++j) {
     const bool live = j < Ks;
     wb[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                          wr, wo, static_cast<int>(live ? j * kFragBytes : kNoLoad), 0));
+                                          wr, wo, static_cast<int>(live ? pack_step_offset(j, wgroup) : kNoLoad), 0));
     xb[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                           xr, j == Ks - 1 ? xo_last : xo, static_cast<int>(live ? j * 64 : kNoLoad), 0));
   }
@@ -386,7 +386,7 @@ __device__ __forceinline__ void own_logit_wave(const VerifyArgs& a, int r, int l
       const int n = s0 + D + j;
       const bool live = n < Ks;
       wb[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                            wr, wo, static_cast<int>(live ? n * kFragBytes : kNoLoad), 0));
+                                            wr, wo, static_cast<int>(live ? pack_step_offset(n, wgroup) : kNoLoad), 0));
       xb[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                             xr, n == Ks - 1 ? xo_last : xo, static_cast<int>(live ? n * 64 : kNoLoad), 0));
     }
@@ -603,12 +603,13 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D
   L.N = a.V;
   L.Ks = (a.K + 31) >> 5;
   L.k_last = a.K - 32 * (L.Ks - 1);
+  L.wgroup = pack_group_bytes(a.V);
   L.split = 1;
   L.tiles = (((a.V + 15) >> 4) + tile_frags<NF, KW>() - 1) / tile_frags<NF, KW>();
   L.items = L.tiles;
   POffsets<MT, NF, XN> o;
   packed_offsets<MT, NF, KW>(L, a.R, lane, wave, o);
-  const auto wr = make_rsrc(L.wp, static_cast<uint32_t>((L.N + 15) >> 4) * L.Ks * kFragBytes);
+  const auto wr = make_rsrc(L.wp, static_cast<uint32_t>(pack_bytes(L.N, L.Ks)));
   const auto xr = make_rsrc(L.x, static_cast<uint32_t>(a.R * L.ldx * 2));
 
   // Row states of the rows this lane's accumulators hold: row 16t + lane%16.
@@ -631,7 +632,7 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D
   if (ld.item < L.items) {
 #pragma unroll
     for (int j = 0; j < D; ++j) {
-      issue_w<NF>(wr, ld, L.items, o.wo, wb[j]);
+      issue_w<NF>(wr, ld, L.items, L.wgroup, o.wo, wb[j]);
       issue_x<MT, NF, XN>(xr, ld, L.items, L.Ks, o, xb[j]);
       pc_advance<NF, D, KW>(L, a.G, wave, ld);
       __builtin_amdgcn_sched_barrier(0);
@@ -656,7 +657,7 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D
         for (int f = 0; f < NF; ++f)
 #pragma unroll
           for (int t = 0; t < MT; ++t) acc[f][t] = mfma_16x16x32<DT>(wb[j][f], xop[t], acc[f][t]);
-        issue_w<NF>(wr, ld, L.items, o.wo, wb[j]);
+        issue_w<NF>(wr, ld, L.items, L.wgroup, o.wo, wb[j]);
         issue_x<MT, NF, XN>(xr, ld, L.items, L.Ks, o, xb[j]);
         pc_advance<NF, D, KW>(L, a.G, wave, ld);
         __builtin_amdgcn_sched_barrier(0);
@@ -925,9 +926,9 @@ int packed_verify_entry(int32_t dtype, const void* x, int64_t ldx, const void* p
   if (R < 1 || R > 64 || V < 1 || V > (int64_t(1) << 30) || K < 8 || K % 8 != 0 || K > (int64_t(1) << 24))
     return PLM_ERR_ARGUMENT;
   if (ldx < K || R * ldx * 2 >= (int64_t(1) << 31)) return PLM_ERR_ARGUMENT;
-  // 32-bit buffer offsets over the packed weight (with the last tile's padding rows).
+  // 32-bit buffer offsets over the packed weight (its padding rows and steps included).
   const int64_t ks = (K + 31) / 32;
-  if (((V + 15) / 16 + 4 * tile->wave_frags) * ks * plm::kFragBytes >= (int64_t(1) << 31)) return PLM_ERR_ARGUMENT;
+  if (plm::pack_bytes(V, ks) >= (int64_t(1) << 31)) return PLM_ERR_ARGUMENT;
   if (ldx % 8 != 0 || !plm::aligned16_ptr(x) || !plm::aligned16_ptr(packed_w)) return PLM_ERR_ALIGNMENT;
   size_t own_off, state_off, idx_off, gstate_off, gidx_off, total;
   plm::verify_layout(R, own_off, state_off, idx_off, gstate_off, gidx_off, total);

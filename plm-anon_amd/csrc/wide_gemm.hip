@@ -83,14 +83,15 @@ __global__ __launch_bounds__(kWideThreads, 2) void wide_gemm_kernel(WideArgs a) 
   const int s_hi = static_cast<int>(static_cast<int64_t>(sp + 1) * a.Ks / a.split);
   const int steps = (s_hi - s_lo + kWideStages - 1) / kWideStages * kWideStages;  // padded: zero steps
 
-  const auto wr = make_rsrc(a.w, static_cast<uint32_t>(((a.N + 15) >> 4) * a.Ks) * 1024u);
+  const auto wr = make_rsrc(a.w, static_cast<uint32_t>(pack_bytes(a.N, a.Ks)));
+  const uint32_t wgroup = pack_group_bytes(a.N);
   const auto xr = make_rsrc(a.x, static_cast<uint32_t>(static_cast<int64_t>(a.M) * a.ldx * 2));
   // This wavefront stages weight fragments 2w, 2w+1 and X fragments 2w, 2w+1 of every K step.
   uint32_t wo[2], xo[2], xl[2];
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     const int f = nt * kWideFrags + 2 * wave + q;
-    wo[q] = static_cast<uint32_t>(f * a.Ks) * 1024u + static_cast<uint32_t>(lane) * 16u;
+    wo[q] = pack_row_offset(f) + static_cast<uint32_t>(lane) * 16u;
     // Coalesced: a quad of lanes reads one row's 64 bytes (row lane/4, bytes 16*(lane%4)); the
     // LDS write puts each 16 bytes where the operand layout wants them (x_slot).
     const int row = mt * kWideRows + 16 * (2 * wave + q) + (lane >> 2);
@@ -104,7 +105,7 @@ __global__ __launch_bounds__(kWideThreads, 2) void wide_gemm_kernel(WideArgs a) 
   auto load = [&](int t, u32x4 (&w)[2], u32x4 (&x)[2]) {
     const int s = s_lo + t;
     const bool live = s < s_hi;
-    const uint32_t sw = live ? static_cast<uint32_t>(s) * 1024u : kWideNoLoad;
+    const uint32_t sw = live ? pack_step_offset(s, wgroup) : kWideNoLoad;
     const uint32_t sx = live ? static_cast<uint32_t>(s) * 64u : kWideNoLoad;
     const bool last = s == a.Ks - 1;
 #pragma unroll

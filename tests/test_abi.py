@@ -194,8 +194,10 @@ def test_silu_mul_argument_validation_happens_before_launch():
 def test_packed_sizes_and_chain_prepare():
     lib = _lib.lib()
     # Fragments of 16 rows x 32 K: N and K round up.
-    assert lib.plm_packed_weight_bytes(50257, 2048) == 3142 * 64 * 1024
-    assert lib.plm_packed_weight_bytes(1000, 1416) == 63 * 45 * 1024
+    # Fragment rows padded to a multiple of 16, K steps to a multiple of 8 (50257 rows: 3142
+    # fragment rows -> 3152; K 1416: 45 steps -> 48).
+    assert lib.plm_packed_weight_bytes(50257, 2048) == 3152 * 64 * 1024
+    assert lib.plm_packed_weight_bytes(1000, 1416) == 64 * 48 * 1024
     assert lib.plm_gemm_packed_workspace_bytes(56, 2048, 8192, _lib.Tile(2, 4, 1, 2)) == 0
     # One fp32 fragment (1 KiB) per (tile, split, fragment of the tile).
     tiles_ = math.ceil(2048 / 16 / 2)
