@@ -69,6 +69,30 @@ def test_released_weight_every_width(device, M):
     assert torch.equal(y, want)
 
 
+@pytest.mark.parametrize("N,K", [(24, 8), (1000, 1416), (300, 4096)])
+def test_packed_layout_is_the_documented_one(device, N, K):
+    """plm_pack_weight's bytes, element for element, against the format include/plm_amd.h states:
+    fragment (f, s) = rows [16f, 16f+16) x K [32s, 32s+32), lane l = row 16f + l%16 and elements
+    32s + 8(l/16) .. +8; rows padded to R (a multiple of 16 fragment rows), K steps to a multiple
+    of 8, fragment (f, s) at KiB (s/8)*8R + 8f + s%8; everything past N or K zero."""
+    import numpy as np
+
+    w = _fresh(N, K, 77, device)
+    p = fast_gemm.pack_weight(w).cpu().numpy()
+    R = -(-(-(-N // 16)) // 16) * 16
+    Ks = -(-K // 32)
+    Ksp = -(-Ks // 8) * 8
+    assert p.size == R * Ksp * 1024
+    full = np.zeros((R * 16, Ksp * 32), dtype=np.uint16)
+    full[:N, :K] = w.view(torch.int16).cpu().numpy().view(np.uint16)
+    # [f, r16, s, kq, e] -> [f, s, lane = 16 kq + r16, e]
+    frags = full.reshape(R, 16, Ksp, 4, 8).transpose(0, 2, 3, 1, 4).reshape(R, Ksp, 64, 8)
+    # stored order: [s / 8][f][s % 8]
+    want = frags.reshape(R, Ksp // 8, 8, 64, 8).transpose(1, 0, 2, 3, 4)
+    got = p.view(np.uint16).reshape(Ksp // 8, R, 8, 64, 8)
+    assert np.array_equal(got, want)
+
+
 @pytest.mark.parametrize("N,K", [(6144, 2048), (50257, 2048), (1000, 1416), (24, 8)])
 def test_unpack_restores_the_weight_bit_for_bit(device, N, K):
     w = _fresh(N, K, N + K, device)
