@@ -84,6 +84,11 @@ __device__ __forceinline__ bool accept_proposal(const VerifyArgs& a, float own, 
   return in_nucleus || is_max;
 }
 
+// e^d for d = a logit less its row's maximum (d <= 0): the hardware exp2 of d log2(e), exactly 1 at
+// d = 0; its error is about an ulp where the terms matter (|d| small) and grows with |d| only
+// for terms far below the row's largest.
+__device__ __forceinline__ float exp_below_max(float d) { return __builtin_amdgcn_exp2f(d * 1.4426950408889634f); }
+
 #pragma clang fp contract(off)
 __device__ __forceinline__ RowState merge(RowState a, RowState b) {
   RowState r;
@@ -91,7 +96,7 @@ __device__ __forceinline__ RowState merge(RowState a, RowState b) {
   if (b.mx == -INFINITY) return RowState{a.mx, a.se, a.ab, r.ai};
   if (a.mx == -INFINITY) return RowState{b.mx, b.se, b.ab, r.ai};
   r.mx = fmaxf(a.mx, b.mx);
-  const float fa = expf(a.mx - r.mx), fb = expf(b.mx - r.mx);
+  const float fa = exp_below_max(a.mx - r.mx), fb = exp_below_max(b.mx - r.mx);
   r.se = a.se * fa + b.se * fb;
   r.ab = a.ab * fa + b.ab * fb;
   return r;
@@ -201,7 +206,7 @@ __global__ __launch_bounds__(64 * KW) void verify_main_kernel(VerifyArgs a) {
             t.ai = oai;
           }
         }
-        float e = valid ? expf(l - t.mx) : 0.f;
+        float e = valid ? exp_below_max(l - t.mx) : 0.f;
         float ab = (valid && l > own_l[j]) ? e : 0.f;
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) {
@@ -530,7 +535,7 @@ __device__ __forceinline__ void fold_columns(const f32x4 (&acc)[NF][MT], int n0,
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float l = lv[f][i];
-        const float ex = l == -INFINITY ? 0.f : expf(l - mx);
+        const float ex = l == -INFINITY ? 0.f : exp_below_max(l - mx);
         e += ex;
         ab += l > own_l[t] ? ex : 0.f;
       }
