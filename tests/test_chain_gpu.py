@@ -229,7 +229,8 @@ def _oracle_columns(x, w, y, cols):
     ref = oracle.linear(x.cpu(), w[cols].cpu()).float()
     diff = (got - ref).abs()
     in_tol = diff <= ATOL + RTOL * ref.abs()
-    step = 2.0 ** (torch.floor(torch.log2(ref.abs().clamp_min(2.0 ** -14))) - 7)
+    bits = 8 if y.dtype == torch.bfloat16 else 11
+    step = 2.0 ** (torch.floor(torch.log2(ref.abs().clamp_min(2.0 ** -14))) - (bits - 1))
     assert bool((in_tol | (diff <= step * 1.0001)).all()), f"max |got - oracle| {diff.max():.4g}"
     assert int((~in_tol).sum()) <= max(1, got.numel() // 1000)
 
@@ -362,6 +363,44 @@ def test_config4_round_chain_all_columns(device):
         bad = [i for i, (y, r) in enumerate(zip(ys, refs)) if not torch.equal(y, r)]
         assert not bad, f"launch {rep}: links {bad[:8]} differ from per-linear launches"
     for i in (0, 1, 2, 3, 124, 125, 126, 127):
+        _oracle_columns(links[i].x, ws[i], ys[i], torch.arange(ws[i].shape[0]))
+    chain.check()
+
+
+def test_fp16_round_chain(device):
+    """The 1.3B round in fp16, the reference's default round dtype (plm/rounds.py:50): all 96 block
+    linears (24 GPT-style blocks, hidden 2048) at M = 56 in one tile-flag launch with the round's
+    chain tile and splits, launched twice with a new input and NaN-filled outputs. Every link equals
+    its per-linear launch bit for bit, and the first and last blocks' four linears match the CPU
+    oracle on every column."""
+    from plm_amd import _lib, gemm_tables
+    from plm_amd.fast_gemm import _tile
+    from plm_amd.tiles import packed_chain_split
+
+    M, hidden = 56, 2048
+    cfg = gemm_tables.round_chain_tile(hidden, M)
+    G = _lib.lib().plm_gemm_packed_resident_workgroups(_lib.DTYPE_CODES[torch.float16], M, _tile(cfg))
+    assert G > 0
+    shapes = [(gm.N, gm.K) for gm in workloads.gpt_block(hidden, 4 * hidden)] * 24
+    gw = torch.Generator(device=device).manual_seed(95)
+    ws = [(torch.randn(n, k, generator=gw, device=device) / math.sqrt(k)).half() for n, k in shapes]
+    g = torch.Generator(device=device).manual_seed(96)
+    x = torch.randn(M, hidden, generator=g, device=device).half()
+    links, ys = _chain(x, ws, [packed_chain_split(n, k, cfg, G) for n, k in shapes])
+    chain = LinearChain(links, cfg, packed=True)
+    assert chain.sync_mode == 2
+    refs = [torch.empty_like(y) for y in ys]
+    for rep in range(2):
+        x.copy_(torch.randn(M, hidden, generator=g, device=device).half())
+        for y in ys:
+            y.fill_(float("nan"))
+        chain.run()
+        for ln, ref in zip(links, refs):
+            hip_linear(ln.x, ln.w, dict(cfg, split_k=ln.split_k), ref)
+        torch.cuda.synchronize()
+        bad = [i for i, (y, r) in enumerate(zip(ys, refs)) if not torch.equal(y, r)]
+        assert not bad, f"launch {rep}: links {bad[:8]} differ from per-linear launches"
+    for i in (0, 1, 2, 3, 92, 93, 94, 95):
         _oracle_columns(links[i].x, ws[i], ys[i], torch.arange(ws[i].shape[0]))
     chain.check()
 
