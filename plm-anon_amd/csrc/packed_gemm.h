@@ -357,6 +357,47 @@ __device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t xr, const PCursor
     xb[t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, last ? o.xo_last[t] : o.xo[t], xs, 0));
 }
 
+// The X loads of pipeline stage j, at the cursor's K step. Row split (KW = 1): the X of two steps
+// is loaded at the even stage, right behind that stage's weights and ahead of the odd stage's (the
+// next step lies in the same item: items start at stage 0 and pad to a multiple of the even D),
+// so that the even stage finds both steps' X arrived and stages them under one barrier.
+template <int MT, int NF, int XN, int KW, int D>
+__device__ __forceinline__ void issue_x_stage(int j, __amdgpu_buffer_rsrc_t xr, const PCursor& c, int items, int Ks,
+                                              const POffsets<MT, NF, XN>& o, u32x4 (&xb)[D][XN]) {
+  if constexpr (KW != 1) {
+    issue_x<MT, NF, XN>(xr, c, items, Ks, o, xb[j]);
+  } else if ((j & 1) == 0) {
+    issue_x<MT, NF, XN>(xr, c, items, Ks, o, xb[j]);
+    PCursor n = c;
+    ++n.st;
+    issue_x<MT, NF, XN>(xr, n, items, Ks, o, xb[j + 1]);
+  }
+}
+
+// Row split (KW = 1): the workgroup's shared X tiles of stage j into the MFMA operand layout. The
+// even stage of a pair stores both steps' tile sets and meets the barrier; the odd stage reads its
+// set without one. Four tile sets: consecutive pairs use alternate halves (`half` flips per pair),
+// so a pair's stores never meet a slower wavefront still reading the pair before: it read those
+// before it reached the barrier in between.
+template <int MT, int XN, int D>
+__device__ __forceinline__ void stage_x_rows(int j, char* xt, int wave, int xt_write, int xt_read,
+                                             const u32x4 (&xb)[D][XN], u32x4 (&xop)[MT], int& half) {
+  const int h = D % 4 == 0 ? (j >> 1) & 1 : half;  // D % 4 == 0: a D-stage block holds whole pairs of pairs
+  char* xs = xt + (2 * h + (j & 1)) * MT * kXTileBytes;
+  if ((j & 1) == 0) {
+#pragma unroll
+    for (int i = 0; i < XN; ++i)
+      if (wave + 4 * i < MT) {
+        *reinterpret_cast<u32x4*>(xs + (wave + 4 * i) * kXTileBytes + xt_write) = xb[j][i];
+        *reinterpret_cast<u32x4*>(xs + (MT + wave + 4 * i) * kXTileBytes + xt_write) = xb[j + 1][i];
+      }
+    lds_sync();
+  }
+#pragma unroll
+  for (int t = 0; t < MT; ++t) xop[t] = *reinterpret_cast<const u32x4*>(xs + t * kXTileBytes + xt_read);
+  if (D % 4 != 0 && (j & 1) == 1) half ^= 1;
+}
+
 // Four columns n..n+3 of Y row m (fewer at N's end); written through to the device-coherent level
 // when a later linear of the chain reads this Y.
 template <int DT>
@@ -945,14 +986,14 @@ constexpr int packed_waves_per_simd() {
   return packed_two_per_cu<MT, NF, D, KW>() ? 2 : 1;
 }
 
-// LDS bytes before the warm-up sink: KW = 1: two shared X tile sets (double-buffered by K step);
+// LDS bytes before the warm-up sink: KW = 1: four shared X tile sets (two K steps, double-buffered);
 // KW = 4: the four wavefronts' fp32 tiles (reduction), then a private X transpose tile set per
 // wavefront; KW > 4: the reduction tiles overlaying the private X tile sets.
 template <int MT, int NF, int KW>
 constexpr size_t packed_lds_body() {
   constexpr size_t red = static_cast<size_t>(KW) * NF * MT * kFragBytes;
   constexpr size_t xts = static_cast<size_t>(KW) * MT * kXTileBytes;
-  if constexpr (KW == 1) return static_cast<size_t>(2) * MT * kXTileBytes;
+  if constexpr (KW == 1) return static_cast<size_t>(4) * MT * kXTileBytes;
   if constexpr (KW == 4) return red + xts;
   return red > xts ? red : xts;
 }
@@ -974,6 +1015,7 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
   const int64_t epoch = a.sync ? sgpr64(collect(reinterpret_cast<const int64_t*>(a.counters + kPkEpochSlot))) : 0;
 
   u32x4 wb[D][NF], xb[D][XN];
+  [[maybe_unused]] int xhalf = 0;  // KW = 1: the half of the X tile sets the next pair of K steps uses
   // The first weight stages of linear `gi` may already be in flight (requested before the last
   // grid barrier): then only X is still to be loaded for them.
   bool w_ready = false;
@@ -1001,7 +1043,7 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
         wait_producer_tiles<NF, KW>(a, L, load_linear<NF, KW>(a, gi - 1, epoch), wave, lane);
 #pragma unroll
         for (int j = 0; j < D; ++j) {
-          issue_x<MT, NF, XN>(xr, ld, L.items, L.Ks, o, xb[j]);
+          issue_x_stage<MT, NF, XN, KW, D>(j, xr, ld, L.items, L.Ks, o, xb);
           pc_advance<NF, D, KW>(L, a.G, wave, ld);
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -1009,14 +1051,14 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
 #pragma unroll
         for (int j = 0; j < D; ++j) {
           issue_w<NF>(wr, ld, L.items, L.wgroup, o.wo, wb[j]);
-          issue_x<MT, NF, XN>(xr, ld, L.items, L.Ks, o, xb[j]);
+          issue_x_stage<MT, NF, XN, KW, D>(j, xr, ld, L.items, L.Ks, o, xb);
           pc_advance<NF, D, KW>(L, a.G, wave, ld);
           __builtin_amdgcn_sched_barrier(0);
         }
       } else {
 #pragma unroll
         for (int j = 0; j < D; ++j) {
-          issue_x<MT, NF, XN>(xr, ld, L.items, L.Ks, o, xb[j]);
+          issue_x_stage<MT, NF, XN, KW, D>(j, xr, ld, L.items, L.Ks, o, xb);
           pc_advance<NF, D, KW>(L, a.G, wave, ld);
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -1038,21 +1080,14 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
 #pragma unroll
             for (int t = 0; t < MT; ++t) xop[t] = *reinterpret_cast<const u32x4*>(xt + t * kXTileBytes + xt_read);
           } else {
-            // Stage j's X tile set (j alternates parity: D is even and items pad to a multiple).
-            char* xs = xt + (j & 1) * MT * kXTileBytes;
-#pragma unroll
-            for (int i = 0; i < XN; ++i)
-              if (wave + 4 * i < MT) *reinterpret_cast<u32x4*>(xs + (wave + 4 * i) * kXTileBytes + xt_write) = xb[j][i];
-            lds_sync();
-#pragma unroll
-            for (int t = 0; t < MT; ++t) xop[t] = *reinterpret_cast<const u32x4*>(xs + t * kXTileBytes + xt_read);
+            stage_x_rows<MT, XN, D>(j, xt, wave, xt_write, xt_read, xb, xop, xhalf);
           }
 #pragma unroll
           for (int f = 0; f < NF; ++f)
 #pragma unroll
             for (int t = 0; t < MT; ++t) acc[f][t] = mfma_16x16x32<DT>(wb[j][f], xop[t], acc[f][t]);
           issue_w<NF>(wr, ld, L.items, L.wgroup, o.wo, wb[j]);
-          issue_x<MT, NF, XN>(xr, ld, L.items, L.Ks, o, xb[j]);
+          issue_x_stage<MT, NF, XN, KW, D>(j, xr, ld, L.items, L.Ks, o, xb);
           pc_advance<NF, D, KW>(L, a.G, wave, ld);
           __builtin_amdgcn_sched_barrier(0);
         };

@@ -631,6 +631,7 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D
   }
 
   u32x4 wb[D][NF], xb[D][XN];
+  int xhalf = 0;  // the half of the X tile sets the next pair of K steps uses
   PCursor ld{b, 0, 0, 0, 0};
   pc_enter<NF, D, KW>(L, wave, ld);
   PCursor cp = ld;
@@ -638,7 +639,7 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D
 #pragma unroll
     for (int j = 0; j < D; ++j) {
       issue_w<NF>(wr, ld, L.items, L.wgroup, o.wo, wb[j]);
-      issue_x<MT, NF, XN>(xr, ld, L.items, L.Ks, o, xb[j]);
+      issue_x_stage<MT, NF, XN, KW, D>(j, xr, ld, L.items, L.Ks, o, xb);
       pc_advance<NF, D, KW>(L, a.G, wave, ld);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -651,19 +652,13 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D
       const int steps = cp.pend - cp.st;  // a multiple of D, at least D
       auto stage = [&](int j) __attribute__((always_inline)) {
         u32x4 xop[MT];
-        char* xs = xt + (j & 1) * MT * kXTileBytes;
-#pragma unroll
-        for (int q = 0; q < XN; ++q)
-          if (wave + 4 * q < MT) *reinterpret_cast<u32x4*>(xs + (wave + 4 * q) * kXTileBytes + xt_write) = xb[j][q];
-        lds_sync();
-#pragma unroll
-        for (int t = 0; t < MT; ++t) xop[t] = *reinterpret_cast<const u32x4*>(xs + t * kXTileBytes + xt_read);
+        stage_x_rows<MT, XN, D>(j, xt, wave, xt_write, xt_read, xb, xop, xhalf);
 #pragma unroll
         for (int f = 0; f < NF; ++f)
 #pragma unroll
           for (int t = 0; t < MT; ++t) acc[f][t] = mfma_16x16x32<DT>(wb[j][f], xop[t], acc[f][t]);
         issue_w<NF>(wr, ld, L.items, L.wgroup, o.wo, wb[j]);
-        issue_x<MT, NF, XN>(xr, ld, L.items, L.Ks, o, xb[j]);
+        issue_x_stage<MT, NF, XN, KW, D>(j, xr, ld, L.items, L.Ks, o, xb);
         pc_advance<NF, D, KW>(L, a.G, wave, ld);
         __builtin_amdgcn_sched_barrier(0);
       };
