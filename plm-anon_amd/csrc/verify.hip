@@ -499,7 +499,11 @@ __device__ __forceinline__ float round_logit(float v) {
   return v;
 }
 
-template <int MT, int NF, int MODE>
+// Branch-free: a lane visits its columns in increasing order, so a strict comparison keeps the
+// lowest index among its equal maxima (NaN never wins). With CHECK (a wavefront whose columns run
+// past V: the last tile) columns past V read as -inf, which neither wins nor adds: e^(-inf - mx) = 0
+// once the row maximum is finite, and a row whose maximum is -inf is not merged.
+template <int MT, int NF, int MODE, bool CHECK>
 __device__ __forceinline__ void fold_columns(const f32x4 (&acc)[NF][MT], int n0, int V, const float (&own_l)[MT],
                                              RowState (&rs)[MT]) {
 #pragma unroll
@@ -512,22 +516,20 @@ __device__ __forceinline__ void fold_columns(const f32x4 (&acc)[NF][MT], int n0,
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int n = n0 + 16 * f + i;
-        const bool valid = n < V;
-        const float l = valid ? round_logit<MODE>(acc[f][t][i]) : -INFINITY;
+        float l = round_logit<MODE>(acc[f][t][i]);
+        if constexpr (CHECK) l = n < V ? l : -INFINITY;
         lv[f][i] = l;
-        if (valid && (l > mx || (l == mx && n < ai))) {
-          mx = l;
-          ai = n;
-        }
+        const bool up = l > mx;
+        mx = up ? l : mx;
+        ai = up ? n : ai;
       }
 #pragma unroll
     for (int off = 16; off <= 32; off <<= 1) {
       const float omx = __shfl_xor(mx, off, 64);
       const int oai = __shfl_xor(ai, off, 64);
-      if (omx > mx || (omx == mx && oai < ai)) {
-        mx = omx;
-        ai = oai;
-      }
+      const bool take = omx > mx || (omx == mx && oai < ai);
+      mx = take ? omx : mx;
+      ai = take ? oai : ai;
     }
     float e = 0.f, ab = 0.f;
 #pragma unroll
@@ -535,7 +537,7 @@ __device__ __forceinline__ void fold_columns(const f32x4 (&acc)[NF][MT], int n0,
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float l = lv[f][i];
-        const float ex = l == -INFINITY ? 0.f : exp_below_max(l - mx);
+        const float ex = exp_below_max(l - mx);
         e += ex;
         ab += l > own_l[t] ? ex : 0.f;
       }
@@ -683,12 +685,17 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D
         own_ready = true;
       }
       if (a.logit_rows > 0) store_logits<DT, MT, NF>(acc, n0, a);
-      if (a.round_mode == PLM_ROUND_BF16)
-        fold_columns<MT, NF, PLM_ROUND_BF16>(acc, n0, a.V, own_l, rs);
-      else if (a.round_mode == PLM_ROUND_F16)
-        fold_columns<MT, NF, PLM_ROUND_F16>(acc, n0, a.V, own_l, rs);
-      else
-        fold_columns<MT, NF, PLM_ROUND_F32>(acc, n0, a.V, own_l, rs);
+      const bool full = (cp.item * kPackedWaves + wave + 1) * NF * 16 <= a.V;  // no column past V
+      if (a.round_mode == PLM_ROUND_BF16) {
+        if (full) fold_columns<MT, NF, PLM_ROUND_BF16, false>(acc, n0, a.V, own_l, rs);
+        else fold_columns<MT, NF, PLM_ROUND_BF16, true>(acc, n0, a.V, own_l, rs);
+      } else if (a.round_mode == PLM_ROUND_F16) {
+        if (full) fold_columns<MT, NF, PLM_ROUND_F16, false>(acc, n0, a.V, own_l, rs);
+        else fold_columns<MT, NF, PLM_ROUND_F16, true>(acc, n0, a.V, own_l, rs);
+      } else {
+        if (full) fold_columns<MT, NF, PLM_ROUND_F32, false>(acc, n0, a.V, own_l, rs);
+        else fold_columns<MT, NF, PLM_ROUND_F32, true>(acc, n0, a.V, own_l, rs);
+      }
       cp.item += a.G;
       if (cp.item >= L.items) break;
       pc_enter<NF, D, KW>(L, wave, cp);
