@@ -52,6 +52,11 @@ struct VerifyArgs {
   int* group_counter;  // packed verify: [G / kVerifyGroupSize], zero between launches
   float* gstate;       // packed verify: [groups][R][3], the merged state of each group
   int* gstate_idx;     // packed verify: [groups][R]
+  // Packed verify: the row states as 16-byte records {max, sum, sum above own, argmax bits}, one
+  // coherent store each and one coherent load each per merge: rec[G][R] over the state and
+  // state_idx areas, grec[groups][R] over gstate and gstate_idx.
+  f32x4* rec;
+  f32x4* grec;
   RoundEpilogue round;  // packed verify: k > 0 runs the round's epilogue after the last merge
   uint16_t* logits;     // packed verify: rows [0, logit_rows) of the logits in the model dtype, or null
   int64_t ld_logits;
@@ -435,13 +440,11 @@ __device__ __forceinline__ void wait_own_logits(const VerifyArgs& a) {
 // The final merges run once per launch, on its critical path, so their code is kept short (rolled
 // loops: code executed once is fetched cold) and their loads are issued in one batch.
 //
-// gather_states: the workgroup's threads load member (first + i), i < count <= 32, of every row
+// gather_records: the workgroup's threads load member (first + i), i < count <= 32, of every row
 // (device-coherent: other workgroups wrote them) into grid[i][m] in LDS; absent entries are left
 // unread.
-__device__ __forceinline__ void gather_states(const float* st, const int* st_idx, int first, int count, int R,
-                                              f32x4* grid) {
-  const auto fr = make_rsrc(st, static_cast<uint32_t>(first + kVerifyGroupSize) * R * 3 * sizeof(float));
-  const auto ir = make_rsrc(st_idx, static_cast<uint32_t>(first + kVerifyGroupSize) * R * sizeof(int));
+__device__ __forceinline__ void gather_records(const f32x4* rec, int first, int count, int R, f32x4* grid) {
+  const auto rr = make_rsrc(rec, static_cast<uint32_t>(first + kVerifyGroupSize) * R * sizeof(f32x4));
   constexpr int kPer = kVerifyGroupSize * 64 / (64 * kPackedWaves);  // entries per thread
   f32x4 v[kPer];
 #pragma unroll
@@ -450,14 +453,19 @@ __device__ __forceinline__ void gather_states(const float* st, const int* st_idx
     const int mem = i >> 6, m = i & 63;
     const bool ok = mem < count && m < R;
     const uint32_t slot = static_cast<uint32_t>((first + mem) * R + m);
-#pragma unroll
-    for (int c = 0; c < 3; ++c)
-      v[k][c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(fr, ok ? (slot * 3 + c) * 4 : kOutOfRange, 0, kCoherent));
-    v[k][3] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ir, ok ? slot * 4 : kOutOfRange, 0, kCoherent));
+    v[k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rr, ok ? slot * 16 : kOutOfRange, 0, kCoherent));
   }
 #pragma unroll
   for (int k = 0; k < kPer; ++k) grid[static_cast<int>(threadIdx.x) + 64 * kPackedWaves * k] = v[k];
   __syncthreads();
+}
+
+// Record `slot` of `slots` set to s, written device-coherent (read by gather_records in another
+// workgroup).
+__device__ __forceinline__ void publish_record(f32x4* rec, int slot, int slots, const RowState& s) {
+  const auto rr = make_rsrc(rec, static_cast<uint32_t>(slots) * sizeof(f32x4));
+  const f32x4 v{s.mx, s.se, s.ab, __builtin_bit_cast(float, s.ai)};
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rr, static_cast<uint32_t>(slot) * 16, 0, kCoherent);
 }
 
 // Every row's state merged over members 0..count-1 of grid: lane = row; wavefront w merges
@@ -720,11 +728,7 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D
     RowState s0 = RowState{st_mx[0][m], st_se[0][m], st_ab[0][m], st_ai[0][m]};
 #pragma unroll
     for (int w = 1; w < kPackedWaves; ++w) s0 = merge(s0, RowState{st_mx[w][m], st_se[w][m], st_ab[w][m], st_ai[w][m]});
-    const int64_t slot = static_cast<int64_t>(b) * a.R + m;
-    publish(a.state + slot * 3 + 0, s0.mx);
-    publish(a.state + slot * 3 + 1, s0.se);
-    publish(a.state + slot * 3 + 2, s0.ab);
-    publish(a.state_idx + slot, s0.ai);
+    publish_record(a.rec, b * a.R + m, a.G * a.R, s0);
   }
   // Two-level merge: the last workgroup of each group of kVerifyGroupSize merges the group's
   // states, the last group to finish merges the group states. Each level is one batch of
@@ -732,20 +736,14 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D
   const int group = b / kVerifyGroupSize;
   const int gsize = min(kVerifyGroupSize, a.G - group * kVerifyGroupSize);
   if (!arrive_last(a.group_counter + group, gsize)) return;
-  gather_states(a.state, a.state_idx, group * kVerifyGroupSize, gsize, a.R, grid);
+  gather_records(a.rec, group * kVerifyGroupSize, gsize, a.R, grid);
   {
     const RowState t = merge_rows(grid, gsize, wave, lane, st_mx, st_se, st_ab, st_ai);
-    if (wave == 0 && lane < a.R) {
-      const int64_t slot = static_cast<int64_t>(group) * a.R + lane;
-      publish(a.gstate + slot * 3 + 0, t.mx);
-      publish(a.gstate + slot * 3 + 1, t.se);
-      publish(a.gstate + slot * 3 + 2, t.ab);
-      publish(a.gstate_idx + slot, t.ai);
-    }
+    if (wave == 0 && lane < a.R) publish_record(a.grec, group * a.R + lane, (group + 1) * a.R, t);
   }
   const int groups = (a.G + kVerifyGroupSize - 1) / kVerifyGroupSize;
   if (!arrive_last(a.counter, groups)) return;
-  gather_states(a.gstate, a.gstate_idx, 0, groups, a.R, grid);
+  gather_records(a.grec, 0, groups, a.R, grid);
   const RowState t = merge_rows(grid, groups, wave, lane, st_mx, st_se, st_ab, st_ai);
   if (wave == 0) {
     if (lane == 0 && a.own_groups > 0) publish(a.own_done, 0);  // every workgroup has counted in and read it
@@ -817,7 +815,9 @@ size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 // Workspace layout: counter area (ints kVerifyCounter, kVerifyOwnDone, kPkErrorSlot and
 // [kVerifyGroupBase, +groups) used) |
 // own[R] | state[kMaxVerifyGroups][R][3] | state_idx[kMaxVerifyGroups][R] | gstate[groups][R][3] |
-// gstate_idx[groups][R], groups = kMaxVerifyGroups / kVerifyGroupSize.
+// gstate_idx[groups][R], groups = kMaxVerifyGroups / kVerifyGroupSize. The packed verify keeps its
+// 16-byte records over the same bytes: rec[kMaxVerifyGroups][R] from state, grec[groups][R] from
+// gstate (each pair of areas holds 12 + 4 bytes per entry).
 constexpr int kMaxVerifyGroupSets = kMaxVerifyGroups / kVerifyGroupSize;
 static_assert(kVerifyGroupBase + kMaxVerifyGroupSets <= 64, "group counters fit before the streaming counters");
 void verify_layout(int64_t R, size_t& own_off, size_t& state_off, size_t& idx_off, size_t& gstate_off,
@@ -968,6 +968,8 @@ int packed_verify_entry(int32_t dtype, const void* x, int64_t ldx, const void* p
   a.group_counter = reinterpret_cast<int*>(ws) + plm::kVerifyGroupBase;
   a.gstate = reinterpret_cast<float*>(ws + gstate_off);
   a.gstate_idx = reinterpret_cast<int*>(ws + gidx_off);
+  a.rec = reinterpret_cast<plm::f32x4*>(ws + state_off);
+  a.grec = reinterpret_cast<plm::f32x4*>(ws + gstate_off);
   a.own_done = reinterpret_cast<int*>(ws) + plm::kVerifyOwnDone;
   a.error = reinterpret_cast<int*>(ws) + plm::kPkErrorSlot;
 
