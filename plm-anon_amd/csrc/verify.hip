@@ -94,16 +94,20 @@ __device__ __forceinline__ bool accept_proposal(const VerifyArgs& a, float own, 
 // for terms far below the row's largest.
 __device__ __forceinline__ float exp_below_max(float d) { return __builtin_amdgcn_exp2f(d * 1.4426950408889634f); }
 
+// An empty state (maximum -inf) leaves the other unchanged; selects rather than branches, as the
+// lanes of a wavefront merge states of different rows.
 #pragma clang fp contract(off)
 __device__ __forceinline__ RowState merge(RowState a, RowState b) {
   RowState r;
   r.ai = (b.mx > a.mx || (b.mx == a.mx && b.ai < a.ai)) ? b.ai : a.ai;
-  if (b.mx == -INFINITY) return RowState{a.mx, a.se, a.ab, r.ai};
-  if (a.mx == -INFINITY) return RowState{b.mx, b.se, b.ab, r.ai};
-  r.mx = fmaxf(a.mx, b.mx);
-  const float fa = exp_below_max(a.mx - r.mx), fb = exp_below_max(b.mx - r.mx);
-  r.se = a.se * fa + b.se * fb;
-  r.ab = a.ab * fa + b.ab * fb;
+  const float mx = fmaxf(a.mx, b.mx);
+  const float fa = exp_below_max(a.mx - mx), fb = exp_below_max(b.mx - mx);
+  const float se = a.se * fa + b.se * fb;
+  const float ab = a.ab * fa + b.ab * fb;
+  const bool a_empty = a.mx == -INFINITY, b_empty = b.mx == -INFINITY;
+  r.mx = b_empty ? a.mx : (a_empty ? b.mx : mx);
+  r.se = b_empty ? a.se : (a_empty ? b.se : se);
+  r.ab = b_empty ? a.ab : (a_empty ? b.ab : ab);
   return r;
 }
 #pragma clang fp contract(on)
@@ -476,12 +480,15 @@ __device__ __forceinline__ RowState merge_rows(const f32x4* grid, int count, int
                                                int (*part_ai)[64]) {
   constexpr int kPerWave = kVerifyGroupSize / kPackedWaves;
   RowState s = empty_state();
-  const int end = min(count, (wave + 1) * kPerWave);
-#pragma unroll 1
-  for (int i = wave * kPerWave; i < end; ++i) {
-    const f32x4 g = grid[i * 64 + lane];
-    const float idx_bits = g[3];  // (a bit cast applied to the vector element itself read element 0)
-    s = merge(s, RowState{g[0], g[1], g[2], __builtin_bit_cast(int, idx_bits)});
+  const int n = count - wave * kPerWave;  // members of this wavefront (the rest of grid is unread)
+  f32x4 g[kPerWave];
+#pragma unroll
+  for (int j = 0; j < kPerWave; ++j) g[j] = grid[(wave * kPerWave + j) * 64 + lane];
+#pragma unroll
+  for (int j = 0; j < kPerWave; ++j) {
+    if (j >= n) break;
+    const float idx_bits = g[j][3];  // (a bit cast applied to the vector element itself read element 0)
+    s = merge(s, RowState{g[j][0], g[j][1], g[j][2], __builtin_bit_cast(int, idx_bits)});
   }
   part_mx[wave][lane] = s.mx;
   part_se[wave][lane] = s.se;
@@ -743,11 +750,13 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D
   }
   const int groups = (a.G + kVerifyGroupSize - 1) / kVerifyGroupSize;
   if (!arrive_last(a.counter, groups)) return;
+  // The proposals' own logits (complete before any workgroup's first fold) load with the records.
+  const float own_v = (wave == 0 && lane < a.R) ? collect(a.own + lane) : 0.f;
   gather_records(a.grec, 0, groups, a.R, grid);
   const RowState t = merge_rows(grid, groups, wave, lane, st_mx, st_se, st_ab, st_ai);
   if (wave == 0) {
     if (lane == 0 && a.own_groups > 0) publish(a.own_done, 0);  // every workgroup has counted in and read it
-    const bool acc = lane < a.R && accept_proposal(a, collect(a.own + lane), t);
+    const bool acc = lane < a.R && accept_proposal(a, own_v, t);
     if (lane < a.R) {
       if (a.accept != nullptr) a.accept[lane] = acc ? 1 : 0;
       if (a.argmax != nullptr) a.argmax[lane] = t.ai;
