@@ -357,14 +357,27 @@ __device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t xr, const PCursor
     xb[t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, last ? o.xo_last[t] : o.xo[t], xs, 0));
 }
 
-// The X loads of pipeline stage j, at the cursor's K step. Row split (KW = 1): the X of two steps
-// is loaded at the even stage, right behind that stage's weights and ahead of the odd stage's (the
-// next step lies in the same item: items start at stage 0 and pad to a multiple of the even D),
-// so that the even stage finds both steps' X arrived and stages them under one barrier.
+// Whether X is loaded and staged for two K steps at a time: always in the row split (KW = 1, one
+// barrier per pair), and with eight wavefronts at widths of four to seven X fragments (two private
+// X tile sets per wavefront fit the LDS up to seven). A pair's two loads read the two halves of the
+// same 128-byte lines of X. Measured on the 1.3B round: at M = 56 the chained round 1049 -> 1027 us
+// and the per-GEMM round 1291 -> 1237 us; at M <= 42 (fewer X fragments per weight fragment) the
+// chained round lost 1-11 %, so narrower widths stage one step at a time.
+template <int MT, int KW>
+constexpr bool packed_pair_x() {
+  if constexpr (KW == 1) return true;
+  if constexpr (KW == 8) return MT >= 4 && static_cast<size_t>(2) * KW * MT * kXTileBytes + kFragBytes <= 160 * 1024;
+  return false;
+}
+
+// The X loads of pipeline stage j, at the cursor's K step. Paired (packed_pair_x): the X of two
+// steps is loaded at the even stage, right behind that stage's weights and ahead of the odd
+// stage's (the next step lies in the same item: items start at stage 0 and pad to a multiple of
+// the even D), so that the even stage finds both steps' X arrived and stages them together.
 template <int MT, int NF, int XN, int KW, int D>
 __device__ __forceinline__ void issue_x_stage(int j, __amdgpu_buffer_rsrc_t xr, const PCursor& c, int items, int Ks,
                                               const POffsets<MT, NF, XN>& o, u32x4 (&xb)[D][XN]) {
-  if constexpr (KW != 1) {
+  if constexpr (!packed_pair_x<MT, KW>()) {
     issue_x<MT, NF, XN>(xr, c, items, Ks, o, xb[j]);
   } else if ((j & 1) == 0) {
     issue_x<MT, NF, XN>(xr, c, items, Ks, o, xb[j]);
@@ -988,11 +1001,12 @@ constexpr int packed_waves_per_simd() {
 
 // LDS bytes before the warm-up sink: KW = 1: four shared X tile sets (two K steps, double-buffered);
 // KW = 4: the four wavefronts' fp32 tiles (reduction), then a private X transpose tile set per
-// wavefront; KW > 4: the reduction tiles overlaying the private X tile sets.
+// wavefront; KW > 4: the reduction tiles overlaying the private X tile sets (two per wavefront
+// when paired).
 template <int MT, int NF, int KW>
 constexpr size_t packed_lds_body() {
   constexpr size_t red = static_cast<size_t>(KW) * NF * MT * kFragBytes;
-  constexpr size_t xts = static_cast<size_t>(KW) * MT * kXTileBytes;
+  constexpr size_t xts = static_cast<size_t>(KW) * MT * kXTileBytes * (KW != 1 && packed_pair_x<MT, KW>() ? 2 : 1);
   if constexpr (KW == 1) return static_cast<size_t>(4) * MT * kXTileBytes;
   if constexpr (KW == 4) return red + xts;
   return red > xts ? red : xts;
@@ -1005,10 +1019,11 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   f32x4* red = packed_lds;
+  constexpr int kXSets = KW != 1 && packed_pair_x<MT, KW>() ? 2 : 1;  // private X tile sets per wavefront
   char* xt = reinterpret_cast<char*>(packed_lds) +
              (KW == 1 ? 0
                       : (KW == 4 ? static_cast<size_t>(4) * NF * MT * kFragBytes : 0) +
-                            static_cast<size_t>(wave) * MT * kXTileBytes);
+                            static_cast<size_t>(wave) * kXSets * MT * kXTileBytes);
   PkLdsVoid* sink = (PkLdsVoid*)(reinterpret_cast<char*>(packed_lds) + packed_lds_body<MT, NF, KW>());
   const int xt_write = (lane >> 2) * 80 + (lane & 3) * 16;
   const int xt_read = (lane & 15) * 80 + (lane >> 4) * 16;
@@ -1074,7 +1089,19 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
         // loads for D steps ahead.
         auto stage = [&](int j) __attribute__((always_inline)) {
           u32x4 xop[MT];
-          if constexpr (KW != 1) {
+          if constexpr (KW != 1 && kXSets == 2) {
+            // The even stage stores both steps' X into the wavefront's two tile sets.
+            if ((j & 1) == 0) {
+#pragma unroll
+              for (int t = 0; t < MT; ++t) {
+                *reinterpret_cast<u32x4*>(xt + t * kXTileBytes + xt_write) = xb[j][t];
+                *reinterpret_cast<u32x4*>(xt + (MT + t) * kXTileBytes + xt_write) = xb[j + 1][t];
+              }
+            }
+            const char* xs = xt + (j & 1) * MT * kXTileBytes;
+#pragma unroll
+            for (int t = 0; t < MT; ++t) xop[t] = *reinterpret_cast<const u32x4*>(xs + t * kXTileBytes + xt_read);
+          } else if constexpr (KW != 1) {
 #pragma unroll
             for (int t = 0; t < MT; ++t) *reinterpret_cast<u32x4*>(xt + t * kXTileBytes + xt_write) = xb[j][t];
 #pragma unroll

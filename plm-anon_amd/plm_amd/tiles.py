@@ -33,11 +33,16 @@ def _regs(mt: int, nf: int, d: int, kw: int) -> int:
     return (d * (nf + xn) + nf * mt + (mt if kw == 1 else 0)) * 4
 
 
+def pair_x(mt: int, kw: int) -> bool:
+    """Whether X is staged two K steps at a time (mirrors ``packed_pair_x``)."""
+    return kw == 1 or (kw == 8 and mt >= 4 and 2 * kw * mt * X_TILE + FRAG <= LDS_LIMIT)
+
+
 def lds_body(mt: int, nf: int, kw: int) -> int:
     """LDS bytes before the warm-up sink (mirrors ``packed_lds_body``)."""
-    red, xts = kw * nf * mt * FRAG, kw * mt * X_TILE
+    red, xts = kw * nf * mt * FRAG, kw * mt * X_TILE * (2 if kw != 1 and pair_x(mt, kw) else 1)
     if kw == 1:
-        return 2 * mt * X_TILE
+        return 4 * mt * X_TILE
     return red + xts if kw == 4 else max(red, xts)
 
 
