@@ -263,7 +263,7 @@ def write_chain_table(hidden: int, table: dict[int, dict]) -> None:
     (TABLES / f"chain_tiles_hidden{hidden}.json").write_text(text + "\n")
 
 
-def tune_chains(hiddens: list[int] | None, log: dict) -> None:
+def tune_chains(hiddens: list[int] | None, log: dict, only_widths: list[int] | None = None) -> None:
     from .gemm_tables import read_chain_table
 
     rounds = chain_rounds()
@@ -271,6 +271,8 @@ def tune_chains(hiddens: list[int] | None, log: dict) -> None:
         block, widths = rounds[hidden]
         table = read_chain_table(hidden)
         for M in widths:
+            if only_widths and M not in only_widths:
+                continue
             best, _, results = tune_chain(hidden, block, M)
             table[M] = best
             log[f"chain,{hidden},{M}"] = [(us, cfg) for us, cfg in results]
@@ -284,13 +286,14 @@ def main(argv: list[str] | None = None) -> None:
     ap.add_argument("--keys", nargs="*", help="only these M,N,K keys")
     ap.add_argument("--log", help="write every candidate's timing to this JSON file")
     ap.add_argument("--chain", action="store_true", help="tune the chained rounds' tiles instead")
+    ap.add_argument("--widths", type=int, nargs="*", help="with --chain: only these round widths")
     args = ap.parse_args(argv)
     if args.heuristic:
         heuristic_tables()
         return
     log = {}
     if args.chain:
-        tune_chains(args.hidden, log)
+        tune_chains(args.hidden, log, args.widths)
         if args.log:
             with open(args.log, "w") as fh:
                 json.dump(log, fh)
