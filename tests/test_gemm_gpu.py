@@ -139,6 +139,10 @@ def test_round_widths_edge_cases(device, M):
                 {"wave_frags": 1, "k_waves": 1, "split_k": 1, "unroll": 2},
                 {"wave_frags": 2, "k_waves": 1, "split_k": 3, "unroll": 4},
                 {"wave_frags": 2, "k_waves": 8, "split_k": 1, "unroll": 2},
+                # eight wavefronts stage X two K steps at a time from MT = 4: odd step ranges per
+                # wavefront and split, the masked last step inside a pair
+                {"wave_frags": 2, "k_waves": 8, "split_k": 3, "unroll": 4},
+                {"wave_frags": 4, "k_waves": 8, "split_k": 2, "unroll": 6},
                 {"wave_frags": 1, "k_waves": 16, "split_k": 2, "unroll": 2}):
         if supported(cfg):
             check(_run(x, w, cfg, device), x, w)
