@@ -241,6 +241,19 @@ def run(out: Path) -> None:
             keys = list(rows[n][1])
             agg = {k: float(np.nanmedian([r[k] for r in rows[n][1:]])) for k in keys}
             print(f"  {n:8s} " + "  ".join(f"{k} {agg[k]:.2f}" for k in keys), flush=True)
+        # Item ends by XCD (workgroup b on XCD b mod 8 under the default round-robin dispatch):
+        # per linear, each workgroup's item end less the linear's median item end; medians per XCD.
+        late = [[] for _ in range(8)]
+        for gi in range(1, 96):
+            v = d[gi, :, 4]
+            have = np.nonzero(v > 0)[0]
+            if len(have) == 0:
+                continue
+            med = np.median(v[have])
+            for b in have:
+                late[b % 8].append((v[b] - med) * 0.01)
+        print("  item end vs the linear's median, by XCD (median, p90 us): " +
+              "  ".join(f"{x}: {np.median(l):+.2f}/{np.percentile(l, 90):+.2f}" for x, l in enumerate(late) if l), flush=True)
         print(f"  last tile to last tile per linear: {(ends[-1] - ends[0]) * 0.01 / 95:.2f} us", flush=True)
 
 
