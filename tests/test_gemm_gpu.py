@@ -148,6 +148,28 @@ def test_round_widths_edge_cases(device, M):
             check(_run(x, w, cfg, device), x, w)
 
 
+def test_seeded_random_shapes_and_tiles(device):
+    """Forty seeded random (M, N, K) with a random compiled tile each (every layout, split and depth
+    the library has for the width): K a multiple of 8 from 8 to 4096, so K steps per wavefront come
+    out odd or even, pairs of X steps straddle item and split ends, and the last step is masked;
+    each product against the oracle."""
+    rng = torch.Generator().manual_seed(2026)
+    checked = 0
+    for case in range(40):
+        M = int(torch.randint(1, 129, (1,), generator=rng))
+        N = int(torch.randint(16, 3001, (1,), generator=rng))
+        K = 8 * int(torch.randint(1, 513, (1,), generator=rng))
+        cands = tiles.candidates(M, N, K, lambda c: fast_gemm.tile_supported(M, K, c))
+        if not cands:
+            continue
+        cfg = cands[int(torch.randint(0, len(cands), (1,), generator=rng))]
+        x, w = _inputs(M, N, K, 100 + case)
+        print(f"case {case}: M={M} N={N} K={K} {cfg}", flush=True)
+        check(_run(x, w, cfg, device), x, w)
+        checked += 1
+    assert checked >= 30
+
+
 def test_split_k_is_deterministic_and_consistent(device):
     M, N, K = 56, 2048, 8192
     x, w = _inputs(M, N, K, 6)
