@@ -436,6 +436,12 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_shortlist_kernel(ShortArg
   }
   __syncthreads();
   int total = counters[1];
+  // The spread reads the first kSpreadSample columns (one 128-byte line) of the M targets' table
+  // rows; the candidates include the targets, so each candidate's line is requested now and is in
+  // the cache by the time the spread's reads go out. The value read is not used.
+  uint16_t warm = 0;
+  if (total <= kRankCap && t < total)
+    warm = a.table[table_row(0xFFFF - static_cast<int>(cand[t] & 0xFFFFu), a.V) * a.A];
   if (total > kCandidateCap) {
     // Many elements tie at the threshold (flat logits): bisect the full 32-bit sort key instead,
     // which leaves exactly M elements at or above it. Rare, so the passes re-read the row rather
@@ -527,6 +533,7 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_shortlist_kernel(ShortArg
     remaining = a.A - wave_sum(floors);
   }
   spread_post<DT>(spread_raw, a.A, M, kSpreadSample, lo_s, hi_s);
+  asm volatile("" ::"v"(warm));  // older than the spread's reads, so back before them
   __syncthreads();  // rem_s, the spread's minima and maxima
   // Remainder ranks: thread 8 m + g compares target m's remainder with targets [16 g, 16 g + 16);
   // the eight partial counts of m sit in one lane octet and add up there.
@@ -732,6 +739,7 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_fit_kernel(FitArgs a) {
   __shared__ float scale_s;
   __shared__ float best_v[kMaxTargets / 64];
   __shared__ int best_i[kMaxTargets / 64];
+  __shared__ int64_t token_s[kMaxTargets];
   const int t = threadIdx.x, lane = t & 63;
   const int64_t p = blockIdx.x;
   const int M = a.M, A = a.A;
@@ -747,6 +755,19 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_fit_kernel(FitArgs a) {
     corr[t] = 0.f;
     load_fx[t] = 0ull;
     if (t == 0) scale_s = kNegLog2e / temperature;
+  }
+
+  // What the end reads from memory is requested now, so its round trips overlap the sweeps: the
+  // target's offset and, when the problem's one item is resolved, its token and the item.
+  const bool resolve = a.table != nullptr;
+  float offset_t = 0.f;
+  int64_t token = 0, item = 0;
+  if (t < M) {
+    offset_t = a.offset[p * M + t];
+    if (resolve) {
+      token = a.tokens[p * M + t];
+      item = a.values[p];
+    }
   }
 
   // The condensed problem, decoded once (iterate.py:130-134): thread t holds items t + 1024 q and
@@ -766,6 +787,14 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_fit_kernel(FitArgs a) {
       target[q][j] = key & 0x7F;
     }
   }
+  // The target's table cost at the item (auxiliary.py:70-75), requested behind the keys. Every
+  // thread issues this one load (the others from an in-bounds stand-in address, the value unused),
+  // so the waits for the keys below leave it in flight on every path.
+  item = item < 0 ? 0 : (item > A - 1 ? A - 1 : item);
+  const uint16_t* cost_src =
+      resolve ? a.table + table_row(token, a.V) * A + item : reinterpret_cast<const uint16_t*>(a.counts + p * M);
+  uint32_t cost_bits = *cost_src;
+  if (resolve && t < M) token_s[t] = token;
   __syncthreads();
 
   for (int it = 0; it < a.iterations; ++it) {
@@ -813,20 +842,21 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_fit_kernel(FitArgs a) {
     temperature *= a.anneal;
   }
 
+  // The cost's load is used here on every path, so it stays in flight through the sweeps (no
+  // earlier wait, no conversion hoisted above them).
+  asm volatile("" : "+v"(cost_bits));
   float bias = 0.f;
   if (t < M) {
-    bias = a.offset[p * M + t] + corr[t];
+    bias = offset_t + corr[t];
     a.out[p * M + t] = bias;
   }
-  if (a.table == nullptr) return;
+  if (!resolve) return;
   // auxiliary.py:70-75 for this problem's one value: argmin_m C[m, a] + b[m], lowest m on ties.
   if (t < ((M + 63) & ~63)) {
-    int64_t item = a.values[p];
-    item = item < 0 ? 0 : (item > A - 1 ? A - 1 : item);
     float v = INFINITY;
     int idx = INT_MAX;
     if (t < M) {
-      v = from_bits16<DT>(a.table[table_row(a.tokens[p * M + t], a.V) * A + item]) + bias;
+      v = from_bits16<DT>(static_cast<uint16_t>(cost_bits)) + bias;
       idx = t;
     }
 #pragma unroll
@@ -852,7 +882,7 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_fit_kernel(FitArgs a) {
         v = best_v[w];
         idx = best_i[w];
       }
-    a.decoded[p] = a.tokens[p * M + idx];
+    a.decoded[p] = token_s[idx];
   }
 }
 
