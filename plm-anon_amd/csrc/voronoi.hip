@@ -88,6 +88,12 @@ template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
   return __builtin_bit_cast(float, dpp<CTRL>(__builtin_bit_cast(int, v)));
 }
+template <int CTRL>
+__device__ __forceinline__ unsigned long long dpp(unsigned long long v) {
+  const uint32_t lo = static_cast<uint32_t>(dpp<CTRL>(static_cast<int>(v)));
+  const uint32_t hi = static_cast<uint32_t>(dpp<CTRL>(static_cast<int>(v >> 32)));
+  return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
 __device__ __forceinline__ int lane_value(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
 __device__ __forceinline__ float lane_value(float v, int lane) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
@@ -723,16 +729,24 @@ struct FitArgs {
 };
 
 // The loads are sums of up to k * A <= 32768 weights. Each weight w (in [0, 1]) enters as the
-// integer round(w 2^31) into a 64-bit LDS counter per target (integer adds: the sum is exact, so
-// it is the same whatever order the workgroup's adds land in); the factor step reads it back as
-// sum 2^-31. Rounding moves a weight by at most 2^-32, and a load by at most its entry count
+// integer round(w 2^31) into one of its target's 64-bit LDS counters (integer adds: the sum is
+// exact, so it is the same whatever order the workgroup's adds land in); the factor step reads it
+// back as sum 2^-31. Rounding moves a weight by at most 2^-32, and a load by at most its entry count
 // times that, which the load floor (1e-2) dwarfs.
 constexpr float kFixedScale = 2147483648.0f;  // 2^31: w = 1 is 2^31, a u32
 constexpr double kFixedUnit = 1.0 / 2147483648.0;
+// The adds of one instruction that land on the same counter are carried out one after another, and
+// the popular targets sit in most items' slots: so each target has kLoadCopies counters, laid out
+// [target][copy], and lane l adds into copy l % kLoadCopies (at most four lanes of an instruction
+// share a counter). The counters are never cleared: the factor step keeps the previous sweep's
+// total and takes the difference, exact in unsigned 64-bit arithmetic whatever the running total.
+constexpr int kLoadCopies = 16;
+constexpr int kCopiesPerThread = kLoadCopies * kMaxTargets / kRowThreads;  // the factor step's share
+static_assert(kCopiesPerThread == 2, "the factor step reads one 16-byte pair per thread");
 
 template <int DT, int K, int IPT>
 __global__ __launch_bounds__(kRowThreads) void voronoi_fit_kernel(FitArgs a) {
-  __shared__ unsigned long long load_fx[kMaxTargets];
+  __shared__ __align__(16) unsigned long long load_fx[kMaxTargets * kLoadCopies];
   __shared__ float corr[kMaxTargets];
   __shared__ float share_s[kMaxTargets];
   __shared__ int live_s[kMaxTargets];
@@ -753,9 +767,11 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_fit_kernel(FitArgs a) {
     live_s[t] = c > 0;
     share_s[t] = logf(fmaxf(static_cast<float>(c), 1e-9f));
     corr[t] = 0.f;
-    load_fx[t] = 0ull;
     if (t == 0) scale_s = kNegLog2e / temperature;
   }
+#pragma unroll
+  for (int i = 0; i < kCopiesPerThread; ++i) load_fx[kCopiesPerThread * t + i] = 0ull;
+  const int copy = lane % kLoadCopies;
 
   // What the end reads from memory is requested now, so its round trips overlap the sweeps: the
   // target's offset and, when the problem's one item is resolved, its token and the item.
@@ -797,6 +813,7 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_fit_kernel(FitArgs a) {
   if (resolve && t < M) token_s[t] = token;
   __syncthreads();
 
+  unsigned long long load_before = 0;  // this lane octet's target's counter total after the last sweep
   for (int it = 0; it < a.iterations; ++it) {
     // Each item's softmax over its K slots (iterate.py:142-145), added into the loads
     // (iterate.py:146-149). exp(-cost / T - max) as exp2 of cost * (-log2(e) / T) less its maximum;
@@ -823,19 +840,29 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_fit_kernel(FitArgs a) {
 #pragma unroll
       for (int j = 0; j < K; ++j) {
         const uint32_t w = static_cast<uint32_t>(fmaf(x[j], r, 0.5f));
-        __hip_atomic_fetch_add(&load_fx[target[q][j]], static_cast<unsigned long long>(w), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_WORKGROUP);
+        __hip_atomic_fetch_add(&load_fx[target[q][j] * kLoadCopies + copy], static_cast<unsigned long long>(w),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       }
     }
     __syncthreads();
-    // The factor step (iterate.py:150-154), one thread per target; its counter restarts at zero.
-    if (t < M) {
-      const float load = static_cast<float>(static_cast<double>(load_fx[t]) * kFixedUnit);
-      load_fx[t] = 0ull;
-      float step = temperature * (logf(fmaxf(load, kLoadFloor)) - share_s[t]);
-      step = fminf(fmaxf(step, -bound), bound);
-      const float c = corr[t] + a.relax * step;
-      corr[t] = live_s[t] ? c : 0.f;
+    // The factor step (iterate.py:150-154). Target m's load: threads 8 m .. 8 m + 7 each add two of
+    // its counters, the eight partial sums are joined by DPP inside the lane octet, and the sweep's
+    // load is the total less the previous sweep's.
+    {
+      const int m = t >> 3;
+      unsigned long long total = load_fx[kCopiesPerThread * t] + load_fx[kCopiesPerThread * t + 1];
+      total += dpp<kDppXor1>(total);
+      total += dpp<kDppXor2>(total);
+      total += dpp<kDppHalfMirror>(total);
+      const unsigned long long fx = total - load_before;
+      load_before = total;
+      if ((t & 7) == 0 && m < M) {
+        const float load = static_cast<float>(static_cast<double>(fx) * kFixedUnit);
+        float step = temperature * (logf(fmaxf(load, kLoadFloor)) - share_s[m]);
+        step = fminf(fmaxf(step, -bound), bound);
+        const float c = corr[m] + a.relax * step;
+        corr[m] = live_s[m] ? c : 0.f;
+      }
       if (t == 0) scale_s = kNegLog2e / (temperature * a.anneal);
     }
     __syncthreads();
