@@ -295,6 +295,22 @@ constexpr int kRankCap = 256;
 // to this many (more only when many equal values sit at the threshold: then each scans its own).
 constexpr int kQualifyCap = 256;
 
+// Adds one to hist[bin] for every active lane of the wavefront, one LDS add per distinct bin (the
+// group's lowest lane adds the group's size). For bins that few values share: adds of one
+// instruction that land on the same counter are carried out one after another, and the per-thread
+// maxima of a row fall into a handful of high-byte bins.
+__device__ __forceinline__ void wave_bin_add(int* hist, uint32_t bin, bool active) {
+  const int lane = threadIdx.x & 63;
+  uint64_t pending = __ballot(active);
+  while (pending) {
+    const int leader = __builtin_ctzll(pending);
+    const uint32_t b = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(bin), leader));
+    const uint64_t same = __ballot(active && bin == b);
+    if (lane == leader) atomicAdd(&hist[b], __popcll(same));
+    pending &= ~same;
+  }
+}
+
 // Wavefront 0 over a 256-bin histogram: the largest bin b whose count of bins >= b reaches `need`.
 // out[0] = b, out[1] = need less the count of bins above b (>= 1).
 __device__ __forceinline__ void select_bin(const int* hist, int need, int* out) {
@@ -396,7 +412,7 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_shortlist_kernel(ShortArg
   // elements all do. Found as a radix selection over the 1024 maxima: a histogram of their high
   // bytes picks the high byte, a histogram of the low bytes of the maxima in that bin the low one.
   __syncthreads();  // the histograms and counters are zero
-  atomicAdd(&hist[0][kmax >> 8], 1);
+  wave_bin_add(hist[0], kmax >> 8, true);
   __syncthreads();
   if (wave == 0) select_bin(hist[0], M, &sel[0]);
   __syncthreads();
