@@ -170,6 +170,29 @@ def test_fit_matches_the_oracle(device, k, a, iterations, eps):
     assert err.max() < FIT_TOL
 
 
+def test_fit_with_one_dominant_target(device):
+    """One token's logit raised so that its quota is about half of the items: its loads are the
+    largest the fit sums, and most lanes of an add instruction carry a weight for it."""
+    a, k, m = 4096, 8, 128
+    table, logits = _case(33, 5, 50257, a)
+    lg = _np(logits)
+    lg[:, 777] = lg.max(axis=1) + 4.0
+    tab_np = _np(table)
+    tokens, counts, _, _ = vo.shortlist(lg, a, m)
+    assert (counts.max(axis=1) > a // 3).all()
+    unit = vo.spread(tab_np, tokens, "bf16")
+    prior = vo.prior(counts, unit, a)
+    key = vo.condense(tab_np, tokens, prior, k)
+    eng = Voronoi.from_table(table.to(device))
+    args = [torch.from_numpy(x).to(device) for x in (key, counts, prior, unit)]
+    bias = eng.fit(*args, 12, 0.15)
+    assert torch.equal(bias, eng.fit(*args, 12, 0.15))
+    ref = vo.fit(key, counts, prior, unit, 12, 0.15)
+    err = np.abs(_np(bias) - ref) / unit[:, None]
+    print(f"fit with one dominant target: max error {err.max():.3e} units", flush=True)
+    assert err.max() < FIT_TOL
+
+
 def test_argmin_for_a_given_bias(device):
     table, _, tab_np, tokens, counts, unit, prior = _stage_inputs(30, n=4, a=2048)
     bias = vo.fit(vo.condense(tab_np, tokens, prior, 8), counts, prior, unit, 12, 0.15)
