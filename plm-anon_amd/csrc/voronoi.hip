@@ -676,6 +676,25 @@ __device__ __forceinline__ void merge_lists(int32_t (&a)[K], const int32_t (&b)[
       }
 }
 
+// Bitonic sorting network over K registers, ascending.
+template <int K>
+__device__ __forceinline__ void sort_ascending(int32_t (&v)[K]) {
+#pragma unroll
+  for (int size = 2; size <= K; size <<= 1)
+#pragma unroll
+    for (int stride = size / 2; stride >= 1; stride >>= 1)
+#pragma unroll
+      for (int i = 0; i < K; ++i) {
+        const int j = i ^ stride;
+        if (j > i) {
+          const int32_t lo = min(v[i], v[j]), hi = max(v[i], v[j]);
+          const bool up = (i & size) == 0;
+          v[i] = up ? lo : hi;
+          v[j] = up ? hi : lo;
+        }
+      }
+}
+
 template <int DT, int K>
 __global__ __launch_bounds__(kItemThreads) void voronoi_condense_kernel(CondenseArgs a) {
   __shared__ int32_t part[2][K][kCondenseItems];
@@ -699,9 +718,27 @@ __global__ __launch_bounds__(kItemThreads) void voronoi_condense_kernel(Condense
   int32_t best[K];
 #pragma unroll
   for (int s = 0; s < K; ++s) best[s] = INT_MAX;
+  // The lane's keys K at a time: each group sorted by a network and merged into the list (about
+  // 40 % fewer min/max operations than inserting the keys one by one from K = 4 on). Keys are
+  // unique (the target sits in their low bits), so either way gives the same K smallest.
+  if constexpr (K >= 4) {
+    static_assert(kTargetsPerWave % K == 0, "groups of K keys");
 #pragma unroll
-  for (int b = 0; b < kTargetsPerWave; ++b)
-    if (m0 + b < m1) insert_key<K>(best, pack_cost(from_bits16<DT>(raw[b]) + lane_value(off, b), m0 + b));
+    for (int c = 0; c < kTargetsPerWave; c += K) {
+      int32_t group[K];
+#pragma unroll
+      for (int i = 0; i < K; ++i) {
+        const int b = c + i;
+        group[i] = m0 + b < m1 ? pack_cost(from_bits16<DT>(raw[b]) + lane_value(off, b), m0 + b) : INT_MAX;
+      }
+      sort_ascending<K>(group);
+      merge_lists<K>(best, group);
+    }
+  } else {
+#pragma unroll
+    for (int b = 0; b < kTargetsPerWave; ++b)
+      if (m0 + b < m1) insert_key<K>(best, pack_cost(from_bits16<DT>(raw[b]) + lane_value(off, b), m0 + b));
+  }
   // Waves 1 and 3 hand their lists to 0 and 2, then 2 to 0 (through the slot it read itself).
   if (wave & 1) {
 #pragma unroll
