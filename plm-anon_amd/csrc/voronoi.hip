@@ -830,12 +830,12 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_fit_kernel(FitArgs a) {
   // target's offset and, when the problem's one item is resolved, its token and the item.
   const bool resolve = a.table != nullptr;
   float offset_t = 0.f;
-  int64_t token = 0, item = 0;
+  int64_t token = 0, decode_item = 0;
   if (t < M) {
     offset_t = a.offset[p * M + t];
     if (resolve) {
       token = a.tokens[p * M + t];
-      item = a.values[p];
+      decode_item = a.values[p];
     }
   }
 
@@ -859,9 +859,9 @@ __global__ __launch_bounds__(kRowThreads) void voronoi_fit_kernel(FitArgs a) {
   // The target's table cost at the item (auxiliary.py:70-75), requested behind the keys. Every
   // thread issues this one load (the others from an in-bounds stand-in address, the value unused),
   // so the waits for the keys below leave it in flight on every path.
-  item = item < 0 ? 0 : (item > A - 1 ? A - 1 : item);
-  const uint16_t* cost_src =
-      resolve ? a.table + table_row(token, a.V) * A + item : reinterpret_cast<const uint16_t*>(a.counts + p * M);
+  decode_item = decode_item < 0 ? 0 : (decode_item > A - 1 ? A - 1 : decode_item);
+  const uint16_t* cost_src = resolve ? a.table + table_row(token, a.V) * A + decode_item
+                                     : reinterpret_cast<const uint16_t*>(a.counts + p * M);
   uint32_t cost_bits = *cost_src;
   if (resolve && t < M) token_s[t] = token;
   __syncthreads();
