@@ -54,7 +54,22 @@ namespace plm {
 constexpr int kPackedWaves = 4;            // wavefronts per workgroup of the row-split layout (KW = 1)
 constexpr int kFragBytes = 1024;           // one packed fragment: 64 lanes x 16 bytes
 constexpr uint32_t kNoLoad = 0x80000000u;  // scalar offset that puts a load out of range (zeros)
-constexpr int kXTileBytes = 16 * 80;       // LDS transpose tile of one X fragment (rows padded to 80 B)
+constexpr int kXTileBytes = 16 * 80;       // LDS transpose tile of one X fragment (16 rows of up to 80 B)
+
+// Where a lane writes and reads its 16 bytes of an X transpose tile. A fragment row holds 32 K
+// values (64 B, four 16-byte chunks); lane l writes chunk l % 4 of row l / 4 (its X load) and reads
+// chunk l / 16 of row l % 16 (the MFMA operand). Swizzled: rows 64 B apart, chunk c of row r at slot
+// c ^ ((r >> 2) & 3), so the 16 lanes of an LDS cycle hit 16 different bank groups in both
+// directions. Padded: rows 80 B apart, reads conflict-free but writes two-way (kept where the
+// swizzled offsets would cost registers the kernel does not have).
+template <bool kSwizzle>
+__device__ __forceinline__ int x_tile_write_offset(int lane) {
+  return kSwizzle ? (lane >> 2) * 64 + (((lane & 3) ^ ((lane >> 4) & 3)) * 16) : (lane >> 2) * 80 + (lane & 3) * 16;
+}
+template <bool kSwizzle>
+__device__ __forceinline__ int x_tile_read_offset(int lane) {
+  return kSwizzle ? (lane & 15) * 64 + (((lane >> 4) ^ ((lane >> 2) & 3)) * 16) : (lane & 15) * 80 + (lane >> 4) * 16;
+}
 
 // Counter-area layout of a packed launch (int indices).
 constexpr int kPkErrorSlot = 2;      // 1 once a bounded wait gave up
@@ -1025,8 +1040,9 @@ __global__ __launch_bounds__(64 * packed_waves<KW>(), (packed_waves_per_simd<MT,
                       : (KW == 4 ? static_cast<size_t>(4) * NF * MT * kFragBytes : 0) +
                             static_cast<size_t>(wave) * kXSets * MT * kXTileBytes);
   PkLdsVoid* sink = (PkLdsVoid*)(reinterpret_cast<char*>(packed_lds) + packed_lds_body<MT, NF, KW>());
-  const int xt_write = (lane >> 2) * 80 + (lane & 3) * 16;
-  const int xt_read = (lane & 15) * 80 + (lane >> 4) * 16;
+  constexpr bool kSwizzleX = !(KW == 8 && MT * NF >= 14);  // the eight-wavefront tiles at 14+ fragments spill
+  const int xt_write = x_tile_write_offset<kSwizzleX>(lane);
+  const int xt_read = x_tile_read_offset<kSwizzleX>(lane);
   const int64_t epoch = a.sync ? sgpr64(collect(reinterpret_cast<const int64_t*>(a.counters + kPkEpochSlot))) : 0;
 
   u32x4 wb[D][NF], xb[D][XN];

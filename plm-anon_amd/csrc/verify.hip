@@ -615,8 +615,8 @@ __global__ __launch_bounds__(64 * kPackedWaves, (packed_waves_per_simd<MT, NF, D
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   char* xt = reinterpret_cast<char*>(packed_lds);
-  const int xt_write = (lane >> 2) * 80 + (lane & 3) * 16;
-  const int xt_read = (lane & 15) * 80 + (lane >> 4) * 16;
+  const int xt_write = x_tile_write_offset<true>(lane);
+  const int xt_read = x_tile_read_offset<true>(lane);
 
   PLinear L{};
   L.x = a.x;
